@@ -1,0 +1,361 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused DiT attention path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+One step = one ``ltx_attn_fwd`` call (QK-RMSNorm statistic, K prologue, attention) on the
+workload the headline metric is quoted on: stage-2 video self-attention at 1280x768x97
+(latent 13x24x40 -> 12480 tokens), H=32, D=128, pre-norm bf16 Q/K/V [1, 12480, 4096] ~ N(0,1),
+q/k norm weights ~ N(1, 0.02), 3-D RoPE tables from the reference's position recipe. FLOPs use
+the reference's convention 4*Sq*Skv*H*D (Sources/ltx/BenchGEMM.swift:154-159).
+
+Prints ONE JSON line. ``roofline`` is for the dominant kernel (the attention kernel itself),
+timed with HIP events recorded by the library around that kernel on the call's stream.
+``cpu_baseline`` times the C restatement of the reference's explicit fp32 path on a bounded
+sample of the same workload, on this host's cores. ``secondary`` holds the other two figures
+the metric names: 3120-token self-attention TFLOP/s and ms per DiT-block attention set.
+"""
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "ltx-2.5-swift_amd"), os.path.join(ROOT, "oracle")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "attention TFLOP/s + % bf16 MFMA peak at 3120/12480 tokens; ms per DiT-block attn"
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_attn_c4.json")
+
+
+class HipEvents:
+    """hipEvent_t handles through the HIP runtime's C API (the library records them)."""
+
+    def __init__(self):
+        self.rt = ctypes.CDLL("libamdhip64.so")
+        self.rt.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.rt.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float),
+                                                ctypes.c_void_p, ctypes.c_void_p]
+        self.rt.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.rt.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self):
+        ev = ctypes.c_void_p()
+        if self.rt.hipEventCreate(ctypes.byref(ev)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        return ev
+
+    def elapsed_ms(self, a, b):
+        self.rt.hipEventSynchronize(b)
+        ms = ctypes.c_float()
+        if self.rt.hipEventElapsedTime(ctypes.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def destroy(self, ev):
+        self.rt.hipEventDestroy(ev)
+
+
+def _randn(shape, seed, device, mean=0.0, std=1.0):
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    t = torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std + mean
+    return t.to(torch.bfloat16)
+
+
+def _dev_bits(bits, device):
+    import numpy as np
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(device).view(
+        torch.bfloat16)
+
+
+def _host_bits(t):
+    import numpy as np
+    import torch
+
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def c4_inputs(device):
+    import ltx_attn as L
+
+    H, D, T = 32, 128, 12480
+    q = _randn((1, T, H * D), 0x5EED, device)
+    k = _randn((1, T, H * D), 0x5EED + 1, device)
+    v = _randn((1, T, H * D), 0x5EED + 2, device)
+    wq = _randn((H * D,), 0x5EED + 3, device, 1.0, 0.02)
+    wk = _randn((H * D,), 0x5EED + 4, device, 1.0, 0.02)
+    cos, sin = L.rope_tables(L.rope_video_positions(13, 24, 40), H * D, [20, 2048, 2048], H)
+    return dict(q=q, k=k, v=v, wq=wq, wk=wk, cos=cos, sin=sin, H=H, D=D, T=T,
+                rot=L.Rotary(_dev_bits(cos, device), _dev_bits(sin, device)))
+
+
+def time_steps(call, steps, warmup, hip, events_per_step=True):
+    """Warmup, then exactly `steps` timed calls bracketed by synchronisation.
+    Returns (wall seconds, list of attention-kernel ms from the library's event hook)."""
+    import torch
+
+    for _ in range(warmup):
+        call(None)
+    torch.cuda.synchronize()
+    evs = [(hip.create(), hip.create()) for _ in range(steps)] if events_per_step else []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        call(evs[i] if evs else None)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kms = [hip.elapsed_ms(a, b) for a, b in evs]
+    for a, b in evs:
+        hip.destroy(a)
+        hip.destroy(b)
+    return wall, kms
+
+
+def bench_c4(device, steps, warmup, hip):
+    import torch
+
+    import ltx_attn as L
+
+    x = c4_inputs(device)
+    H, D, T = x["H"], x["D"], x["T"]
+    out = torch.empty_like(x["q"])
+    ws = torch.empty(512 << 20, dtype=torch.uint8, device=device)
+
+    def call(ev):
+        L.attention_fwd(x["q"], x["k"], x["v"], heads=H, q_norm_w=x["wq"], k_norm_w=x["wk"],
+                        rotary=x["rot"], out=out, workspace=ws,
+                        events=None if ev is None else (ev[0], ev[1]))
+
+    wall, kms = time_steps(call, steps, warmup, hip)
+    flops = 4.0 * T * T * H * D
+    return x, {
+        "flops": flops, "wall_s": wall, "ms_per_step": wall / steps * 1e3,
+        "tflops": flops * steps / wall / 1e12,
+        "kernel_ms": sum(kms) / len(kms), "kernel_ms_min": min(kms), "kernel_ms_max": max(kms),
+        "kernel_tflops": flops / (sum(kms) / len(kms) * 1e-3) / 1e12,
+        "bytes": 4.0 * T * H * D * 2,
+    }
+
+
+def bench_c1(device, steps, warmup, hip):
+    import torch
+
+    import ltx_attn as L
+
+    H, D, T = 32, 128, 3120
+    q = _randn((1, T, H * D), 0x5EED + 10, device)
+    k = _randn((1, T, H * D), 0x5EED + 11, device)
+    v = _randn((1, T, H * D), 0x5EED + 12, device)
+    out = torch.empty_like(q)
+
+    def call(ev):
+        L.attention_fwd(q, k, v, heads=H, out=out,
+                        events=None if ev is None else (ev[0], ev[1]))
+
+    wall, kms = time_steps(call, steps, warmup, hip)
+    flops = 4.0 * T * T * H * D
+    km = sum(kms) / len(kms)
+    return {"tflops": flops * steps / wall / 1e12, "ms_per_call": wall / steps * 1e3,
+            "kernel_ms": km, "kernel_tflops": flops / (km * 1e-3) / 1e12,
+            "pct_peak": 100.0 * flops / (km * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+
+
+def bench_c5(device, steps, warmup, hip):
+    """The six attentions of one DiT block at 1280x768x121, B=2 (CFG), in block order
+    (Sources/LTXModules/DiTBlock.swift:343-438): attn1, audio_attn1, attn2, audio_attn2,
+    audio_to_video, video_to_audio."""
+    import torch
+
+    import ltx_attn as L
+
+    Tv, Ta, Tt, B = 15360, 152, 1024, 2
+    tabs = L.rotaries(121, 768, 1280, audio_tokens=Ta)
+    rot = {k: L.Rotary(_dev_bits(c, device), _dev_bits(s, device)) for k, (c, s) in tabs.items()}
+    s = {}
+    for name, T, inner, seed in (("v", Tv, 4096, 50), ("a", Ta, 2048, 60),
+                                 ("t4096", Tt, 4096, 70), ("t2048", Tt, 2048, 80),
+                                 ("v2048", Tv, 2048, 90)):
+        s[name] = _randn((B, T, inner), 0x5EED + seed, device)
+    w4 = _randn((4096,), 0x5EED + 100, device, 1.0, 0.02)
+    w2 = _randn((2048,), 0x5EED + 101, device, 1.0, 0.02)
+    ws = torch.empty(512 << 20, dtype=torch.uint8, device=device)
+    valid = [94, 94]
+    calls = [
+        ("attn1", s["v"], s["v"], w4, rot["videoSelf"], None, None),
+        ("audio_attn1", s["a"], s["a"], w2, rot["audioSelf"], None, None),
+        ("attn2", s["v"], s["t4096"], w4, None, None, valid),
+        ("audio_attn2", s["a"], s["t2048"], w2, None, None, valid),
+        ("audio_to_video_attn", s["v2048"], s["a"], w2, rot["videoCross"], rot["audioCross"],
+         None),
+        ("video_to_audio_attn", s["a"], s["v2048"], w2, rot["audioCross"], rot["videoCross"],
+         None),
+    ]
+    outs = [torch.empty_like(c[1]) for c in calls]
+    flops = 0.0
+    for _, q, kv, _, _, _, vl in calls:
+        Lq, Lk, inner = q.shape[1], kv.shape[1], q.shape[2]
+        nk = Lk if vl is None else vl[0]
+        flops += 4.0 * q.shape[0] * Lq * nk * inner
+
+    def call(ev):
+        for i, (_, q, kv, w, r, kr, vl) in enumerate(calls):
+            L.attention_fwd(q, kv, kv, heads=32, q_norm_w=w, k_norm_w=w, rotary=r,
+                            key_rotary=kr, k_valid_len=vl, out=outs[i], workspace=ws)
+
+    wall, _ = time_steps(call, steps, warmup, hip, events_per_step=False)
+    # per-attention kernel time (one call each, events around the attention kernel)
+    per = {}
+    for i, (name, q, kv, w, r, kr, vl) in enumerate(calls):
+        a, b = hip.create(), hip.create()
+        L.attention_fwd(q, kv, kv, heads=32, q_norm_w=w, k_norm_w=w, rotary=r, key_rotary=kr,
+                        k_valid_len=vl, out=outs[i], workspace=ws, events=(a, b))
+        torch.cuda.synchronize()
+        per[name] = round(hip.elapsed_ms(a, b), 4)
+        hip.destroy(a)
+        hip.destroy(b)
+    ms = wall / steps * 1e3
+    return {"ms_per_block": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+            "kernel_ms": per}
+
+
+def cpu_baseline(x, budget_s):
+    """The C restatement of the reference's explicit path (fp32 logits, softmax, P.V, with
+    its bf16 rounding points), multithreaded, on a bounded sample of the c4 workload:
+    all 12480 keys, a contiguous block of queries, some heads."""
+    import oracle as O
+
+    threads = min(16, os.cpu_count() or 1)
+    H, D, T = x["H"], x["D"], x["T"]
+    qb, kb, vb = _host_bits(x["q"]), _host_bits(x["k"]), _host_bits(x["v"])
+    wq, wk = _host_bits(x["wq"]), _host_bits(x["wk"])
+    kw = dict(q_norm_w=wq, k_norm_w=wk, q_cos=x["cos"], q_sin=x["sin"], mode="reference",
+              threads=threads)
+    # calibrate on 64 queries of one head, then size the sample to the budget
+    t0 = time.perf_counter()
+    O.c_attention(qb, kb, vb, H, heads_range=(0, 1), q_range=(0, 64), **kw)
+    t_cal = time.perf_counter() - t0
+    per_row = t_cal / 64.0
+    rows_total = max(64, int(budget_s / max(per_row, 1e-9)))
+    nh = max(1, min(H, rows_total // T))
+    nq = T if rows_total >= T else max(64, rows_total)
+    t0 = time.perf_counter()
+    O.c_attention(qb, kb, vb, H, heads_range=(0, nh), q_range=(0, nq), **kw)
+    dt = time.perf_counter() - t0
+    flops = 4.0 * nq * T * nh * D
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": (f"{nh} head(s) x {nq} queries x {T} keys of the 12480-token workload "
+                       f"(norm + 3-D RoPE + explicit fp32 SDPA), {dt:.1f} s on {cpu}; "
+                       "substitute for the reference's MLX CPU path (mlx not installed)")}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-budget", type=float, default=12.0,
+                    help="seconds of CPU work for the cpu_baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print("bench.py measures one MI355X: the attention path runs on a single GPU in this "
+              "build (multi-GPU head/query sharding is described in DESIGN.md, not built); "
+              f"--gpus {args.gpus} is not supported.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import ltx_attn as L
+
+    L.load_library()
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    hip = HipEvents()
+
+    x, c4 = bench_c4(device, args.steps, args.warmup, hip)
+    print(f"# c4: {c4['ms_per_step']:.3f} ms/step, attention kernel {c4['kernel_ms']:.3f} ms "
+          f"({c4['kernel_tflops']:.1f} TFLOP/s)", file=sys.stderr, flush=True)
+    secondary = {}
+    if not args.no_secondary:
+        c1 = bench_c1(device, 10, 3, hip)
+        print(f"# c1: {c1['kernel_ms']:.3f} ms kernel, {c1['kernel_tflops']:.1f} TFLOP/s",
+              file=sys.stderr, flush=True)
+        c5 = bench_c5(device, 5, 2, hip)
+        print(f"# c5: {c5['ms_per_block']:.3f} ms per block attention set", file=sys.stderr,
+              flush=True)
+        secondary = {
+            "video_self_3120_tflops": round(c1["kernel_tflops"], 2),
+            "video_self_3120_pct_peak": round(c1["pct_peak"], 2),
+            "video_self_3120_ms": round(c1["kernel_ms"], 4),
+            "dit_block_attn_ms": round(c5["ms_per_block"], 4),
+            "dit_block_attn_tflops": round(c5["tflops"], 2),
+            "dit_block_attn_kernel_ms": c5["kernel_ms"],
+            "video_self_12480_kernel_ms_min_max": [round(c4["kernel_ms_min"], 4),
+                                                   round(c4["kernel_ms_max"], 4)],
+        }
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as fh:
+            traffic = json.load(fh).get("hbm_bytes_per_launch")
+    achieved = c4["kernel_tflops"]
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": traffic, "kernel": "fmha_fwd_kernel<128,false>",
+                "kernel_avg_ms": round(c4["kernel_ms"], 4),
+                "flops_per_launch": c4["flops"]}
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(x, args.cpu_budget)
+
+    line = {
+        "metric": METRIC,
+        "value": round(c4["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c4["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "stage-2 video self-attention 1280x768x97: 12480 tokens, "
+                               "H=32, D=128, B=1, fused QK-RMSNorm (eps 1e-6) + 3-D RoPE",
+                   "B": 1, "H": 32, "Lq": 12480, "Lk": 12480, "D": 128,
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+        "provenance": L.provenance(),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

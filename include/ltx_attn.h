@@ -1,0 +1,176 @@
+/*
+ * ltx_attn.h -- C ABI of the MI355X (gfx950) fused DiT attention library.
+ *
+ * One shared library, libltx_attn.so, replaces the arithmetic of the LTX 2.5 DiT attention
+ * hot path: QK-RMSNorm over the inner dim, the head split, split-half RoPE and scaled
+ * dot-product attention. In the reference that is
+ *
+ *     Sources/LTXModules/DiTAttention.swift:358-381   (inside DiTAttention.callAsFunction,
+ *                                                     declared at :315-318)
+ *       q = rmsNorm(q, q_norm.weight); k = rmsNorm(k, k_norm.weight)   :360-361 (-> :202-204)
+ *       qh = split(q); kh = split(k)                                   :362 (-> :346-349)
+ *       qh = applySplitRoPE(qh, rotary); kh = applySplitRoPE(kh, keyRotary ?? rotary)
+ *                                                                      :364-367 (-> :226-234)
+ *       out = MLXFast.scaledDotProductAttention(qh, kh, vh, scale, mask: .none)  :374-376
+ *
+ * and the rotary-table builders of Sources/LTXModules/DiTForward.swift:455-738.
+ *
+ * Everything is plain C: pointers, sizes and status codes. Device buffers are HIP device
+ * pointers; `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *
+ * Contract of ltx_attn_fwd (all of it checked on the host before anything is launched):
+ *   - no allocation: scratch memory is the caller's `workspace`, sized by
+ *     ltx_attn_workspace_bytes() for the same arguments;
+ *   - no hidden global mutable state; reentrant across streams and threads (the detail
+ *     string of the last failure is thread-local, like dlerror);
+ *   - asynchronous on `stream`; inputs must stay valid until the stream reaches the call.
+ */
+#ifndef LTX_ATTN_H
+#define LTX_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LTX_ATTN_ABI_VERSION 1
+
+/* Status codes. The reference throws `DiTAttention.Failure` for structural errors
+ * (DiTAttention.swift:107-121); a Swift wrapper maps these onto thrown errors. */
+typedef enum {
+    LTX_ATTN_OK = 0,
+    LTX_ATTN_EINVAL = 1,       /* bad shape, stride, alignment, pointer or valid length   */
+    LTX_ATTN_EUNSUPPORTED = 2, /* head dim other than 64/128, or a batch above the limit  */
+    LTX_ATTN_EHIP = 3,         /* a HIP runtime call or kernel launch failed               */
+    LTX_ATTN_EWORKSPACE = 4    /* workspace missing or smaller than ltx_attn_workspace_bytes */
+} ltx_attn_status;
+
+/* How K gets its norm + RoPE (only matters when a K norm weight or K tables are given). */
+typedef enum {
+    LTX_ATTN_KPREP_AUTO = 0,     /* pick by cost: prologue when K is re-read by >= 2 query blocks */
+    LTX_ATTN_KPREP_FUSED = 1,    /* normalise + rotate K inside the attention kernel's LDS staging */
+    LTX_ATTN_KPREP_PROLOGUE = 2  /* one pass writes normed+rotated K (bf16) into the workspace     */
+} ltx_attn_kprep;
+
+/* Largest batch for which per-row key-padding lengths may be given. */
+#define LTX_ATTN_MAX_BATCH 64
+
+/*
+ * One attention call. Element strides (not bytes). Token l of batch row b, head h, channel d
+ * of q lives at q + b*q_bs + l*q_rs + h*q_hs + d. The reference's merged projection layout
+ * [B, L, H*D] is q_bs = L*H*D, q_rs = H*D, q_hs = D; its split layout [B, H, L, D]
+ * (DiTAttention.swift:346-349) is q_bs = H*L*D, q_hs = L*D, q_rs = D.
+ * `out` uses the same scheme; the merged layout [B, Lq, H*D] is what `to_out` consumes
+ * after the gate (DiTAttention.swift:402-404).
+ */
+typedef struct ltx_attn_args {
+    int32_t B, H, Lq, Lk, D;      /* D in {64, 128}; H*D = inner (4096 video, 2048 audio/cross) */
+
+    const void *q, *k, *v;        /* bf16 device pointers, 16-byte aligned                  */
+    int64_t q_bs, q_rs, q_hs;     /* strides: multiples of 8 elements; q_hs >= D              */
+    int64_t k_bs, k_rs, k_hs;
+    int64_t v_bs, v_rs, v_hs;
+
+    /* QK-RMSNorm (DiTAttention.swift:190-204, :360-361): bf16 [H*D] weights, statistic over
+     * all H*D channels of a token (not per head; channel (h, d) is inner index h*D + d).
+     * NULL = that input is already normalised. */
+    const void *q_norm_w, *k_norm_w;
+    float norm_eps;               /* 1e-6 in the reference (DiTAttention.swift:66)           */
+
+    /* Split RoPE (DiTAttention.swift:206-234): bf16 cos/sin tables [H, L, D/2] contiguous,
+     * broadcast over the batch (the reference's [1, H, L, D/2]). q tables NULL = no RoPE.
+     * k tables NULL with q tables given = K uses q's tables (`keyRotary ?? rotary`, :366),
+     * which needs Lq == Lk. k tables without q tables is EINVAL. */
+    const void *q_cos, *q_sin;
+    const void *k_cos, *k_sin;
+
+    /* Key padding: HOST pointer to B int32 counts; batch row b attends to keys [0, n_b).
+     * NULL = every key valid. 1 <= n_b <= Lk (0 is EINVAL, as TextConditioningLayout.swift:65
+     * rejects an empty mask). Fully padded tiles are skipped, not computed. */
+    const int32_t *k_valid_len;
+
+    float scale;                  /* softmax scale; 1/sqrt(D) in the reference (:372)        */
+
+    void *out;                    /* bf16 device pointer, 16-byte aligned                   */
+    int64_t o_bs, o_rs, o_hs;
+
+    void *workspace;              /* device scratch, 256-byte aligned, or NULL if 0 bytes needed */
+    size_t workspace_bytes;
+
+    int32_t kprep;                /* ltx_attn_kprep                                            */
+    int32_t num_splits;           /* 0 = auto; >= 1 forces that many key splits (split-KV)    */
+
+    /* Optional timing hook: hipEvent_t handles (as void*) recorded on `stream` immediately
+     * before and after the attention kernel itself (not the norm/RoPE prologue or the
+     * split-KV combine). NULL = not recorded. */
+    void *ev_attn_start, *ev_attn_stop;
+} ltx_attn_args;
+
+/* Fill `a` with defaults: zero sizes and pointers, norm_eps = 1e-6, kprep AUTO, splits auto. */
+void ltx_attn_args_init(ltx_attn_args *a);
+
+/* Bytes of workspace ltx_attn_fwd needs for these arguments (0 if none). Pure host function;
+ * returns 0 and sets the thread's error detail if the arguments are invalid. */
+size_t ltx_attn_workspace_bytes(const ltx_attn_args *a);
+
+/* Check the arguments without launching anything (the first step of ltx_attn_fwd). */
+ltx_attn_status ltx_attn_validate(const ltx_attn_args *a);
+
+/* Run norm -> split -> RoPE -> SDPA asynchronously on `stream` (a hipStream_t or NULL).
+ * Replaces DiTAttention.swift:360-381 (MLXFast.scaledDotProductAttention at :374-376). */
+ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream);
+
+/* Static text for a status code. */
+const char *ltx_attn_status_string(ltx_attn_status s);
+
+/* Detail of the calling thread's last failure ("" if none). */
+const char *ltx_attn_last_error(void);
+
+/* Provenance string recorded beside a render, like `attentionPath` in the reference's
+ * .provenance.json (Sources/LTXPipeline/Renderer.swift:477-490). */
+const char *ltx_attn_provenance(void);
+
+/* ABI version of the loaded library (LTX_ATTN_ABI_VERSION it was built with). */
+int32_t ltx_attn_abi_version(void);
+
+/* sizeof(ltx_attn_args) as compiled into the library, so an FFI mirror of the struct
+ * (Swift, ctypes, ...) can verify its layout at load time. */
+size_t ltx_attn_args_size(void);
+
+/* ----------------------------------------------------------------------------------------
+ * RoPE table construction (host side, no GPU): the reference builds these once per forward
+ * and hands them to every block (DiTForward.swift:680-738).
+ * -------------------------------------------------------------------------------------- */
+
+/* frequencyGrid (DiTForward.swift:455-466): n = inner/(2*nPos) values,
+ * f_i = theta^(i/(n-1)) * pi/2 in double, endpoint exponent exactly 1, stored as float.
+ * Returns the count written to `out` (capacity `cap`), or -1 on bad arguments. */
+int32_t ltx_rope_frequency_grid(double theta, int32_t n_pos, int32_t inner, float *out,
+                                int32_t cap);
+
+/* videoPositions (DiTForward.swift:486-520): patch bounds [3][tokens][2] (float, seconds for
+ * time with the causal correction, pixels for space); tokens = frames*height*width in
+ * (t, y, x) order. Returns tokens, or -1. */
+int32_t ltx_rope_video_positions(int32_t latent_frames, int32_t latent_height,
+                                 int32_t latent_width, int32_t temporal_scale,
+                                 int32_t spatial_scale, double frame_rate, float *out,
+                                 int64_t cap);
+
+/* audioPositions (DiTForward.swift:606-619): bounds [1][tokens][2] in seconds. */
+int32_t ltx_rope_audio_positions(int32_t tokens, int32_t hop_length, int32_t sample_rate,
+                                 int32_t downsample, float *out, int64_t cap);
+
+/* rotary(positions:innerDim:maxPos:heads:theta:dtype:) (DiTForward.swift:641-678):
+ * positions [n_pos][tokens][2] -> bf16 bit patterns cos/sin [heads][tokens][inner/2/heads].
+ * Returns 0 or -1. */
+int32_t ltx_rope_tables(const float *positions, int32_t n_pos, int32_t tokens, int32_t inner,
+                        const int32_t *max_pos, int32_t heads, double theta, uint16_t *cos_out,
+                        uint16_t *sin_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LTX_ATTN_H */

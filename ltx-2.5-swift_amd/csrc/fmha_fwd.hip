@@ -1,0 +1,669 @@
+// Fused DiT attention for MI355X (gfx950): bf16 MFMA flash attention with the QK-RMSNorm and
+// split RoPE of the LTX 2.5 DiT (Sources/LTXModules/DiTAttention.swift:358-381) fused into
+// the Q/K loads.
+//
+// Work decomposition
+//   One workgroup = 4 waves; each wave owns 64 queries of one (batch, head) and walks the key
+//   sequence in tiles of 64 keys. K and V tiles are staged through LDS (double buffered, with
+//   the next tile prefetched into registers while the current one is computed).
+//
+// MFMA mapping (v_mfma_f32_32x32x16_bf16; C/D element i of lane l sits at column l%32,
+// row 8*(i/4) + 4*(l/32) + i%4)
+//   S^T = K . Q'^T   A = K rows from LDS (key x d), B = Q' from registers (d x query).
+//                    Each lane therefore holds ONE query and 16 keys of every 32x32 block, so
+//                    the softmax row statistics are lane-local plus one exchange with lane^32.
+//   O^T = V^T . P^T  A = V^T from LDS (d x key), B = P^T taken straight from the S registers
+//                    (converted to bf16), so P never leaves the registers.
+//   The reduction index of an MFMA can be permuted freely as long as A and B agree; V^T is
+//   stored with bits 2 and 3 of the key index swapped so the 8 keys a lane supplies for P are
+//   contiguous in LDS and every A operand is a single 16-byte LDS read.
+//
+// Softmax
+//   Q is pre-multiplied by scale*log2(e) (in fp32, before its one bf16 rounding), so
+//   p = exp2(s - m). The running max m is taken from the first tile and then kept as long as
+//   no p of a later tile would exceed 2^64 (checked on the tile's bf16 row sum); the MFMA
+//   accumulator is initialised with -m, so the subtraction costs nothing. When a tile does
+//   overflow the bound the wave rebases (rescales O and l) and recomputes that tile's p --
+//   exact, and rare. The row sum is accumulated from the bf16-rounded p that feed P.V, so the
+//   weights applied are exactly the weights normalised.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "fmha_params.hpp"
+
+namespace ltx {
+namespace {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int KT = kKeyTile;
+constexpr int QW = kQueriesPerWave;
+constexpr int NW = kWavesPerGroup;
+constexpr int QT = kQueriesPerGroup;
+constexpr int NT = NW * 64;                 // threads per workgroup
+constexpr float kRebaseBound = 1.8446744e19f;  // 2^64: largest p a tile may produce
+
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
+    bf16x2 v = {(bf16)a, (bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ void unpack8(const u32x4 w, float f[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = bf_lo(w[i]);
+        f[2 * i + 1] = bf_hi(w[i]);
+    }
+}
+
+__device__ __forceinline__ u32x4 pack8(const float f[8]) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = pack_bf2(f[2 * i], f[2 * i + 1]);
+    return w;
+}
+
+__device__ __forceinline__ u32x4 ldg16(const void *p) { return *(const u32x4 *)p; }
+
+// Raw buffer resource over [base, base + bytes): loads past the end return zero.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;   // 32-bit data format, no swizzle (gfx9 family)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
+    const int n = bytes <= 0 ? 0 : (bytes >= 0x7fffffff ? 0x7fffffff : (int)bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, kRsrcWord3);
+}
+
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ f32x16 splat16(float x) {
+    f32x16 v;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = x;
+    return v;
+}
+
+__device__ __forceinline__ float xlane32(float x) { return __shfl_xor(x, 32, 64); }
+
+// Position of key k (0..63) inside an LDS row of V^T: bits 2 and 3 swapped.
+__device__ __forceinline__ int vt_pos(int k) {
+    return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// ------------------------------------------------------------------------------------------
+// Main kernel
+// ------------------------------------------------------------------------------------------
+template <int D, bool KFUSED>
+struct FmhaTile {
+    static constexpr int NC = D / 16;       // 16-wide reduction chunks of Q.K^T
+    static constexpr int NDB = D / 32;      // 32-row blocks of O^T
+    static constexpr int KS = D + 8;        // K LDS row stride (elements)
+    static constexpr int VS = KT + 8;       // V^T LDS row stride (elements)
+    static constexpr int K_ELEMS = KT * KS;
+    static constexpr int V_ELEMS = D * VS;
+    static constexpr int STAGE = K_ELEMS + V_ELEMS;
+    static constexpr int OS = D + 8;        // epilogue staging row stride
+    static constexpr int LDS_ELEMS =
+        (2 * STAGE > NW * QW * OS) ? 2 * STAGE : NW * QW * OS;
+
+    // K staging, plain: 16-byte chunks per thread
+    static constexpr int KCPR = D / 8;                  // chunks per row
+    static constexpr int KCH = KT * KCPR / NT;          // chunks per thread
+    static constexpr int KROWS_STEP = NT / KCPR;
+    // K staging, fused: pair units (chunk c and c + D/16) per thread
+    static constexpr int KPPR = D / 16;
+    static constexpr int KFP = KT * KPPR / NT;
+    static constexpr int KFROWS_STEP = NT / KPPR;
+    // V staging: units of 4 keys x 8 channels
+    static constexpr int VUNITS = (KT / 4) * (D / 8);
+    static_assert(KCH >= 1 && KFP >= 1 && VUNITS <= NT, "tile geometry");
+};
+
+template <int D, bool KFUSED>
+__global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(1, 1)))
+void fmha_fwd_kernel(const FmhaParams p) {
+    using T = FmhaTile<D, KFUSED>;
+    constexpr int NC = T::NC, NDB = T::NDB, KS = T::KS, VS = T::VS;
+    __shared__ __attribute__((aligned(16))) bf16 smem[T::LDS_ELEMS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int r = lane & 31;
+    const int g = lane >> 5;
+
+    // ---- work item: consecutive items of one XCD share (batch, head, split) -------------
+    const int N = p.total_groups;
+    const int bid = blockIdx.x;
+    const int xcd = bid & 7;
+    const int item = xcd * (N >> 3) + min(xcd, N & 7) + (bid >> 3);
+    const int qblk = item % p.nqblk;
+    int rest = item / p.nqblk;
+    const int split = rest % p.num_splits;
+    rest /= p.num_splits;
+    const int h = rest % p.H;
+    const int b = rest / p.H;
+
+    const int n_valid = p.valid[b];
+    const int ntiles = (n_valid + KT - 1) / KT;
+    const int t_begin = split * p.tiles_per_split;
+    const int t_end = min(t_begin + p.tiles_per_split, ntiles);
+
+    const int q0 = qblk * QT + wave * QW;
+    const bool active = q0 < p.Lq;
+
+    const bf16 *Kb = (const bf16 *)p.k + (int64_t)b * p.k_bs + (int64_t)h * p.k_hs;
+    const bf16 *Vb = (const bf16 *)p.v + (int64_t)b * p.v_bs + (int64_t)h * p.v_hs;
+
+    // ---- Q: load, normalise, rotate, scale, round once -------------------------------
+    bf16x8 qf[2][NC];
+    {
+        const bf16 *Qb = (const bf16 *)p.q + (int64_t)b * p.q_bs + (int64_t)h * p.q_hs;
+        const int nq = max(0, min(QW, p.Lq - q0));   // valid queries of this wave
+        const rsrc_t rq = make_rsrc(Qb + (int64_t)(active ? q0 : 0) * p.q_rs,
+                                    (int64_t)nq * p.q_rs * 2);
+        float wq[NC][8];
+        if (p.q_rstd) {
+            const bf16 *w = (const bf16 *)p.q_w + h * D;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) unpack8(ldg16(w + 16 * c + 8 * g), wq[c]);
+        }
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int qi = 32 * qb + r;               // query within the wave
+            const int qc = min(q0 + qi, p.Lq - 1);     // clamped index for side tables
+            float x[NC][8];
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+                unpack8(bload16(rq, (uint32_t)(qi * p.q_rs * 2 + (16 * c + 8 * g) * 2)), x[c]);
+            if (p.q_rstd) {
+                const float rs = p.q_rstd[(int64_t)b * p.Lq + qc];
+#pragma unroll
+                for (int c = 0; c < NC; ++c)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[c][e] = (x[c][e] * rs) * wq[c][e];
+            }
+            if (p.q_cos) {
+                const int64_t toff = ((int64_t)h * p.Lq + qc) * (D / 2);
+                const bf16 *cs = (const bf16 *)p.q_cos + toff;
+                const bf16 *sn = (const bf16 *)p.q_sin + toff;
+#pragma unroll
+                for (int c = 0; c < NC / 2; ++c) {
+                    float fc[8], fs[8];
+                    unpack8(ldg16(cs + 16 * c + 8 * g), fc);
+                    unpack8(ldg16(sn + 16 * c + 8 * g), fs);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float x1 = x[c][e], x2 = x[c + NC / 2][e];
+                        x[c][e] = x1 * fc[e] - x2 * fs[e];
+                        x[c + NC / 2][e] = x2 * fc[e] + x1 * fs[e];
+                    }
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[c][e] *= p.qk_scale_log2;
+                qf[qb][c] = __builtin_bit_cast(bf16x8, pack8(x[c]));
+            }
+        }
+    }
+
+    // ---- staging of one key tile (global -> registers -> LDS) -------------------------
+    // Buffer loads: the resource of tile t starts at key t*KT and ends at the last valid
+    // key, so rows past it read as zero without a branch.
+    const int64_t krow_bytes = p.k_rs * 2, vrow_bytes = p.v_rs * 2;
+    auto tile_rsrc = [&](const bf16 *base, int64_t row_elems, int tile) {
+        const int rows = min(KT, n_valid - tile * KT);
+        return make_rsrc(base + (int64_t)tile * KT * row_elems, (int64_t)rows * row_elems * 2);
+    };
+    u32x4 kreg[KFUSED ? 2 * T::KFP : T::KCH];
+    u32x4 kcs[KFUSED ? T::KFP : 1], ksn[KFUSED ? T::KFP : 1];
+    float krs[KFUSED ? T::KFP : 1];
+    u32x4 vreg[4];
+    float kw1[8], kw2[8];
+    if (KFUSED && p.k_rstd) {
+        const int c = tid % T::KPPR;
+        const bf16 *w = (const bf16 *)p.k_w + h * D;
+        unpack8(ldg16(w + 8 * c), kw1);
+        unpack8(ldg16(w + D / 2 + 8 * c), kw2);
+    }
+    const bool vthr = tid < T::VUNITS;
+    const int vkg = tid & 15;
+    const int vdc = tid >> 4;
+
+    auto stage_load = [&](int tile) {
+        const rsrc_t rk = tile_rsrc(Kb, p.k_rs, tile);
+        if (!KFUSED) {
+            const int c = tid % T::KCPR;
+#pragma unroll
+            for (int i = 0; i < T::KCH; ++i) {
+                const int row = tid / T::KCPR + i * T::KROWS_STEP;
+                kreg[i] = bload16(rk, (uint32_t)(row * krow_bytes + 16 * c));
+            }
+        } else {
+            const int c = tid % T::KPPR;
+#pragma unroll
+            for (int i = 0; i < T::KFP; ++i) {
+                const int row = tid / T::KPPR + i * T::KFROWS_STEP;
+                const int key = min(tile * KT + row, n_valid - 1);
+                kreg[2 * i] = bload16(rk, (uint32_t)(row * krow_bytes + 16 * c));
+                kreg[2 * i + 1] = bload16(rk, (uint32_t)(row * krow_bytes + D + 16 * c));
+                krs[i] = p.k_rstd ? p.k_rstd[(int64_t)b * p.Lk + key] : 1.0f;
+                if (p.k_cos) {
+                    const int64_t toff = ((int64_t)h * p.Lk + key) * (D / 2) + 8 * c;
+                    kcs[i] = ldg16((const bf16 *)p.k_cos + toff);
+                    ksn[i] = ldg16((const bf16 *)p.k_sin + toff);
+                }
+            }
+        }
+        if (vthr) {
+            const rsrc_t rv = tile_rsrc(Vb, p.v_rs, tile);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                vreg[i] = bload16(rv, (uint32_t)((4 * vkg + i) * vrow_bytes + 16 * vdc));
+        }
+    };
+
+    auto stage_store = [&](int buf) {
+        bf16 *Ks = smem + buf * T::STAGE;
+        bf16 *Vt = Ks + T::K_ELEMS;
+        if (!KFUSED) {
+            const int c = tid % T::KCPR;
+#pragma unroll
+            for (int i = 0; i < T::KCH; ++i) {
+                const int row = tid / T::KCPR + i * T::KROWS_STEP;
+                *(u32x4 *)(Ks + row * KS + 8 * c) = kreg[i];
+            }
+        } else {
+            const int c = tid % T::KPPR;
+#pragma unroll
+            for (int i = 0; i < T::KFP; ++i) {
+                const int row = tid / T::KPPR + i * T::KFROWS_STEP;
+                float x1[8], x2[8];
+                unpack8(kreg[2 * i], x1);
+                unpack8(kreg[2 * i + 1], x2);
+                if (p.k_rstd) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        x1[e] = (x1[e] * krs[i]) * kw1[e];
+                        x2[e] = (x2[e] * krs[i]) * kw2[e];
+                    }
+                }
+                if (p.k_cos) {
+                    float fc[8], fs[8];
+                    unpack8(kcs[i], fc);
+                    unpack8(ksn[i], fs);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float a = x1[e], bb = x2[e];
+                        x1[e] = a * fc[e] - bb * fs[e];
+                        x2[e] = bb * fc[e] + a * fs[e];
+                    }
+                }
+                *(u32x4 *)(Ks + row * KS + 8 * c) = pack8(x1);
+                *(u32x4 *)(Ks + row * KS + D / 2 + 8 * c) = pack8(x2);
+            }
+        }
+        if (vthr) {
+            const int pos = vt_pos(4 * vkg);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t w0 = vreg[0][j >> 1], w1 = vreg[1][j >> 1];
+                const uint32_t w2 = vreg[2][j >> 1], w3 = vreg[3][j >> 1];
+                u32x2 out;
+                if ((j & 1) == 0) {
+                    out[0] = (w0 & 0xffffu) | (w1 << 16);
+                    out[1] = (w2 & 0xffffu) | (w3 << 16);
+                } else {
+                    out[0] = (w0 >> 16) | (w1 & 0xffff0000u);
+                    out[1] = (w2 >> 16) | (w3 & 0xffff0000u);
+                }
+                *(u32x2 *)(Vt + (8 * vdc + j) * VS + pos) = out;
+            }
+        }
+    };
+
+    // ---- running state ----------------------------------------------------------------
+    f32x16 o[NDB][2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) o[db][0] = o[db][1] = splat16(0.f);
+    float m[2] = {0.f, 0.f};   // running max (log2 units), identical in lanes l and l^32
+    float l[2] = {0.f, 0.f};   // this lane's share of the row sum
+    f32x16 negm[2] = {splat16(0.f), splat16(0.f)};
+    bool started = false;      // wave-uniform: a running max exists
+
+    // One 32-key half of a tile: S^T block, softmax, and its share of O^T.
+    auto compute_half = [&](const bf16 *Ks, const bf16 *Vt, int kb, int key0, bool masked) {
+        f32x16 s[2];
+        s[0] = started ? negm[0] : splat16(0.f);
+        s[1] = started ? negm[1] : splat16(0.f);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const bf16x8 a = *(const bf16x8 *)(Ks + (kb * 32 + r) * KS + 16 * c + 8 * g);
+            s[0] = mfma32(a, qf[0][c], s[0]);
+            s[1] = mfma32(a, qf[1][c], s[1]);
+        }
+        if (masked) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = key0 + 8 * (i >> 2) + 4 * g + (i & 3);
+                if (key >= n_valid) s[0][i] = s[1][i] = -INFINITY;
+            }
+        }
+        if (!started) {
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                float mx = s[qb][0];
+#pragma unroll
+                for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[qb][i]);
+                mx = fmaxf(mx, xlane32(mx));
+                m[qb] = mx;
+                negm[qb] = splat16(-mx);
+                s[qb] -= splat16(mx);
+            }
+            started = true;
+        }
+        bf16x8 pb[2][2];   // [qb][half]
+        float ts[2];
+        const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
+        // At most two passes: the second only after a rebase, whose p are all <= 1.
+        for (int pass = 0; pass < 2; ++pass) {
+            ts[0] = ts[1] = 0.f;
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                    float pv[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) pv[e] = __builtin_amdgcn_exp2f(s[qb][8 * hf + e]);
+                    const u32x4 w = pack8(pv);
+                    pb[qb][hf] = __builtin_bit_cast(bf16x8, w);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        ts[qb] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[e]),
+                                                                 ones, ts[qb], false);
+                }
+            const bool bad = !(ts[0] <= kRebaseBound) || !(ts[1] <= kRebaseBound);
+            if (!__any(bad)) break;
+            // A later block outgrew the running max: rebase to this block's max (exact).
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                float mx = s[qb][0];
+#pragma unroll
+                for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[qb][i]);
+                mx = fmaxf(mx, xlane32(mx));
+                const float d = mx > 0.f ? mx : 0.f;
+                const float f = __builtin_amdgcn_exp2f(-d);
+                m[qb] += d;
+                negm[qb] = splat16(-m[qb]);
+                l[qb] *= f;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) o[db][qb] *= splat16(f);
+                s[qb] -= splat16(d);
+            }
+        }
+        l[0] += ts[0];
+        l[1] += ts[1];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int t4 = 2 * kb + hf;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const bf16x8 a = *(const bf16x8 *)(Vt + (db * 32 + r) * VS + 16 * t4 + 8 * g);
+                o[db][0] = mfma32(a, pb[0][hf], o[db][0]);
+                o[db][1] = mfma32(a, pb[1][hf], o[db][1]);
+            }
+        }
+    };
+
+    // ---- main loop ----------------------------------------------------------------------
+    if (t_begin < t_end) {
+        stage_load(t_begin);
+        stage_store(0);
+    }
+    __syncthreads();
+    for (int t = t_begin; t < t_end; ++t) {
+        const int buf = (t - t_begin) & 1;
+        const bool has_next = t + 1 < t_end;
+        if (has_next) stage_load(t + 1);
+        if (active) {
+            const bf16 *Ks = smem + buf * T::STAGE;
+            const bf16 *Vt = Ks + T::K_ELEMS;
+            const int key0 = t * KT;
+            // Keys past n_valid are zero-filled in LDS and masked here; a half with no valid
+            // key is skipped outright.
+            compute_half(Ks, Vt, 0, key0, key0 + 32 > n_valid);
+            if (key0 + 32 < n_valid) compute_half(Ks, Vt, 1, key0 + 32, key0 + KT > n_valid);
+        }
+        if (has_next) stage_store(buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue ---------------------------------------------------------------------
+    float lt[2];
+    lt[0] = l[0] + xlane32(l[0]);
+    lt[1] = l[1] + xlane32(l[1]);
+
+    if (p.num_splits > 1) {
+        if (!active) return;
+        const bool empty = t_begin >= t_end;
+        const int64_t rowbase = (((int64_t)split * p.B + b) * p.H + h) * p.Lq;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int q = q0 + 32 * qb + r;
+            if (q >= p.Lq) continue;
+            float *po = p.part_o + (rowbase + q) * D;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    f32x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = o[db][qb][4 * i4 + e];
+                    *(f32x4 *)(po + db * 32 + 8 * i4 + 4 * g) = v;
+                }
+            if (g == 0) {
+                float *ml = p.part_ml + (rowbase + q) * 2;
+                ml[0] = empty ? -INFINITY : m[qb];
+                ml[1] = empty ? 0.f : lt[qb];
+            }
+        }
+        return;
+    }
+
+    // Unsplit: normalise, stage O through LDS, store coalesced 16-byte rows.
+    bf16 *Os = smem + wave * QW * T::OS;
+    if (active) {
+        const float inv0 = 1.0f / lt[0], inv1 = 1.0f / lt[1];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const float inv = qb ? inv1 : inv0;
+                    u32x2 w;
+                    w[0] = pack_bf2(o[db][qb][4 * i4 + 0] * inv, o[db][qb][4 * i4 + 1] * inv);
+                    w[1] = pack_bf2(o[db][qb][4 * i4 + 2] * inv, o[db][qb][4 * i4 + 3] * inv);
+                    *(u32x2 *)(Os + (32 * qb + r) * T::OS + db * 32 + 8 * i4 + 4 * g) = w;
+                }
+    }
+    __syncthreads();
+    if (active) {
+        bf16 *Ob = (bf16 *)p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs;
+        constexpr int CPR = D / 8;
+#pragma unroll
+        for (int it = 0; it < QW * CPR / 64; ++it) {
+            const int u = lane + 64 * it;
+            const int row = u / CPR, c = u % CPR;
+            const int q = q0 + row;
+            if (q < p.Lq)
+                *(u32x4 *)(Ob + (int64_t)q * p.o_rs + 8 * c) =
+                    *(const u32x4 *)(Os + row * T::OS + 8 * c);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Prologue: per-token RMS statistic over the inner dim (DiTAttention.swift:202-204), and for
+// the K-prologue strategy the normalised + rotated tensor in the merged layout.
+// One workgroup per token row.
+// ------------------------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void qk_prep_kernel(const PrepParams p) {
+    constexpr int PPH = D / 16;               // pair units per head
+    constexpr int MAXU = 4;                   // pair units per thread (inner <= 16384)
+    const int tid = threadIdx.x;
+    const int rid = blockIdx.x;
+    const int b = rid / p.L;
+    const int lrow = rid % p.L;
+    const int inner = p.H * D;
+    const int units = p.H * PPH;
+    const bf16 *row = (const bf16 *)p.x + (int64_t)b * p.bs + (int64_t)lrow * p.rs;
+
+    float x1[MAXU][8], x2[MAXU][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < MAXU; ++k) {
+        const int u = tid + 256 * k;
+        if (u < units) {
+            const int hh = u / PPH, c = u % PPH;
+            const bf16 *src = row + (int64_t)hh * p.hs;
+            unpack8(ldg16(src + 8 * c), x1[k]);
+            unpack8(ldg16(src + D / 2 + 8 * c), x2[k]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += x1[k][e] * x1[k][e] + x2[k][e] * x2[k][e];
+        }
+    }
+    float rstd = 1.0f;
+    if (p.w) {
+        __shared__ float red[4];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        const float tot = red[0] + red[1] + red[2] + red[3];
+        rstd = 1.0f / sqrtf(tot / (float)inner + p.eps);
+        if (tid == 0 && p.rstd) p.rstd[rid] = rstd;
+    }
+    if (!p.out) return;
+    bf16 *dst = (bf16 *)p.out + (int64_t)rid * inner;
+#pragma unroll
+    for (int k = 0; k < MAXU; ++k) {
+        const int u = tid + 256 * k;
+        if (u >= units) continue;
+        const int hh = u / PPH, c = u % PPH;
+        if (p.w) {
+            float w1[8], w2[8];
+            const bf16 *w = (const bf16 *)p.w + hh * D;
+            unpack8(ldg16(w + 8 * c), w1);
+            unpack8(ldg16(w + D / 2 + 8 * c), w2);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                x1[k][e] = (x1[k][e] * rstd) * w1[e];
+                x2[k][e] = (x2[k][e] * rstd) * w2[e];
+            }
+        }
+        if (p.cos) {
+            const int64_t toff = ((int64_t)hh * p.L + lrow) * (D / 2) + 8 * c;
+            float fc[8], fs[8];
+            unpack8(ldg16((const bf16 *)p.cos + toff), fc);
+            unpack8(ldg16((const bf16 *)p.sin + toff), fs);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float a = x1[k][e], bb = x2[k][e];
+                x1[k][e] = a * fc[e] - bb * fs[e];
+                x2[k][e] = bb * fc[e] + a * fs[e];
+            }
+        }
+        *(u32x4 *)(dst + hh * D + 8 * c) = pack8(x1[k]);
+        *(u32x4 *)(dst + hh * D + D / 2 + 8 * c) = pack8(x2[k]);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Split-KV combine: O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s, rounded to bf16.
+// ------------------------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void combine_kernel(const CombineParams p) {
+    constexpr int TPR = D / 4;                 // threads per row (4 channels each)
+    constexpr int RPB = 256 / TPR;             // rows per block
+    const int tid = threadIdx.x;
+    const int64_t row = (int64_t)blockIdx.x * RPB + tid / TPR;
+    const int64_t rows = (int64_t)p.B * p.H * p.Lq;
+    if (row >= rows) return;
+    const int d = 4 * (tid % TPR);
+    const int S = p.num_splits;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, p.part_ml[(s * rows + row) * 2]);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+    for (int s = 0; s < S; ++s) {
+        const float ms = p.part_ml[(s * rows + row) * 2];
+        if (ms == -INFINITY) continue;
+        const float w = __builtin_amdgcn_exp2f(ms - M);
+        den += w * p.part_ml[(s * rows + row) * 2 + 1];
+        acc += w * *(const f32x4 *)(p.part_o + (s * rows + row) * D + d);
+    }
+    const float inv = 1.0f / den;
+    const int q = (int)(row % p.Lq);
+    const int hb = (int)(row / p.Lq);
+    const int hh = hb % p.H, b = hb / p.H;
+    u32x2 w;
+    w[0] = pack_bf2(acc[0] * inv, acc[1] * inv);
+    w[1] = pack_bf2(acc[2] * inv, acc[3] * inv);
+    *(u32x2 *)((bf16 *)p.o + (int64_t)b * p.o_bs + (int64_t)q * p.o_rs + (int64_t)hh * p.o_hs +
+               d) = w;
+}
+
+}  // namespace
+
+int launch_fmha(const FmhaParams &p, int D, bool k_fused, void *stream) {
+    const dim3 grid(p.total_groups), block(NT);
+    hipStream_t st = (hipStream_t)stream;
+    if (D == 128) {
+        if (k_fused) hipLaunchKernelGGL((fmha_fwd_kernel<128, true>), grid, block, 0, st, p);
+        else hipLaunchKernelGGL((fmha_fwd_kernel<128, false>), grid, block, 0, st, p);
+    } else {
+        if (k_fused) hipLaunchKernelGGL((fmha_fwd_kernel<64, true>), grid, block, 0, st, p);
+        else hipLaunchKernelGGL((fmha_fwd_kernel<64, false>), grid, block, 0, st, p);
+    }
+    return (int)hipGetLastError();
+}
+
+int launch_prep(const PrepParams &p, int D, void *stream) {
+    const dim3 grid(p.B * p.L), block(256);
+    hipStream_t st = (hipStream_t)stream;
+    if (D == 128) hipLaunchKernelGGL(qk_prep_kernel<128>, grid, block, 0, st, p);
+    else hipLaunchKernelGGL(qk_prep_kernel<64>, grid, block, 0, st, p);
+    return (int)hipGetLastError();
+}
+
+int launch_combine(const CombineParams &p, int D, void *stream) {
+    const int64_t rows = (int64_t)p.B * p.H * p.Lq;
+    const int rpb = 256 / (D / 4);
+    const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block(256);
+    hipStream_t st = (hipStream_t)stream;
+    if (D == 128) hipLaunchKernelGGL(combine_kernel<128>, grid, block, 0, st, p);
+    else hipLaunchKernelGGL(combine_kernel<64>, grid, block, 0, st, p);
+    return (int)hipGetLastError();
+}
+
+}  // namespace ltx

@@ -1,0 +1,77 @@
+// Kernel parameter blocks shared by the HIP kernels (fmha_fwd.hip) and the C-ABI layer
+// (ltx_attn_abi.cpp). Plain data only: no HIP or torch types.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ltx {
+
+constexpr int kMaxBatch = 64;      // per-row key lengths travel in the kernel arguments
+constexpr int kKeyTile = 64;       // keys per LDS tile
+constexpr int kQueriesPerWave = 64;
+constexpr int kWavesPerGroup = 4;
+constexpr int kQueriesPerGroup = kQueriesPerWave * kWavesPerGroup;  // 256
+constexpr int kMaxSplits = 16;
+
+// Main attention kernel.
+struct FmhaParams {
+    const void *q, *k, *v;           // bf16
+    int64_t q_bs, q_rs, q_hs;
+    int64_t k_bs, k_rs, k_hs;
+    int64_t v_bs, v_rs, v_hs;
+    void *o;                         // bf16 output (unsplit) -- element strides below
+    int64_t o_bs, o_rs, o_hs;
+    int32_t B, H, Lq, Lk;
+
+    // Q prologue, applied in registers when the wave loads its queries.
+    const float *q_rstd;             // [B][Lq] or null (no norm)
+    const void *q_w;                 // bf16 [H*D] (with q_rstd)
+    const void *q_cos, *q_sin;       // bf16 [H][Lq][D/2] or null (no RoPE)
+
+    // K prologue applied while staging K into LDS (KFUSED kernels only).
+    const float *k_rstd;             // [B][Lk] or null
+    const void *k_w;
+    const void *k_cos, *k_sin;       // bf16 [H][Lk][D/2] or null
+
+    float qk_scale_log2;             // softmax scale * log2(e), folded into Q
+
+    int32_t nqblk;                   // ceil(Lq / 256)
+    int32_t num_splits;              // >= 1
+    int32_t tiles_per_split;         // key tiles per split
+    int32_t total_groups;            // B * H * num_splits * nqblk
+
+    float *part_o;                   // split-KV partials [S][B][H][Lq][D] fp32 (num_splits > 1)
+    float *part_ml;                  // [S][B][H][Lq][2]: running max (log2 units), row sum
+
+    int32_t valid[kMaxBatch];        // keys valid per batch row (Lk when unmasked)
+};
+
+// Per-token RMS statistic over the inner dim, optionally writing the normalised and rotated
+// tensor (the K prologue).
+struct PrepParams {
+    const void *x;                   // bf16
+    int64_t bs, rs, hs;
+    int32_t B, L, H;
+    const void *w;                   // bf16 [H*D] or null (no norm)
+    float eps;
+    const void *cos, *sin;           // bf16 [H][L][D/2] or null
+    float *rstd;                     // [B][L] or null
+    void *out;                       // bf16 [B][L][H*D] contiguous or null
+};
+
+// Split-KV combine.
+struct CombineParams {
+    const float *part_o;
+    const float *part_ml;
+    void *o;
+    int64_t o_bs, o_rs, o_hs;
+    int32_t B, H, Lq, num_splits;
+};
+
+// Launchers (fmha_fwd.hip). Return the hipError_t of the launch as int.
+int launch_fmha(const FmhaParams &p, int D, bool k_fused, void *stream);
+int launch_prep(const PrepParams &p, int D, void *stream);
+int launch_combine(const CombineParams &p, int D, void *stream);
+
+}  // namespace ltx

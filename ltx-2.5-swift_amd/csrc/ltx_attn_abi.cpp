@@ -1,0 +1,356 @@
+// C-ABI entry points of libltx_attn.so (declared in include/ltx_attn.h).
+//
+// Replaces the arithmetic of Sources/LTXModules/DiTAttention.swift:358-381: the QK-RMSNorm
+// (:360-361 -> :202-204), the head split (:362 -> :346-349), split RoPE (:364-367 ->
+// :226-234) and MLXFast.scaledDotProductAttention (:374-376). Everything here runs on the
+// host: argument validation (before any launch), the choice of K strategy and split count,
+// the workspace layout, and the launches on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "../../include/ltx_attn.h"
+#include "fmha_params.hpp"
+
+namespace {
+
+thread_local char g_err[512];
+
+ltx_attn_status fail(ltx_attn_status s, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return s;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Everything ltx_attn_fwd decides from the arguments alone.
+struct Plan {
+    bool q_norm = false, k_norm = false;
+    bool q_rope = false, k_rope = false;
+    bool k_prologue = false;   // K normalised/rotated by a separate pass into the workspace
+    bool k_fused = false;      // K normalised/rotated while staging into LDS
+    int nqblk = 0;
+    int ntiles_max = 0;
+    int splits = 1;
+    int tiles_per_split = 0;
+    // workspace layout (byte offsets)
+    size_t off_qrstd = 0, off_krstd = 0, off_kprep = 0, off_part_o = 0, off_part_ml = 0;
+    size_t bytes = 0;
+};
+
+ltx_attn_status check_tensor(const char *name, const void *ptr, int64_t bs, int64_t rs,
+                             int64_t hs, int B, int L, int H, int D) {
+    if (!ptr) return fail(LTX_ATTN_EINVAL, "%s is NULL", name);
+    if (!aligned16(ptr)) return fail(LTX_ATTN_EINVAL, "%s is not 16-byte aligned", name);
+    if (bs < 0 || rs < 0 || hs < 0)
+        return fail(LTX_ATTN_EINVAL, "%s has a negative stride", name);
+    if ((bs % 8) || (rs % 8) || (hs % 8))
+        return fail(LTX_ATTN_EINVAL,
+                    "%s strides (%lld, %lld, %lld) must be multiples of 8 elements", name,
+                    (long long)bs, (long long)rs, (long long)hs);
+    if (H > 1 && hs < D)
+        return fail(LTX_ATTN_EINVAL, "%s head stride %lld overlaps a %d-wide head", name,
+                    (long long)hs, D);
+    if (L > 1 && rs < D)
+        return fail(LTX_ATTN_EINVAL, "%s row stride %lld is below the head dim %d", name,
+                    (long long)rs, D);
+    if (B > 1 && bs == 0) return fail(LTX_ATTN_EINVAL, "%s batch stride is 0", name);
+    return LTX_ATTN_OK;
+}
+
+ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
+    g_err[0] = 0;
+    if (!a) return fail(LTX_ATTN_EINVAL, "args is NULL");
+    if (a->B < 1 || a->H < 1 || a->Lq < 1 || a->Lk < 1)
+        return fail(LTX_ATTN_EINVAL, "B, H, Lq, Lk must be >= 1 (got %d, %d, %d, %d)", a->B,
+                    a->H, a->Lq, a->Lk);
+    if (a->D != 64 && a->D != 128)
+        return fail(LTX_ATTN_EUNSUPPORTED, "head dim %d is not 64 or 128", a->D);
+    const int B = a->B, H = a->H, D = a->D;
+    if ((int64_t)H * D > 16384)
+        return fail(LTX_ATTN_EUNSUPPORTED, "inner dim %lld above 16384", (long long)H * D);
+    ltx_attn_status s;
+    if ((s = check_tensor("q", a->q, a->q_bs, a->q_rs, a->q_hs, B, a->Lq, H, D))) return s;
+    if ((s = check_tensor("k", a->k, a->k_bs, a->k_rs, a->k_hs, B, a->Lk, H, D))) return s;
+    if ((s = check_tensor("v", a->v, a->v_bs, a->v_rs, a->v_hs, B, a->Lk, H, D))) return s;
+    if ((s = check_tensor("out", a->out, a->o_bs, a->o_rs, a->o_hs, B, a->Lq, H, D))) return s;
+    if (!(a->scale > 0.f) || !isfinite(a->scale))
+        return fail(LTX_ATTN_EINVAL, "scale must be positive and finite");
+
+    pl->q_norm = a->q_norm_w != nullptr;
+    pl->k_norm = a->k_norm_w != nullptr;
+    if ((pl->q_norm && !aligned16(a->q_norm_w)) || (pl->k_norm && !aligned16(a->k_norm_w)))
+        return fail(LTX_ATTN_EINVAL, "norm weights must be 16-byte aligned");
+    if ((pl->q_norm || pl->k_norm) && !(a->norm_eps >= 0.f && isfinite(a->norm_eps)))
+        return fail(LTX_ATTN_EINVAL, "norm_eps must be finite and >= 0");
+
+    const bool qt = a->q_cos || a->q_sin, kt = a->k_cos || a->k_sin;
+    if ((a->q_cos == nullptr) != (a->q_sin == nullptr) ||
+        (a->k_cos == nullptr) != (a->k_sin == nullptr))
+        return fail(LTX_ATTN_EINVAL, "a rotary table pair needs both cos and sin");
+    if (kt && !qt)
+        return fail(LTX_ATTN_EINVAL,
+                    "key rotary tables without query tables (keyRotary without rotary)");
+    if (qt && !kt && a->Lq != a->Lk)
+        return fail(LTX_ATTN_EINVAL,
+                    "K shares Q's rotary tables but Lq (%d) != Lk (%d); pass k_cos/k_sin",
+                    a->Lq, a->Lk);
+    for (const void *t : {a->q_cos, a->q_sin, a->k_cos, a->k_sin})
+        if (t && !aligned16(t)) return fail(LTX_ATTN_EINVAL, "rotary tables must be 16-byte aligned");
+    pl->q_rope = qt;
+    pl->k_rope = qt;
+
+    if (a->k_valid_len) {
+        if (B > ltx::kMaxBatch)
+            return fail(LTX_ATTN_EUNSUPPORTED, "key-padding lengths need B <= %d (got %d)",
+                        ltx::kMaxBatch, B);
+        for (int b = 0; b < B; ++b)
+            if (a->k_valid_len[b] < 1 || a->k_valid_len[b] > a->Lk)
+                return fail(LTX_ATTN_EINVAL, "k_valid_len[%d] = %d outside [1, %d]", b,
+                            a->k_valid_len[b], a->Lk);
+    } else if (B > 65535) {
+        return fail(LTX_ATTN_EUNSUPPORTED, "batch %d too large", B);
+    }
+    if (a->kprep < LTX_ATTN_KPREP_AUTO || a->kprep > LTX_ATTN_KPREP_PROLOGUE)
+        return fail(LTX_ATTN_EINVAL, "kprep %d is not an ltx_attn_kprep", a->kprep);
+    if (a->num_splits < 0 || a->num_splits > ltx::kMaxSplits)
+        return fail(LTX_ATTN_EINVAL, "num_splits %d outside [0, %d]", a->num_splits,
+                    ltx::kMaxSplits);
+
+    pl->nqblk = (a->Lq + ltx::kQueriesPerGroup - 1) / ltx::kQueriesPerGroup;
+    pl->ntiles_max = (a->Lk + ltx::kKeyTile - 1) / ltx::kKeyTile;
+    if (a->k_valid_len) {
+        int nmax = 1;
+        for (int b = 0; b < B; ++b) nmax = std::max(nmax, (int)a->k_valid_len[b]);
+        pl->ntiles_max = (nmax + ltx::kKeyTile - 1) / ltx::kKeyTile;
+    }
+
+    // K strategy: a separate prologue pays one extra read+write of K; fusing pays the
+    // norm/RoPE arithmetic once per query block that re-reads K.
+    const bool k_work = pl->k_norm || pl->k_rope;
+    if (k_work) {
+        if (a->kprep == LTX_ATTN_KPREP_PROLOGUE) pl->k_prologue = true;
+        else if (a->kprep == LTX_ATTN_KPREP_FUSED) pl->k_fused = true;
+        else if (pl->nqblk >= 2) pl->k_prologue = true;
+        else pl->k_fused = true;
+    }
+
+    // Split-KV when (batch, head, query block) items alone cannot fill the chip.
+    const int64_t base = (int64_t)B * H * pl->nqblk;
+    int splits = a->num_splits;
+    if (splits == 0) {
+        splits = 1;
+        if (base < 256) {
+            splits = (int)((320 + base - 1) / base);
+            splits = std::min(splits, ltx::kMaxSplits);
+            splits = std::min(splits, std::max(1, pl->ntiles_max / 2));
+        }
+    }
+    splits = std::max(1, std::min(splits, pl->ntiles_max));
+    if (B > ltx::kMaxBatch) splits = 1;   // batches beyond one argument table run unsplit
+    pl->tiles_per_split = (pl->ntiles_max + splits - 1) / splits;
+    pl->splits = (pl->ntiles_max + pl->tiles_per_split - 1) / pl->tiles_per_split;
+    if (base * pl->splits > 0x7fffffff)
+        return fail(LTX_ATTN_EUNSUPPORTED, "grid too large");
+
+    size_t off = 0;
+    if (pl->q_norm) {
+        pl->off_qrstd = off;
+        off = align_up(off + sizeof(float) * (size_t)B * a->Lq, 256);
+    }
+    if (pl->k_norm && pl->k_fused) {
+        pl->off_krstd = off;
+        off = align_up(off + sizeof(float) * (size_t)B * a->Lk, 256);
+    }
+    if (pl->k_prologue) {
+        pl->off_kprep = off;
+        off = align_up(off + 2 * (size_t)B * a->Lk * H * D, 256);
+    }
+    if (pl->splits > 1) {
+        const size_t rows = (size_t)pl->splits * B * H * a->Lq;
+        pl->off_part_o = off;
+        off = align_up(off + sizeof(float) * rows * D, 256);
+        pl->off_part_ml = off;
+        off = align_up(off + sizeof(float) * rows * 2, 256);
+    }
+    pl->bytes = off;
+    return LTX_ATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void ltx_attn_args_init(ltx_attn_args *a) {
+    if (!a) return;
+    memset(a, 0, sizeof *a);
+    a->norm_eps = 1e-6f;
+    a->kprep = LTX_ATTN_KPREP_AUTO;
+    a->num_splits = 0;
+}
+
+size_t ltx_attn_workspace_bytes(const ltx_attn_args *a) {
+    Plan pl;
+    if (make_plan(a, &pl) != LTX_ATTN_OK) return 0;
+    return pl.bytes;
+}
+
+ltx_attn_status ltx_attn_validate(const ltx_attn_args *a) {
+    Plan pl;
+    ltx_attn_status s = make_plan(a, &pl);
+    if (s) return s;
+    if (pl.bytes > 0) {
+        if (!a->workspace || a->workspace_bytes < pl.bytes)
+            return fail(LTX_ATTN_EWORKSPACE, "workspace of %zu bytes needed (got %zu at %p)",
+                        pl.bytes, a->workspace_bytes, a->workspace);
+        if ((uintptr_t)a->workspace & 255u)
+            return fail(LTX_ATTN_EINVAL, "workspace must be 256-byte aligned");
+    }
+    return LTX_ATTN_OK;
+}
+
+ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
+    ltx_attn_status s = ltx_attn_validate(a);
+    if (s) return s;
+    Plan pl;
+    make_plan(a, &pl);
+    char *ws = (char *)a->workspace;
+    const int B = a->B, H = a->H, D = a->D;
+
+    // 1. prologue passes: statistic (and, for the K prologue, the prepared K)
+    if (pl.q_norm) {
+        ltx::PrepParams pp{};
+        pp.x = a->q; pp.bs = a->q_bs; pp.rs = a->q_rs; pp.hs = a->q_hs;
+        pp.B = B; pp.L = a->Lq; pp.H = H;
+        pp.w = a->q_norm_w; pp.eps = a->norm_eps;
+        pp.rstd = (float *)(ws + pl.off_qrstd);
+        if (int e = ltx::launch_prep(pp, D, stream))
+            return fail(LTX_ATTN_EHIP, "q prologue launch: %s", hipGetErrorString((hipError_t)e));
+    }
+    const void *kptr = a->k;
+    int64_t k_bs = a->k_bs, k_rs = a->k_rs, k_hs = a->k_hs;
+    if (pl.k_prologue || (pl.k_fused && pl.k_norm)) {
+        ltx::PrepParams pp{};
+        pp.x = a->k; pp.bs = a->k_bs; pp.rs = a->k_rs; pp.hs = a->k_hs;
+        pp.B = B; pp.L = a->Lk; pp.H = H;
+        pp.w = a->k_norm_w; pp.eps = a->norm_eps;
+        if (pl.k_prologue) {
+            pp.out = ws + pl.off_kprep;
+            pp.cos = a->k_cos ? a->k_cos : a->q_cos;
+            pp.sin = a->k_sin ? a->k_sin : a->q_sin;
+        } else {
+            pp.rstd = (float *)(ws + pl.off_krstd);
+        }
+        if (int e = ltx::launch_prep(pp, D, stream))
+            return fail(LTX_ATTN_EHIP, "k prologue launch: %s", hipGetErrorString((hipError_t)e));
+        if (pl.k_prologue) {
+            kptr = ws + pl.off_kprep;
+            k_bs = (int64_t)a->Lk * H * D; k_rs = (int64_t)H * D; k_hs = D;
+        }
+    }
+
+    // 2. attention
+    ltx::FmhaParams fp{};
+    fp.q = a->q; fp.q_bs = a->q_bs; fp.q_rs = a->q_rs; fp.q_hs = a->q_hs;
+    fp.k = kptr; fp.k_bs = k_bs; fp.k_rs = k_rs; fp.k_hs = k_hs;
+    fp.v = a->v; fp.v_bs = a->v_bs; fp.v_rs = a->v_rs; fp.v_hs = a->v_hs;
+    fp.o = a->out; fp.o_bs = a->o_bs; fp.o_rs = a->o_rs; fp.o_hs = a->o_hs;
+    fp.B = B; fp.H = H; fp.Lq = a->Lq; fp.Lk = a->Lk;
+    if (pl.q_norm) { fp.q_rstd = (const float *)(ws + pl.off_qrstd); fp.q_w = a->q_norm_w; }
+    if (pl.q_rope) { fp.q_cos = a->q_cos; fp.q_sin = a->q_sin; }
+    if (pl.k_fused) {
+        if (pl.k_norm) { fp.k_rstd = (const float *)(ws + pl.off_krstd); fp.k_w = a->k_norm_w; }
+        if (pl.k_rope) {
+            fp.k_cos = a->k_cos ? a->k_cos : a->q_cos;
+            fp.k_sin = a->k_sin ? a->k_sin : a->q_sin;
+        }
+    }
+    fp.qk_scale_log2 = (float)((double)a->scale * 1.4426950408889634);
+    fp.nqblk = pl.nqblk;
+    fp.num_splits = pl.splits;
+    fp.tiles_per_split = pl.tiles_per_split;
+    fp.total_groups = B * H * pl.splits * pl.nqblk;
+    if (pl.splits > 1) {
+        fp.part_o = (float *)(ws + pl.off_part_o);
+        fp.part_ml = (float *)(ws + pl.off_part_ml);
+    }
+    for (int b = 0; b < std::min(B, ltx::kMaxBatch); ++b)
+        fp.valid[b] = a->k_valid_len ? a->k_valid_len[b] : a->Lk;
+    if (!a->k_valid_len && B > ltx::kMaxBatch) {
+        // Unmasked batches beyond the argument table are launched in slices of kMaxBatch.
+        for (int b0 = 0; b0 < B; b0 += ltx::kMaxBatch) {
+            ltx::FmhaParams sp = fp;
+            const int nb = std::min(ltx::kMaxBatch, B - b0);
+            sp.B = nb;
+            sp.q = (const char *)a->q + 2 * (int64_t)b0 * a->q_bs;
+            sp.k = (const char *)kptr + 2 * (int64_t)b0 * k_bs;
+            sp.v = (const char *)a->v + 2 * (int64_t)b0 * a->v_bs;
+            sp.o = (char *)a->out + 2 * (int64_t)b0 * a->o_bs;
+            if (sp.q_rstd) sp.q_rstd += (int64_t)b0 * a->Lq;
+            if (sp.k_rstd) sp.k_rstd += (int64_t)b0 * a->Lk;
+            sp.total_groups = nb * H * pl.splits * pl.nqblk;
+            if (a->ev_attn_start && b0 == 0)
+                if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_start, (hipStream_t)stream))
+                    return fail(LTX_ATTN_EHIP, "event record: %s", hipGetErrorString(e));
+            if (int e = ltx::launch_fmha(sp, D, pl.k_fused, stream))
+                return fail(LTX_ATTN_EHIP, "attention launch: %s", hipGetErrorString((hipError_t)e));
+        }
+        if (a->ev_attn_stop)
+            if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_stop, (hipStream_t)stream))
+                return fail(LTX_ATTN_EHIP, "event record: %s", hipGetErrorString(e));
+        return LTX_ATTN_OK;
+    }
+    if (a->ev_attn_start)
+        if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_start, (hipStream_t)stream))
+            return fail(LTX_ATTN_EHIP, "event record: %s", hipGetErrorString(e));
+    if (int e = ltx::launch_fmha(fp, D, pl.k_fused, stream))
+        return fail(LTX_ATTN_EHIP, "attention launch: %s", hipGetErrorString((hipError_t)e));
+    if (a->ev_attn_stop)
+        if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_stop, (hipStream_t)stream))
+            return fail(LTX_ATTN_EHIP, "event record: %s", hipGetErrorString(e));
+
+    // 3. split-KV combine
+    if (pl.splits > 1) {
+        ltx::CombineParams cp{};
+        cp.part_o = fp.part_o; cp.part_ml = fp.part_ml;
+        cp.o = a->out; cp.o_bs = a->o_bs; cp.o_rs = a->o_rs; cp.o_hs = a->o_hs;
+        cp.B = B; cp.H = H; cp.Lq = a->Lq; cp.num_splits = pl.splits;
+        if (int e = ltx::launch_combine(cp, D, stream))
+            return fail(LTX_ATTN_EHIP, "combine launch: %s", hipGetErrorString((hipError_t)e));
+    }
+    return LTX_ATTN_OK;
+}
+
+const char *ltx_attn_status_string(ltx_attn_status s) {
+    switch (s) {
+    case LTX_ATTN_OK: return "ok";
+    case LTX_ATTN_EINVAL: return "invalid argument";
+    case LTX_ATTN_EUNSUPPORTED: return "unsupported configuration";
+    case LTX_ATTN_EHIP: return "HIP runtime error";
+    case LTX_ATTN_EWORKSPACE: return "workspace too small";
+    }
+    return "unknown status";
+}
+
+const char *ltx_attn_last_error(void) { return g_err; }
+
+const char *ltx_attn_provenance(void) {
+    return "hip-gfx950 fused flash attention v1 (bf16 mfma_f32_32x32x16, online fp32 softmax, "
+           "QK-RMSNorm+RoPE fused)";
+}
+
+int32_t ltx_attn_abi_version(void) { return LTX_ATTN_ABI_VERSION; }
+
+size_t ltx_attn_args_size(void) { return sizeof(ltx_attn_args); }
+
+}  // extern "C"

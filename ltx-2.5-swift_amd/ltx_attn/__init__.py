@@ -1,0 +1,415 @@
+"""Python host binding of libltx_attn.so (MI355X fused DiT attention).
+
+A thin ctypes layer over the C ABI in ``include/ltx_attn.h``. It mirrors the reference's call
+surface for the replaced unit:
+
+* ``DiTAttentionCore``  -- the norm -> split -> RoPE -> SDPA part of
+  ``DiTAttention.callAsFunction`` (``Sources/LTXModules/DiTAttention.swift:315-381``), with the
+  reference's ``Variant`` / ``Rotary`` / ``Failure`` vocabulary (``:69-122``).
+* ``scaled_dot_product_attention`` -- ``MLXFast.scaledDotProductAttention(queries:keys:values:
+  scale:mask:)`` on ``[B, H, L, D]`` inputs (``DiTAttention.swift:374-376``), plus an optional
+  key-padding length per batch row.
+* ``rope_*`` -- the rotary-table builders of ``Sources/LTXModules/DiTForward.swift:455-738``.
+
+PyTorch supplies device memory and the stream only; every arithmetic step runs in the HIP
+library. If the library is missing this module raises -- there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import enum
+import math
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libltx_attn.so")
+
+OK, EINVAL, EUNSUPPORTED, EHIP, EWORKSPACE = 0, 1, 2, 3, 4
+KPREP_AUTO, KPREP_FUSED, KPREP_PROLOGUE = 0, 1, 2
+MAX_BATCH = 64
+
+
+class Args(ctypes.Structure):
+    """``ltx_attn_args`` (field order and types as in include/ltx_attn.h)."""
+
+    _fields_ = [
+        ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("Lq", ctypes.c_int32),
+        ("Lk", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("q_bs", ctypes.c_int64), ("q_rs", ctypes.c_int64), ("q_hs", ctypes.c_int64),
+        ("k_bs", ctypes.c_int64), ("k_rs", ctypes.c_int64), ("k_hs", ctypes.c_int64),
+        ("v_bs", ctypes.c_int64), ("v_rs", ctypes.c_int64), ("v_hs", ctypes.c_int64),
+        ("q_norm_w", ctypes.c_void_p), ("k_norm_w", ctypes.c_void_p),
+        ("norm_eps", ctypes.c_float),
+        ("q_cos", ctypes.c_void_p), ("q_sin", ctypes.c_void_p),
+        ("k_cos", ctypes.c_void_p), ("k_sin", ctypes.c_void_p),
+        ("k_valid_len", ctypes.POINTER(ctypes.c_int32)),
+        ("scale", ctypes.c_float),
+        ("out", ctypes.c_void_p),
+        ("o_bs", ctypes.c_int64), ("o_rs", ctypes.c_int64), ("o_hs", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("kprep", ctypes.c_int32), ("num_splits", ctypes.c_int32),
+        ("ev_attn_start", ctypes.c_void_p), ("ev_attn_stop", ctypes.c_void_p),
+    ]
+
+
+EXPORTED_SYMBOLS = (
+    "ltx_attn_args_init", "ltx_attn_workspace_bytes", "ltx_attn_validate", "ltx_attn_fwd",
+    "ltx_attn_status_string", "ltx_attn_last_error", "ltx_attn_provenance",
+    "ltx_attn_abi_version", "ltx_attn_args_size", "ltx_rope_frequency_grid", "ltx_rope_video_positions",
+    "ltx_rope_audio_positions", "ltx_rope_tables",
+)
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load (once) and type the library. Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"libltx_attn.so not found at {path}; build it with "
+                           "`python -c 'import __graft_entry__ as g; g.build()'` or "
+                           "`make -C ltx-2.5-swift_amd/csrc`")
+    lib = ctypes.CDLL(path)
+    P = ctypes.POINTER(Args)
+    lib.ltx_attn_args_init.argtypes = [P]
+    lib.ltx_attn_args_init.restype = None
+    lib.ltx_attn_workspace_bytes.argtypes = [P]
+    lib.ltx_attn_workspace_bytes.restype = ctypes.c_size_t
+    lib.ltx_attn_validate.argtypes = [P]
+    lib.ltx_attn_validate.restype = ctypes.c_int
+    lib.ltx_attn_fwd.argtypes = [P, ctypes.c_void_p]
+    lib.ltx_attn_fwd.restype = ctypes.c_int
+    lib.ltx_attn_status_string.argtypes = [ctypes.c_int]
+    lib.ltx_attn_status_string.restype = ctypes.c_char_p
+    lib.ltx_attn_last_error.argtypes = []
+    lib.ltx_attn_last_error.restype = ctypes.c_char_p
+    lib.ltx_attn_provenance.argtypes = []
+    lib.ltx_attn_provenance.restype = ctypes.c_char_p
+    lib.ltx_attn_abi_version.argtypes = []
+    lib.ltx_attn_abi_version.restype = ctypes.c_int32
+    lib.ltx_attn_args_size.argtypes = []
+    lib.ltx_attn_args_size.restype = ctypes.c_size_t
+    if lib.ltx_attn_args_size() != ctypes.sizeof(Args):
+        raise RuntimeError(f"ltx_attn_args layout mismatch: library {lib.ltx_attn_args_size()} "
+                           f"bytes, binding {ctypes.sizeof(Args)} bytes")
+    lib.ltx_rope_frequency_grid.argtypes = [ctypes.c_double, ctypes.c_int32, ctypes.c_int32,
+                                            ctypes.c_void_p, ctypes.c_int32]
+    lib.ltx_rope_frequency_grid.restype = ctypes.c_int32
+    lib.ltx_rope_video_positions.argtypes = [ctypes.c_int32] * 5 + [
+        ctypes.c_double, ctypes.c_void_p, ctypes.c_int64]
+    lib.ltx_rope_video_positions.restype = ctypes.c_int32
+    lib.ltx_rope_audio_positions.argtypes = [ctypes.c_int32] * 4 + [ctypes.c_void_p,
+                                                                     ctypes.c_int64]
+    lib.ltx_rope_audio_positions.restype = ctypes.c_int32
+    lib.ltx_rope_tables.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                    ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
+                                    ctypes.c_double, ctypes.c_void_p, ctypes.c_void_p]
+    lib.ltx_rope_tables.restype = ctypes.c_int32
+    _lib = lib
+    return lib
+
+
+def provenance() -> str:
+    return load_library().ltx_attn_provenance().decode()
+
+
+# --------------------------------------------------------------------------------------
+# Errors (DiTAttention.Failure, DiTAttention.swift:107-121)
+# --------------------------------------------------------------------------------------
+
+class Failure(Exception):
+    """A status other than OK from the library, or a structural misuse caught here."""
+
+    def __init__(self, status: int, detail: str):
+        self.status = status
+        self.detail = detail
+        name = {EINVAL: "invalid argument", EUNSUPPORTED: "unsupported configuration",
+                EHIP: "HIP runtime error", EWORKSPACE: "workspace too small"}.get(status, "?")
+        super().__init__(f"{name}: {detail}")
+
+
+class RotaryWithoutPosition(Failure):
+    """``Failure.rotaryWithoutPosition`` (DiTAttention.swift:110, :118-119)."""
+
+    def __init__(self, variant: "Variant"):
+        super().__init__(EINVAL, f"{variant.value} takes no rotary embedding; supplying one "
+                                 "would rotate a stream that has no latent position")
+        self.variant = variant
+
+
+def _check(status: int) -> None:
+    if status != OK:
+        detail = load_library().ltx_attn_last_error().decode()
+        raise Failure(status, detail)
+
+
+# --------------------------------------------------------------------------------------
+# Variants and rotary pairs (DiTAttention.swift:69-105)
+# --------------------------------------------------------------------------------------
+
+class Variant(enum.Enum):
+    videoSelf = "attn1"
+    videoCross = "attn2"
+    audioSelf = "audio_attn1"
+    audioCross = "audio_attn2"
+    audioToVideo = "audio_to_video_attn"   # video queries over audio K/V
+    videoToAudio = "video_to_audio_attn"   # audio queries over video K/V
+
+    @property
+    def takes_rotary(self) -> bool:
+        """``attn2`` / ``audio_attn2`` are never rotated (DiTAttention.swift:84-89)."""
+        return self not in (Variant.videoCross, Variant.audioCross)
+
+
+@dataclass
+class Rotary:
+    """One ``(cos, sin)`` pair, each bf16 ``[H, L, D/2]`` on the device (the reference's
+    ``[1, H, L, D/2]`` with the batch axis dropped)."""
+
+    cos: "object"
+    sin: "object"
+
+
+# --------------------------------------------------------------------------------------
+# Core call
+# --------------------------------------------------------------------------------------
+
+def _strides_merged(t, heads):
+    """Element strides (bs, rs, hs) of a ``[B, L, H*D]`` tensor view."""
+    B, L, inner = t.shape
+    sb, sr, sc = t.stride()
+    if sc != 1:
+        raise Failure(EINVAL, "the channel axis must be contiguous")
+    return sb, sr, inner // heads
+
+
+def _strides_split(t):
+    """Element strides (bs, rs, hs) of a ``[B, H, L, D]`` tensor view."""
+    sb, sh, sr, sd = t.stride()
+    if sd != 1:
+        raise Failure(EINVAL, "the head-dim axis must be contiguous")
+    return sb, sr, sh
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
+                  k_norm_w=None, eps: float = 1e-6, rotary: Optional[Rotary] = None,
+                  key_rotary: Optional[Rotary] = None,
+                  k_valid_len: Optional[Sequence[int]] = None, scale: Optional[float] = None,
+                  out=None, kprep: int = KPREP_AUTO, num_splits: int = 0, stream=None,
+                  workspace=None, events=None):
+    """One call of ``ltx_attn_fwd``. Tensors are torch bf16 on the current HIP device.
+
+    ``layout="merged"``: q ``[B, Lq, H*D]``, k/v ``[B, Lk, H*D]``, out ``[B, Lq, H*D]``.
+    ``layout="split"``:  q ``[B, H, Lq, D]``, k/v ``[B, H, Lk, D]``, out ``[B, H, Lq, D]``.
+    Returns ``out``.
+    """
+    import torch
+
+    lib = load_library()
+    if layout == "merged":
+        B, Lq, inner = q.shape
+        Lk = k.shape[1]
+        D = inner // heads
+        qs, ks, vs = (_strides_merged(t, heads) for t in (q, k, v))
+        if out is None:
+            out = torch.empty((B, Lq, inner), dtype=q.dtype, device=q.device)
+        os_ = _strides_merged(out, heads)
+    elif layout == "split":
+        B, H, Lq, D = q.shape
+        if H != heads:
+            raise Failure(EINVAL, f"q has {H} heads, expected {heads}")
+        Lk = k.shape[2]
+        qs, ks, vs = (_strides_split(t) for t in (q, k, v))
+        if out is None:
+            out = torch.empty((B, heads, Lq, D), dtype=q.dtype, device=q.device)
+        os_ = _strides_split(out)
+    else:
+        raise ValueError(layout)
+    for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
+        if t.dtype != torch.bfloat16 or not t.is_cuda:
+            raise Failure(EINVAL, f"{name} must be a bf16 device tensor")
+
+    a = Args()
+    lib.ltx_attn_args_init(ctypes.byref(a))
+    a.B, a.H, a.Lq, a.Lk, a.D = B, heads, Lq, Lk, D
+    a.q, a.k, a.v = _ptr(q), _ptr(k), _ptr(v)
+    a.q_bs, a.q_rs, a.q_hs = qs
+    a.k_bs, a.k_rs, a.k_hs = ks
+    a.v_bs, a.v_rs, a.v_hs = vs
+    keep = []
+    if q_norm_w is not None:
+        a.q_norm_w = _ptr(q_norm_w)
+    if k_norm_w is not None:
+        a.k_norm_w = _ptr(k_norm_w)
+    a.norm_eps = eps
+    if rotary is not None:
+        a.q_cos, a.q_sin = _ptr(rotary.cos), _ptr(rotary.sin)
+    if key_rotary is not None:
+        a.k_cos, a.k_sin = _ptr(key_rotary.cos), _ptr(key_rotary.sin)
+    if k_valid_len is not None:
+        arr = (ctypes.c_int32 * B)(*[int(x) for x in k_valid_len])
+        keep.append(arr)
+        a.k_valid_len = ctypes.cast(arr, ctypes.POINTER(ctypes.c_int32))
+    a.scale = float(np.float32(1.0 / math.sqrt(D))) if scale is None else float(scale)
+    a.out = _ptr(out)
+    a.o_bs, a.o_rs, a.o_hs = os_
+    a.kprep = kprep
+    a.num_splits = num_splits
+    if events is not None:
+        a.ev_attn_start, a.ev_attn_stop = events
+    need = lib.ltx_attn_workspace_bytes(ctypes.byref(a))
+    st = lib.ltx_attn_validate(ctypes.byref(a))
+    if st not in (OK, EWORKSPACE):
+        _check(st)
+    if need:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need + 256, dtype=torch.uint8, device=q.device)
+        base = workspace.data_ptr()
+        a.workspace = ctypes.c_void_p((base + 255) // 256 * 256)
+        a.workspace_bytes = need
+    if stream is None:
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+    _check(lib.ltx_attn_fwd(ctypes.byref(a), ctypes.c_void_p(stream)))
+    # keep the workspace alive until the stream has consumed it
+    if need:
+        out._ltx_workspace = workspace  # noqa: SLF001 -- lifetime anchor
+    return out
+
+
+def workspace_bytes(**kw) -> int:
+    """Workspace the call with these shapes/options needs (host-only query)."""
+    lib = load_library()
+    a = Args()
+    lib.ltx_attn_args_init(ctypes.byref(a))
+    for k_, v_ in kw.items():
+        setattr(a, k_, v_)
+    return lib.ltx_attn_workspace_bytes(ctypes.byref(a))
+
+
+def scaled_dot_product_attention(queries, keys, values, scale: float, mask=None,
+                                 k_valid_len=None, **kw):
+    """``MLXFast.scaledDotProductAttention`` on ``[B, H, L, D]`` bf16 tensors.
+
+    ``mask`` must be None (the DiT path passes ``.none``, DiTAttention.swift:374-376); a
+    key-padding mask is given as ``k_valid_len`` (first n keys valid per batch row).
+    """
+    if mask is not None:
+        raise Failure(EUNSUPPORTED, "only mask=None or k_valid_len key padding is supported")
+    return attention_fwd(queries, keys, values, heads=queries.shape[1], layout="split",
+                         scale=scale, k_valid_len=k_valid_len, **kw)
+
+
+class DiTAttentionCore:
+    """The replaced unit of ``DiTAttention`` (``DiTAttention.swift:358-381``).
+
+    Takes the pre-norm projections ``q = to_q(x)``, ``k = to_k(context)``, ``v = to_v(context)``
+    in the merged ``[B, L, H*D]`` layout plus the ``q_norm`` / ``k_norm`` weights, and returns
+    the attention output in the merged layout (what the gate and ``to_out`` consume).
+    """
+
+    heads = 32            # DiTAttention.heads (:64)
+    norm_epsilon = 1e-6   # DiTAttention.normEpsilon (:66)
+
+    def __init__(self, q_norm_weight, k_norm_weight, heads: int = 32):
+        self.q_norm_weight = q_norm_weight
+        self.k_norm_weight = k_norm_weight
+        self.heads = heads
+
+    def __call__(self, q, k, v, *, variant: Variant, rotary: Optional[Rotary] = None,
+                 key_rotary: Optional[Rotary] = None, k_valid_len=None, **kw):
+        if rotary is not None and not variant.takes_rotary:
+            raise RotaryWithoutPosition(variant)
+        if key_rotary is not None and rotary is None:
+            raise Failure(EINVAL, "keyRotary without rotary")
+        inner = q.shape[-1]
+        if inner % self.heads:
+            raise Failure(EINVAL, f"inner dim {inner} is not a multiple of {self.heads} heads")
+        return attention_fwd(q, k, v, heads=self.heads, q_norm_w=self.q_norm_weight,
+                             k_norm_w=self.k_norm_weight, eps=self.norm_epsilon,
+                             rotary=rotary, key_rotary=key_rotary, k_valid_len=k_valid_len,
+                             **kw)
+
+
+# --------------------------------------------------------------------------------------
+# RoPE tables (host, through the C ABI)
+# --------------------------------------------------------------------------------------
+
+def rope_frequency_grid(theta: float, n_pos: int, inner: int) -> np.ndarray:
+    lib = load_library()
+    cap = max(1, inner // (2 * max(1, n_pos)))
+    out = np.zeros(cap, dtype=np.float32)
+    n = lib.ltx_rope_frequency_grid(theta, n_pos, inner, out.ctypes.data, cap)
+    if n < 0:
+        raise Failure(EINVAL, "bad frequency-grid arguments")
+    return out[:n]
+
+
+def rope_video_positions(latent_frames, latent_height, latent_width, temporal_scale=8,
+                         spatial_scale=32, frame_rate=24.0) -> np.ndarray:
+    lib = load_library()
+    tokens = latent_frames * latent_height * latent_width
+    out = np.zeros((3, tokens, 2), dtype=np.float32)
+    n = lib.ltx_rope_video_positions(latent_frames, latent_height, latent_width,
+                                     temporal_scale, spatial_scale, frame_rate,
+                                     out.ctypes.data, out.size)
+    if n < 0:
+        raise Failure(EINVAL, "bad video-position arguments")
+    return out
+
+
+def rope_audio_positions(tokens, hop_length=160, sample_rate=16000, downsample=4) -> np.ndarray:
+    lib = load_library()
+    out = np.zeros((1, tokens, 2), dtype=np.float32)
+    n = lib.ltx_rope_audio_positions(tokens, hop_length, sample_rate, downsample,
+                                     out.ctypes.data, out.size)
+    if n < 0:
+        raise Failure(EINVAL, "bad audio-position arguments")
+    return out
+
+
+def rope_tables(positions: np.ndarray, inner: int, max_pos, heads: int = 32,
+                theta: float = 10000.0):
+    """bf16 bit patterns ``(cos, sin)``, each ``[heads, tokens, inner/2/heads]`` uint16."""
+    lib = load_library()
+    positions = np.ascontiguousarray(positions, dtype=np.float32)
+    n_pos, tokens = positions.shape[0], positions.shape[1]
+    mp = np.ascontiguousarray(max_pos, dtype=np.int32)
+    per_head = inner // 2 // heads
+    cos = np.zeros((heads, tokens, per_head), dtype=np.uint16)
+    sin = np.zeros_like(cos)
+    rc = lib.ltx_rope_tables(positions.ctypes.data, n_pos, tokens, inner, mp.ctypes.data,
+                             heads, theta, cos.ctypes.data, sin.ctypes.data)
+    if rc != 0:
+        raise Failure(EINVAL, "bad rotary-table arguments")
+    return cos, sin
+
+
+def rotaries(frames: int, height: int, width: int, frame_rate: float = 24.0,
+             video_width: int = 4096, audio_width: int = 2048, heads: int = 32,
+             theta: float = 10000.0, audio_tokens: Optional[int] = None):
+    """The four tables of ``DiTForward.rotaries(geometry:dtype:)`` (DiTForward.swift:698-738)
+    as numpy bf16 bit patterns, keyed ``videoSelf``, ``audioSelf``, ``videoCross``,
+    ``audioCross``."""
+    lf = 1 if frames <= 1 else (frames - 1) // 8 + 1
+    video = rope_video_positions(lf, height // 32, width // 32, 8, 32, frame_rate)
+    if audio_tokens is None:
+        audio_tokens = int(round(frames / frame_rate * 25.0))
+    audio = rope_audio_positions(audio_tokens)
+    return {
+        "videoSelf": rope_tables(video, video_width, [20, 2048, 2048], heads, theta),
+        "audioSelf": rope_tables(audio, audio_width, [20], heads, theta),
+        "videoCross": rope_tables(video[0:1], audio_width, [20], heads, theta),
+        "audioCross": rope_tables(audio, audio_width, [20], heads, theta),
+    }

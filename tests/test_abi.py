@@ -1,0 +1,221 @@
+"""The C-ABI boundary on the host: the library loads, exports every symbol include/ltx_attn.h
+declares, validates arguments before launching anything (so every error path is testable
+without a GPU), sizes its workspace, and builds the RoPE tables like the reference."""
+
+import ctypes
+import json
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import ltx_attn as L
+import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ltx_attn.h")
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ltx_(?:attn|rope)_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.load_library()
+    declared = _declared_functions()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(L.EXPORTED_SYMBOLS)
+    nm = subprocess.run(["nm", "-D", "--defined-only", L.LIB_PATH], capture_output=True,
+                        text=True, check=True).stdout
+    for name in declared:
+        assert re.search(rf"\bT {name}\b", nm), name
+
+
+def test_struct_layout_and_version():
+    lib = L.load_library()
+    assert lib.ltx_attn_args_size() == ctypes.sizeof(L.Args)
+    assert lib.ltx_attn_abi_version() == 1
+    assert "gfx950" in L.provenance()
+    for s in range(5):
+        assert lib.ltx_attn_status_string(s)
+
+
+# ---------------------------------------------------------------------------------------
+# Validation: host-only, nothing is dereferenced on the device.
+# ---------------------------------------------------------------------------------------
+
+FAKE = 0x7F0000000000   # 256-byte aligned fake device address (never dereferenced)
+
+
+def _args(B=1, H=32, Lq=3120, Lk=3120, D=128, **kw):
+    a = L.Args()
+    L.load_library().ltx_attn_args_init(ctypes.byref(a))
+    a.B, a.H, a.Lq, a.Lk, a.D = B, H, Lq, Lk, D
+    inner = H * D
+    a.q, a.k, a.v, a.out = FAKE, FAKE + (1 << 32), FAKE + (2 << 32), FAKE + (3 << 32)
+    a.q_bs, a.q_rs, a.q_hs = Lq * inner, inner, D
+    a.k_bs, a.k_rs, a.k_hs = Lk * inner, inner, D
+    a.v_bs, a.v_rs, a.v_hs = Lk * inner, inner, D
+    a.o_bs, a.o_rs, a.o_hs = Lq * inner, inner, D
+    a.scale = 1.0 / np.sqrt(D)
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _validate(a):
+    lib = L.load_library()
+    st = lib.ltx_attn_validate(ctypes.byref(a))
+    return st, lib.ltx_attn_last_error().decode()
+
+
+def test_valid_arguments_pass():
+    st, msg = _validate(_args())
+    assert st == L.OK, msg
+
+
+@pytest.mark.parametrize("field,value,status", [
+    ("D", 96, L.EUNSUPPORTED),
+    ("D", 80, L.EUNSUPPORTED),
+    ("B", 0, L.EINVAL),
+    ("Lk", 0, L.EINVAL),
+    ("q", FAKE + 8, L.EINVAL),          # misaligned
+    ("v", 0, L.EINVAL),                 # NULL
+    ("k_rs", 4100, L.EINVAL),           # not a multiple of 8
+    ("q_hs", 64, L.EINVAL),             # heads overlap
+    ("scale", 0.0, L.EINVAL),
+    ("scale", float("nan"), L.EINVAL),
+    ("kprep", 7, L.EINVAL),
+    ("num_splits", 17, L.EINVAL),
+])
+def test_invalid_arguments_are_rejected(field, value, status):
+    a = _args()
+    setattr(a, field, value)
+    st, msg = _validate(a)
+    assert st == status, msg
+    assert msg
+
+
+def test_rotary_rules():
+    # k tables without q tables: keyRotary without rotary
+    st, msg = _validate(_args(k_cos=FAKE, k_sin=FAKE))
+    assert st == L.EINVAL and "keyRotary" in msg
+    # only one of a pair
+    st, _ = _validate(_args(q_cos=FAKE))
+    assert st == L.EINVAL
+    # K reuses Q's tables but the streams differ in length (cross-modal without k_pe)
+    st, msg = _validate(_args(Lq=3120, Lk=126, D=64, H=32, q_cos=FAKE, q_sin=FAKE))
+    assert st == L.EINVAL and "Lq" in msg
+    st, msg = _validate(_args(Lq=3120, Lk=126, D=64, H=32, q_cos=FAKE, q_sin=FAKE,
+                              k_cos=FAKE, k_sin=FAKE))
+    assert st == L.EWORKSPACE, msg      # arguments fine; the K prologue needs scratch
+
+
+def test_key_padding_rules():
+    lens = (ctypes.c_int32 * 2)(94, 0)
+    a = _args(B=2, Lk=1024)
+    a.k_valid_len = ctypes.cast(lens, ctypes.POINTER(ctypes.c_int32))
+    st, msg = _validate(a)
+    assert st == L.EINVAL and "k_valid_len[1]" in msg     # empty mask
+    lens[1] = 1025
+    st, _ = _validate(a)
+    assert st == L.EINVAL
+    lens[1] = 1
+    st, msg = _validate(a)
+    assert st == L.OK, msg
+    big = (ctypes.c_int32 * 65)(*([5] * 65))
+    a = _args(B=65, Lk=16, Lq=16)
+    a.k_valid_len = ctypes.cast(big, ctypes.POINTER(ctypes.c_int32))
+    assert _validate(a)[0] == L.EUNSUPPORTED
+
+
+def test_workspace_sizing_and_check():
+    lib = L.load_library()
+    # plain attention, enough work to fill the chip: no workspace
+    a = _args()
+    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == 0
+    # 12480-token self-attention with norm + RoPE: q statistic + prepared K
+    a = _args(Lq=12480, Lk=12480, q_norm_w=FAKE, k_norm_w=FAKE, q_cos=FAKE, q_sin=FAKE)
+    need = lib.ltx_attn_workspace_bytes(ctypes.byref(a))
+    rstd = (12480 * 4 + 255) // 256 * 256
+    kprep = (12480 * 4096 * 2 + 255) // 256 * 256
+    assert need == rstd + kprep
+    st, msg = _validate(a)
+    assert st == L.EWORKSPACE and str(need) in msg
+    a.workspace, a.workspace_bytes = FAKE, need - 1
+    assert _validate(a)[0] == L.EWORKSPACE
+    a.workspace_bytes = need
+    assert _validate(a)[0] == L.OK
+    a.workspace = FAKE + 16
+    assert _validate(a)[0] == L.EINVAL      # 256-byte alignment
+    # fused K strategy: only the statistics
+    a = _args(Lq=12480, Lk=12480, q_norm_w=FAKE, k_norm_w=FAKE, q_cos=FAKE, q_sin=FAKE,
+              kprep=L.KPREP_FUSED)
+    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == 2 * rstd
+    # 126 audio queries over 3120 video keys (49 key tiles): split-KV partials; 8 requested
+    # splits become 7 splits of 7 tiles (no split is left empty)
+    a = _args(Lq=126, Lk=3120, D=64, num_splits=8)
+    need = lib.ltx_attn_workspace_bytes(ctypes.byref(a))
+    rows = 7 * 32 * 126
+    assert need == (rows * 64 * 4 + 255) // 256 * 256 + (rows * 2 * 4 + 255) // 256 * 256
+
+
+def test_zero_work_needs_no_gpu():
+    """Validation failures return before any HIP call: this runs on a GPU-less host."""
+    lib = L.load_library()
+    a = _args(D=96)
+    assert lib.ltx_attn_fwd(ctypes.byref(a), None) == L.EUNSUPPORTED
+
+
+# ---------------------------------------------------------------------------------------
+# RoPE tables built by the library (host code) vs the oracle and the reference digests
+# ---------------------------------------------------------------------------------------
+
+def test_frequency_grid_and_positions_bit_exact():
+    for n_pos, inner in ((3, 4096), (1, 2048), (1, 4096)):
+        np.testing.assert_array_equal(L.rope_frequency_grid(10000.0, n_pos, inner),
+                                      O.frequency_grid(10000.0, n_pos, inner))
+    np.testing.assert_array_equal(L.rope_video_positions(4, 6, 10)[None],
+                                  O.video_positions(4, 6, 10))
+    np.testing.assert_array_equal(L.rope_video_positions(13, 24, 40)[None],
+                                  O.video_positions(13, 24, 40))
+    np.testing.assert_array_equal(L.rope_audio_positions(126)[None], O.audio_positions(126))
+
+
+def test_rope_tables_match_oracle():
+    lib_t = L.rotaries(25, 192, 320)
+    ora_t = O.rotaries(25, 192, 320)
+    for name in lib_t:
+        for a, b in zip(lib_t[name], ora_t[name]):
+            assert a.shape == b.shape
+            same = np.mean(a == b)
+            diff = np.max(np.abs(a.astype(np.int32) - b.astype(np.int32)))
+            assert same > 0.999 and diff <= 1, (name, same, diff)
+
+
+def test_rope_tables_match_reference_digests():
+    with open(os.path.join(GOLDEN, "tiny_v5_rope_digests.json")) as fh:
+        dig = json.load(fh)
+    tabs = L.rotaries(25, 192, 320)
+    for table, tap, tol in (("videoSelf", "block_00.attn1.in.kw_pe", 1e-9),
+                            ("videoCross", "block_00.audio_to_video_attn.in.kw_pe", 1e-9),
+                            ("audioSelf", "block_00.audio_attn1.in.kw_pe", 2e-6),
+                            ("audioCross", "block_00.video_to_audio_attn.in.kw_pe", 2e-6)):
+        for bits, key in zip(tabs[table], (tap, tap + ".el1")):
+            x = O.bf16_bits_to_f32(bits).astype(np.float64)
+            assert abs(x.mean() - dig[key]["mean"]) < tol, key
+            assert abs(x.std(ddof=1) - dig[key]["std"]) < tol, key
+
+
+def test_rope_builders_reject_bad_arguments():
+    with pytest.raises(L.Failure):
+        L.rope_frequency_grid(10000.0, 3, 4)      # one-element grid
+    with pytest.raises(L.Failure):
+        L.rope_tables(np.zeros((1, 4, 2), np.float32), 2048, [0], 32)   # maxPos 0

@@ -1,0 +1,386 @@
+"""GPU parity: the HIP library, called through its C ABI, against the CPU oracle.
+
+Tolerance (stated by the target): on the bf16 outputs, relative RMS error <= 5e-3 and
+max-abs error <= 2e-2 against the fp32/float64 oracle of the same seeded inputs. Each check
+also asserts that the kernel is no further from the truth than the reference's own rounding
+points put the reference (``mode="reference"`` of the oracle), plus a small slack.
+"""
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import ltx_attn as L
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+REL_RMS = 5e-3
+MAX_ABS = 2e-2
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def dev(bits, device):
+    import torch
+
+    t = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(device)
+    return t.view(torch.bfloat16)
+
+
+def host_bits(t):
+    import torch
+
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def host_f32(t):
+    return O.bf16_bits_to_f32(host_bits(t))
+
+
+def check(got, truth, ref_out=None, label=""):
+    c = O.compare(got, truth)
+    _say(f"  {label}: relRMS {c['rel_rms']:.3e} maxAbs {c['max_abs']:.3e}")
+    assert c["rel_rms"] <= REL_RMS, (label, c)
+    assert c["max_abs"] <= MAX_ABS, (label, c)
+    if ref_out is not None:
+        r = O.compare(ref_out, truth)
+        _say(f"  {label}: reference arithmetic relRMS {r['rel_rms']:.3e}")
+        assert c["rel_rms"] <= max(r["rel_rms"], 2.5e-3) * 1.25, (label, c, r)
+    return c
+
+
+def run(device, q, k, v, heads, **kw):
+    """numpy bf16 bits in, numpy fp32 (bf16 values) out, merged layout."""
+    import torch
+
+    tq, tk, tv = dev(q, device), dev(k, device), dev(v, device)
+    extra = {}
+    for name in ("q_norm_w", "k_norm_w"):
+        if kw.get(name) is not None:
+            extra[name] = dev(kw.pop(name), device)
+        else:
+            kw.pop(name, None)
+    qc, qs, kc, ks = (kw.pop(n, None) for n in ("q_cos", "q_sin", "k_cos", "k_sin"))
+    if qc is not None:
+        extra["rotary"] = L.Rotary(dev(qc, device), dev(qs, device))
+    if kc is not None:
+        extra["key_rotary"] = L.Rotary(dev(kc, device), dev(ks, device))
+    out = L.attention_fwd(tq, tk, tv, heads=heads, **extra, **kw)
+    torch.cuda.synchronize()
+    return host_f32(out)
+
+
+# ---------------------------------------------------------------------------------------
+# The reference's own attention test, through MLXFast's signature
+# ---------------------------------------------------------------------------------------
+
+def test_mlx_capability_uniform_case(device):
+    """MLXCapabilityTests.fusedAttention (Tests/LTXModulesTests/MLXCapabilityTests.swift:78-91)."""
+    import torch
+
+    heads, tokens, head_dim = 4, 16, 64
+    q = torch.ones((1, heads, tokens, head_dim), dtype=torch.bfloat16, device=device)
+    k = torch.ones_like(q)
+    v = torch.ones_like(q) * 2.0
+    out = L.scaled_dot_product_attention(q, k, v, scale=1.0 / math.sqrt(head_dim))
+    torch.cuda.synchronize()
+    assert list(out.shape) == [1, heads, tokens, head_dim]
+    assert abs(out[0, 0, 0, 0].item() - 2.0) < 1e-4
+    assert torch.all((out.float() - 2.0).abs() < 1e-4)
+
+
+# ---------------------------------------------------------------------------------------
+# Committed golden vectors
+# ---------------------------------------------------------------------------------------
+
+def _fixtures():
+    data = np.load(os.path.join(GOLDEN, "fixtures.npz"), allow_pickle=False)
+    names = sorted({k.split("/")[0] for k in data.files})
+    return data, names
+
+
+@pytest.mark.parametrize("name", _fixtures()[1])
+def test_golden_fixture(device, name):
+    data, _ = _fixtures()
+    g = {k.split("/", 1)[1]: data[k] for k in data.files if k.startswith(name + "/")}
+    meta = json.loads(str(g["meta"]))
+    _say(f"golden {name} {meta}")
+    kw = {key: g[key] for key in ("q_norm_w", "k_norm_w", "q_cos", "q_sin", "k_cos", "k_sin")
+          if key in g}
+    if "valid_len" in g:
+        kw["k_valid_len"] = list(g["valid_len"])
+    for kprep in (L.KPREP_FUSED, L.KPREP_PROLOGUE):
+        got = run(device, g["q"], g["k"], g["v"], meta["heads"], kprep=kprep, **dict(kw))
+        check(got, g["out_exact"], O.bf16_bits_to_f32(g["out_ref_bf16"]),
+              f"{name} kprep={kprep}")
+
+
+# ---------------------------------------------------------------------------------------
+# Edge shapes, small enough for the float64 oracle
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("B,H,Lq,Lk,D,valid", [
+    (1, 2, 1, 1, 64, None),
+    (1, 2, 7, 5, 128, None),
+    (2, 3, 65, 63, 64, None),
+    (1, 2, 257, 129, 128, None),
+    (2, 2, 300, 200, 128, [200, 1]),
+    (2, 2, 100, 1024, 64, [94, 1]),
+    (3, 1, 33, 100, 128, [64, 65, 100]),
+])
+def test_edge_shapes(device, B, H, Lq, Lk, D, valid):
+    _say(f"edge B={B} H={H} Lq={Lq} Lk={Lk} D={D} valid={valid}")
+    seed = B * 1000 + Lq * 7 + Lk
+    q = O.randn_bf16_bits((B, Lq, H * D), seed)
+    k = O.randn_bf16_bits((B, Lk, H * D), seed + 1)
+    v = O.randn_bf16_bits((B, Lk, H * D), seed + 2)
+    truth = O.attention(q, k, v, H, valid_len=valid, mode="exact")
+    got = run(device, q, k, v, H, k_valid_len=valid)
+    check(got, truth, None, "edge")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("splits", [1, 2, 3, 16])
+def test_split_kv_matches(device, D, splits):
+    """Short query stream over a long key stream (the audio-queries case), forced splits."""
+    B, H, Lq, Lk = 1, 4, 126, 1500
+    _say(f"split D={D} splits={splits}")
+    q = O.randn_bf16_bits((B, Lq, H * D), 11)
+    k = O.randn_bf16_bits((B, Lk, H * D), 12)
+    v = O.randn_bf16_bits((B, Lk, H * D), 13)
+    truth = O.attention(q, k, v, H, mode="exact")
+    got = run(device, q, k, v, H, num_splits=splits)
+    check(got, truth, None, f"splits={splits}")
+
+
+def test_split_kv_ragged_rows_with_empty_splits(device):
+    """Batch rows with very different valid lengths: later splits of the short row are empty."""
+    B, H, Lq, Lk, D = 2, 2, 40, 1024, 64
+    q = O.randn_bf16_bits((B, Lq, H * D), 21)
+    k = O.randn_bf16_bits((B, Lk, H * D), 22)
+    v = O.randn_bf16_bits((B, Lk, H * D), 23)
+    valid = [1000, 3]
+    truth = O.attention(q, k, v, H, valid_len=valid, mode="exact")
+    got = run(device, q, k, v, H, k_valid_len=valid, num_splits=8)
+    check(got, truth, None, "ragged split")
+
+
+def test_rebase_path_large_logits(device):
+    """Logits that grow along the key axis force the running max to be rebased."""
+    B, H, Lq, Lk, D = 1, 2, 64, 640, 64
+    rng = np.random.default_rng(5)
+    qf = rng.standard_normal((B, Lq, H * D)).astype(np.float32) * 3.0
+    kf = rng.standard_normal((B, Lk, H * D)).astype(np.float32)
+    kf *= (1.0 + np.arange(Lk, dtype=np.float32) / 40.0)[None, :, None]
+    q, k = O.f32_to_bf16_bits(qf), O.f32_to_bf16_bits(kf)
+    v = O.randn_bf16_bits((B, Lk, H * D), 6)
+    truth = O.attention(q, k, v, H, mode="exact")
+    got = run(device, q, k, v, H)
+    check(got, truth, None, "rebase")
+
+
+def test_split_layout_and_strided_output(device):
+    import torch
+
+    B, H, Lq, Lk, D = 2, 4, 96, 80, 128
+    q = O.randn_bf16_bits((B, H, Lq, D), 31)
+    k = O.randn_bf16_bits((B, H, Lk, D), 32)
+    v = O.randn_bf16_bits((B, H, Lk, D), 33)
+    merged = lambda x: x.transpose(0, 2, 1, 3).reshape(B, x.shape[2], H * D)  # noqa: E731
+    truth = O.attention(merged(q), merged(k), merged(v), H, mode="exact")
+    tq, tk, tv = dev(q, device), dev(k, device), dev(v, device)
+    out = L.scaled_dot_product_attention(tq, tk, tv, scale=1.0 / math.sqrt(D))
+    torch.cuda.synchronize()
+    got = host_f32(out).transpose(0, 2, 1, 3).reshape(B, Lq, H * D)
+    check(got, truth, None, "split layout")
+    # merged output written into a wider row: the padding must stay untouched
+    big = torch.full((B, Lq, H * D + 64), 7.0, dtype=torch.bfloat16, device=device)
+    view = big[:, :, 32:32 + H * D]
+    L.attention_fwd(dev(merged(q), device), dev(merged(k), device), dev(merged(v), device),
+                    heads=H, out=view)
+    torch.cuda.synchronize()
+    assert torch.all(big[:, :, :32] == 7.0) and torch.all(big[:, :, 32 + H * D:] == 7.0)
+    check(host_f32(view.contiguous()), truth, None, "strided out")
+
+
+def test_deterministic(device):
+    B, H, L_, D = 1, 8, 700, 128
+    q = O.randn_bf16_bits((B, L_, H * D), 41)
+    k = O.randn_bf16_bits((B, L_, H * D), 42)
+    v = O.randn_bf16_bits((B, L_, H * D), 43)
+    a = run(device, q, k, v, H)
+    b = run(device, q, k, v, H)
+    assert np.array_equal(a, b)
+
+
+def test_dit_attention_core_rules(device):
+    """DiTAttentionCore mirrors DiTAttention: rotary on attn2/audio_attn2 is refused."""
+    import torch
+
+    w = torch.ones(4096, dtype=torch.bfloat16, device=device)
+    core = L.DiTAttentionCore(w, w)
+    x = torch.zeros((1, 8, 4096), dtype=torch.bfloat16, device=device)
+    tab = torch.zeros((32, 8, 64), dtype=torch.bfloat16, device=device)
+    with pytest.raises(L.RotaryWithoutPosition):
+        core(x, x, x, variant=L.Variant.videoCross, rotary=L.Rotary(tab, tab))
+    with pytest.raises(L.Failure):
+        core(x, x, x, variant=L.Variant.videoSelf, key_rotary=L.Rotary(tab, tab))
+
+
+# ---------------------------------------------------------------------------------------
+# The BASELINE shapes at full size; the oracle checks sampled heads and query ranges
+# ---------------------------------------------------------------------------------------
+
+def _gpu_bits(shape, seed, device, mean=0.0, std=1.0):
+    """Seeded N(mean, std) bf16 drawn on the GPU (fast at full size), plus its host bits."""
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    t = (torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std + mean)
+    t = t.to(torch.bfloat16)
+    return t, host_bits(t)
+
+
+def _index_rotary(indices, inner, heads):
+    """1-D temporal tables from integer positions (frame index / audio index), built with the
+    reference's rotary recipe (frequency grid, centre/maxPos, theta 1e4)."""
+    pos = np.zeros((1, 1, len(indices), 2), dtype=np.float32)
+    pos[0, 0, :, 0] = indices
+    pos[0, 0, :, 1] = indices
+    return O.rotary_tables(pos, inner, [20], heads)
+
+
+def _sample_check(device, tq, tk, tv, heads, bits, kw_host, kw_dev, ranges, hsel, label,
+                  **call_kw):
+    import torch
+
+    out = L.attention_fwd(tq, tk, tv, heads=heads, **kw_dev, **call_kw)
+    torch.cuda.synchronize()
+    got = host_f32(out)
+    B, Lq, inner = got.shape
+    D = inner // heads
+    qb, kb, vb = bits
+    for (q0, q1) in ranges:
+        for h in hsel:
+            truth = O.c_attention(qb, kb, vb, heads, mode="exact", heads_range=(h, h + 1),
+                                  q_range=(q0, q1), **kw_host)
+            refm = O.c_attention(qb, kb, vb, heads, mode="reference", heads_range=(h, h + 1),
+                                 q_range=(q0, q1), **kw_host)
+            g = got[:, q0:q1, h * D:(h + 1) * D].reshape(truth.shape)
+            check(g, truth, O.round_bf16(refm), f"{label} h={h} q=[{q0},{q1})")
+
+
+def test_c1_video_self_3120(device):
+    _say("c1 video self-attention [1,32,3120,128]")
+    shape = (1, 3120, 4096)
+    tq, qb = _gpu_bits(shape, 0x5EED, device)
+    tk, kb = _gpu_bits(shape, 0x5EED + 1, device)
+    tv, vb = _gpu_bits(shape, 0x5EED + 2, device)
+    _sample_check(device, tq, tk, tv, 32, (qb, kb, vb), {}, {}, [(0, 96), (3024, 3120)],
+                  [0, 31], "c1")
+
+
+@pytest.mark.parametrize("B,valid", [(1, [94]), (2, [94, 1])])
+def test_c2_text_cross_masked(device, B, valid):
+    _say(f"c2 text cross B={B} valid={valid}")
+    tq, qb = _gpu_bits((B, 3120, 4096), 0x5EED + 10, device)
+    tk, kb = _gpu_bits((B, 1024, 4096), 0x5EED + 11, device)
+    tv, vb = _gpu_bits((B, 1024, 4096), 0x5EED + 12, device)
+    _sample_check(device, tq, tk, tv, 32, (qb, kb, vb), {"valid_len": valid},
+                  {"k_valid_len": valid}, [(0, 64), (3056, 3120)], [0, 13], "c2")
+
+
+@pytest.mark.parametrize("direction", ["video_q", "audio_q"])
+def test_c3_cross_modal(device, direction):
+    _say(f"c3 cross-modal {direction}")
+    Tv, Ta, H, D = 3120, 126, 32, 64
+    vid_idx = np.arange(Tv) // (20 * 12)           # latent frame index 0..12
+    aud_idx = np.arange(Ta)                        # 0..125
+    vc, vs = _index_rotary(vid_idx, H * D, H)
+    ac, as_ = _index_rotary(aud_idx, H * D, H)
+    if direction == "video_q":
+        Lq, Lk, qt, kt = Tv, Ta, (vc, vs), (ac, as_)
+    else:
+        Lq, Lk, qt, kt = Ta, Tv, (ac, as_), (vc, vs)
+    tq, qb = _gpu_bits((1, Lq, H * D), 0x5EED + 20, device)
+    tk, kb = _gpu_bits((1, Lk, H * D), 0x5EED + 21, device)
+    tv, vb = _gpu_bits((1, Lk, H * D), 0x5EED + 22, device)
+    kw_host = dict(q_cos=qt[0], q_sin=qt[1], k_cos=kt[0], k_sin=kt[1])
+    kw_dev = dict(rotary=L.Rotary(dev(qt[0], device), dev(qt[1], device)),
+                  key_rotary=L.Rotary(dev(kt[0], device), dev(kt[1], device)))
+    ranges = [(0, 64), (Lq - 62, Lq)]
+    _sample_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, ranges, [0, 31],
+                  f"c3 {direction}")
+
+
+@pytest.mark.parametrize("kprep", [L.KPREP_PROLOGUE, L.KPREP_FUSED])
+def test_c4_stage2_self_12480_norm_rope(device, kprep):
+    _say(f"c4 12480 self-attention, norm + 3-D RoPE, kprep={kprep}")
+    H, D, T = 32, 128, 12480
+    tq, qb = _gpu_bits((1, T, H * D), 0x5EED + 30, device)
+    tk, kb = _gpu_bits((1, T, H * D), 0x5EED + 31, device)
+    tv, vb = _gpu_bits((1, T, H * D), 0x5EED + 32, device)
+    wq, wqb = _gpu_bits((H * D,), 0x5EED + 33, device, 1.0, 0.02)
+    wk, wkb = _gpu_bits((H * D,), 0x5EED + 34, device, 1.0, 0.02)
+    cos, sin = L.rope_tables(L.rope_video_positions(13, 24, 40), H * D, [20, 2048, 2048], H)
+    kw_host = dict(q_norm_w=wqb, k_norm_w=wkb, q_cos=cos, q_sin=sin)
+    kw_dev = dict(q_norm_w=wq, k_norm_w=wk, rotary=L.Rotary(dev(cos, device), dev(sin, device)))
+    _sample_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev,
+                  [(0, 64), (6200, 6264), (T - 64, T)], [0, 17, 31], "c4", kprep=kprep)
+
+
+def test_c5_block_set(device):
+    """One DiT block's six attentions at B=2 (15360 video, 152 audio, 1024 text with 94
+    valid), with norm + RoPE where the reference applies it (DiTBlock.swift:343-438)."""
+    import torch
+
+    H = 32
+    Tv, Ta, Tt = 15360, 152, 1024
+    vt = L.rotaries(121, 768, 1280, audio_tokens=Ta)
+    tabs = {k: (dev(c, device), dev(s, device)) for k, (c, s) in vt.items()}
+    streams = {}
+    for name, T, inner, seed in (("v", Tv, 4096, 50), ("a", Ta, 2048, 60),
+                                 ("t4096", Tt, 4096, 70), ("t2048", Tt, 2048, 80),
+                                 ("v2048", Tv, 2048, 90)):
+        streams[name] = _gpu_bits((2, T, inner), 0x5EED + seed, device)
+    w = {n: _gpu_bits((i,), 0x5EED + s, device, 1.0, 0.02)
+         for n, i, s in (("w4096", 4096, 100), ("w2048", 2048, 101))}
+    valid = [94, 94]
+    cases = [
+        # label, q stream, kv stream, D, norm, q table, k table, valid
+        ("attn1", "v", "v", 128, "w4096", "videoSelf", None, None),
+        ("audio_attn1", "a", "a", 64, "w2048", "audioSelf", None, None),
+        ("attn2", "v", "t4096", 128, "w4096", None, None, valid),
+        ("audio_attn2", "a", "t2048", 64, "w2048", None, None, valid),
+        ("audio_to_video", "v2048", "a", 64, "w2048", "videoCross", "audioCross", None),
+        ("video_to_audio", "a", "v2048", 64, "w2048", "audioCross", "videoCross", None),
+    ]
+    for label, qs, ks, D, wn, qtab, ktab, vl in cases:
+        _say(f"c5 {label}")
+        tq, qb = streams[qs]
+        tk, kb = streams[ks]
+        tv, vb = streams[ks]
+        kw_host = dict(q_norm_w=w[wn][1], k_norm_w=w[wn][1])
+        kw_dev = dict(q_norm_w=w[wn][0], k_norm_w=w[wn][0])
+        if qtab:
+            kw_host.update(q_cos=vt[qtab][0], q_sin=vt[qtab][1])
+            kw_dev["rotary"] = L.Rotary(*tabs[qtab])
+        if ktab:
+            kw_host.update(k_cos=vt[ktab][0], k_sin=vt[ktab][1])
+            kw_dev["key_rotary"] = L.Rotary(*tabs[ktab])
+        if vl:
+            kw_host["valid_len"] = vl
+            kw_dev["k_valid_len"] = vl
+        Lq = tq.shape[1]
+        ranges = [(0, min(64, Lq))] if Lq <= 256 else [(0, 64), (Lq - 64, Lq)]
+        _sample_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, ranges, [5],
+                      f"c5 {label}")
+        torch.cuda.synchronize()

@@ -1,0 +1,324 @@
+"""Pins the CPU oracle (oracle/oracle.py and oracle/attn_oracle.c) before anything is checked
+against it.
+
+Each check is chosen so that a plausible mistake fails it: a dropped term, a wrong sign or
+index, a transposed operand, a per-head instead of per-token norm, interleaved instead of
+split RoPE, tail instead of leading RoPE padding, a wrong mask convention. None of them
+re-types the oracle's own formula.
+"""
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _bits(x):
+    return O.f32_to_bf16_bits(np.asarray(x, dtype=np.float32))
+
+
+# ---------------------------------------------------------------------------------------
+# SDPA core
+# ---------------------------------------------------------------------------------------
+
+def test_mlx_capability_uniform_case():
+    """Tests/LTXModulesTests/MLXCapabilityTests.swift:78-91: ones Q/K, V = 2 -> 2.0 +- 1e-4,
+    [1, 4, 16, 64], scale 1/sqrt(64)."""
+    B, H, L, D = 1, 4, 16, 64
+    q = np.ones((B, L, H * D), np.float32)
+    v = np.full((B, L, H * D), 2.0, np.float32)
+    for mode in ("exact", "reference"):
+        out = O.attention(_bits(q), _bits(q), _bits(v), H, scale=1.0 / math.sqrt(D), mode=mode)
+        assert out.shape == (B, L, H * D)
+        assert abs(out[0, 0, 0] - 2.0) < 1e-4
+        assert np.all(np.abs(out - 2.0) < 1e-4)
+    c = O.c_attention(_bits(q), _bits(q), _bits(v), H, scale=1.0 / math.sqrt(D))
+    assert np.all(np.abs(c - 2.0) < 1e-4)
+
+
+def _python_sdpa(q, k, v, scale):
+    """Definition-level brute force with math.exp, lists only (tiny inputs)."""
+    out = []
+    for qi in q:
+        logits = [scale * sum(a * b for a, b in zip(qi, kj)) for kj in k]
+        mx = max(logits)
+        w = [math.exp(x - mx) for x in logits]
+        z = sum(w)
+        out.append([sum(w[j] * v[j][d] for j in range(len(k))) / z for d in range(len(v[0]))])
+    return out
+
+
+def test_sdpa_matches_python_brute_force():
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((1, 1, 3, 4))
+    k = rng.standard_normal((1, 1, 5, 4))
+    v = rng.standard_normal((1, 1, 5, 4))
+    got = O.sdpa(q, k, v, 0.37)[0, 0]
+    ref = _python_sdpa(q[0, 0].tolist(), k[0, 0].tolist(), v[0, 0].tolist(), 0.37)
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+    # a transposed K (q . k with k swapped axes) is caught
+    bad = O.sdpa(q, k[..., ::-1], v, 0.37)[0, 0]
+    assert np.max(np.abs(bad - np.asarray(ref))) > 1e-3
+
+
+def test_sdpa_closed_forms():
+    rng = np.random.default_rng(3)
+    q = rng.standard_normal((2, 3, 7, 8))
+    k = rng.standard_normal((2, 3, 9, 8))
+    v = rng.standard_normal((2, 3, 9, 8))
+    # Lk = 1 -> O = V
+    np.testing.assert_allclose(O.sdpa(q, k[:, :, :1], v[:, :, :1], 0.5),
+                               np.broadcast_to(v[:, :, :1], (2, 3, 7, 8)), atol=1e-12)
+    # equal keys -> O = mean(V)
+    keq = np.broadcast_to(k[:, :, :1], k.shape)
+    np.testing.assert_allclose(O.sdpa(q, keq, v, 0.5),
+                               np.broadcast_to(v.mean(axis=2, keepdims=True), q.shape),
+                               atol=1e-12)
+    # scale 0 -> mean(V)
+    np.testing.assert_allclose(O.sdpa(q, k, v, 0.0),
+                               np.broadcast_to(v.mean(axis=2, keepdims=True), q.shape),
+                               atol=1e-12)
+    # permuting keys together with values leaves O unchanged
+    perm = rng.permutation(9)
+    np.testing.assert_allclose(O.sdpa(q, k[:, :, perm], v[:, :, perm], 0.5),
+                               O.sdpa(q, k, v, 0.5), atol=1e-12)
+    # permuting keys alone changes it
+    assert np.max(np.abs(O.sdpa(q, k[:, :, perm], v, 0.5) - O.sdpa(q, k, v, 0.5))) > 1e-3
+    # rows of P sum to 1: V = ones -> O = ones
+    np.testing.assert_allclose(O.sdpa(q, k, np.ones_like(v), 0.5), np.ones(q.shape), atol=1e-12)
+
+
+def test_key_padding_equals_truncation():
+    """Masked SDPA over Lk keys with n valid == SDPA over K[:n], V[:n] (the additive
+    -bf16max convention of TextConditioningLayout.swift:94-107 with >= 1 valid key)."""
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((2, 2, 6, 8))
+    k = rng.standard_normal((2, 2, 10, 8))
+    v = rng.standard_normal((2, 2, 10, 8))
+    got = O.sdpa(q, k, v, 0.4, valid_len=[4, 1])
+    np.testing.assert_allclose(got[0], O.sdpa(q[:1], k[:1, :, :4], v[:1, :, :4], 0.4)[0])
+    # n = 1 -> O = V[0]
+    np.testing.assert_allclose(got[1], np.broadcast_to(v[1, :, :1], (2, 6, 8)), atol=1e-12)
+    # the additive -bf16max mask gives the same numbers
+    logits = np.einsum("hqd,hkd->hqk", q[0], k[0]) * 0.4
+    logits[:, :, 4:] += -O.BF16_MAX
+    p = np.exp(logits - logits.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    np.testing.assert_allclose(got[0], p @ v[0], atol=1e-12)
+    with pytest.raises(ValueError):
+        O.sdpa(q, k, v, 0.4, valid_len=[0, 3])
+
+
+def test_softmax_shift_invariance():
+    """Adding a per-row constant to the logits leaves O unchanged: q -> q + c*k_mean-free dir
+    is awkward, so shift via an extra key-independent term: equal-norm augmentation."""
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((1, 1, 4, 8))
+    k = rng.standard_normal((1, 1, 6, 8))
+    v = rng.standard_normal((1, 1, 6, 8))
+    # append a dimension where every key has the same value -> adds q_extra*c to each logit
+    q2 = np.concatenate([q, rng.standard_normal((1, 1, 4, 1)) * 5], -1)
+    k2 = np.concatenate([k, np.full((1, 1, 6, 1), 3.0)], -1)
+    v2 = v
+    np.testing.assert_allclose(O.sdpa(q2, k2, v2, 0.3), O.sdpa(q, k, v, 0.3), atol=1e-12)
+
+
+# ---------------------------------------------------------------------------------------
+# RMSNorm over the inner dim
+# ---------------------------------------------------------------------------------------
+
+def test_rms_norm_statistic_spans_all_heads():
+    rng = np.random.default_rng(2)
+    H, D = 4, 8
+    x = rng.standard_normal((3, H * D))
+    x[:, :D] *= 10.0                       # head 0 is much louder than the others
+    w = np.ones(H * D)
+    y = O.rms_norm(x, w, 1e-6, "exact")
+    # RMS over the whole row is 1 ...
+    np.testing.assert_allclose(np.sqrt(np.mean(y * y, axis=-1)), 1.0, rtol=1e-6)
+    # ... and the heads keep their relative loudness (a per-head norm would flatten it)
+    per_head = np.sqrt(np.mean(y.reshape(3, H, D) ** 2, axis=-1))
+    assert np.all(per_head[:, 0] > 3 * per_head[:, 1])
+    # scale invariance
+    np.testing.assert_allclose(O.rms_norm(7.5 * x, w, 0.0, "exact"),
+                               O.rms_norm(x, w, 0.0, "exact"), rtol=1e-12)
+    # the weight is per inner channel
+    w2 = np.arange(1, H * D + 1, dtype=np.float64)
+    np.testing.assert_allclose(O.rms_norm(x, w2, 1e-6, "exact"), y * w2, rtol=1e-12)
+
+
+def test_rms_norm_reference_mode_rounds_once_to_bf16():
+    rng = np.random.default_rng(4)
+    x = O.bf16_bits_to_f32(O.randn_bf16_bits((5, 256), 9))
+    w = O.bf16_bits_to_f32(O.randn_bf16_bits((256,), 10, 1.0, 0.02))
+    r = O.rms_norm(x, w, 1e-6, "reference")
+    assert np.all(O.round_bf16(r) == r)   # representable in bf16
+    e = O.rms_norm(x, w, 1e-6, "exact")
+    assert np.max(np.abs(r - e) / np.maximum(np.abs(e), 1e-3)) <= 2.0 ** -8
+
+
+# ---------------------------------------------------------------------------------------
+# Split RoPE apply
+# ---------------------------------------------------------------------------------------
+
+def test_split_rope_convention_and_invariants():
+    D = 8
+    x = np.arange(1, D + 1, dtype=np.float64).reshape(1, 1, 1, D)
+    ang = np.array([0.3, -1.1, 2.0, 0.7])
+    c, s = np.cos(ang).reshape(1, 1, 4), np.sin(ang).reshape(1, 1, 4)
+    y = O.split_rope(x, c, s, "exact")[0, 0, 0]
+    # hand-written: pairs are (d, d + D/2), not adjacent channels
+    x1, x2 = x[0, 0, 0, :4], x[0, 0, 0, 4:]
+    np.testing.assert_allclose(y[:4], x1 * np.cos(ang) - x2 * np.sin(ang))
+    np.testing.assert_allclose(y[4:], x2 * np.cos(ang) + x1 * np.sin(ang))
+    assert abs(y[0] - (1 * math.cos(0.3) - 5 * math.sin(0.3))) < 1e-12
+    # identity when cos = 1, sin = 0 (also what the video pad channels are)
+    np.testing.assert_allclose(O.split_rope(x, np.ones((1, 1, 4)), np.zeros((1, 1, 4))), x)
+    # per-pair norm preserved
+    np.testing.assert_allclose(y[:4] ** 2 + y[4:] ** 2, x1 ** 2 + x2 ** 2)
+
+
+def test_rope_relative_position_property():
+    """<R_m q, R_n k> depends only on m - n for a single 1-D frequency."""
+    rng = np.random.default_rng(8)
+    D = 16
+    q = rng.standard_normal(D)
+    k = rng.standard_normal(D)
+    f = rng.uniform(0.1, 2.0, D // 2)
+
+    def rot(x, pos):
+        a = f * pos
+        return O.split_rope(x.reshape(1, 1, 1, D), np.cos(a).reshape(1, 1, -1),
+                            np.sin(a).reshape(1, 1, -1))[0, 0, 0]
+
+    d1 = rot(q, 5.0) @ rot(k, 2.0)
+    d2 = rot(q, 13.0) @ rot(k, 10.0)
+    assert abs(d1 - d2) < 1e-10
+    assert abs(d1 - rot(q, 5.0) @ rot(k, 3.0)) > 1e-6
+
+
+# ---------------------------------------------------------------------------------------
+# RoPE tables against the reference's own digests (tiny_v5 manifest)
+# ---------------------------------------------------------------------------------------
+
+def _digests():
+    with open(os.path.join(GOLDEN, "tiny_v5_rope_digests.json")) as fh:
+        return json.load(fh)
+
+
+def _stats(bits):
+    x = O.bf16_bits_to_f32(bits).astype(np.float64)
+    return x.mean(), x.std(ddof=1), x.min(), x.max()   # torch.std is unbiased
+
+
+@pytest.mark.parametrize("table,tap,tol", [
+    ("videoSelf", "block_00.attn1.in.kw_pe", 1e-9),
+    ("videoCross", "block_00.audio_to_video_attn.in.kw_pe", 1e-9),
+    ("audioSelf", "block_00.audio_attn1.in.kw_pe", 2e-6),
+    ("audioCross", "block_00.video_to_audio_attn.in.kw_pe", 2e-6),
+])
+def test_rope_tables_match_reference_digests(table, tap, tol):
+    """320x192x25 @ 24 fps: 240 video / 26 audio tokens. The reference reports its video
+    tables bit-exact against upstream and the audio grid as needing a tolerance
+    (docs/FRAGILE_CONTRACTS.md, the rotary paragraph); the same split holds here."""
+    dig = _digests()
+    tabs = O.rotaries(25, 192, 320, 24.0)
+    cos, sin = tabs[table]
+    for bits, key in ((cos, tap), (sin, tap + ".el1")):
+        d = dig[key]
+        assert list(bits.shape) == d["shape"][1:]
+        mean, std, mn, mx = _stats(bits)
+        assert abs(mean - d["mean"]) < tol, (key, mean, d["mean"])
+        assert abs(std - d["std"]) < tol, (key, std, d["std"])
+        assert mn == d["min"] and mx == d["max"]
+
+
+def test_rope_table_structure():
+    # frequency grid: first pi/2, last theta*pi/2 exactly (endpoint overwritten)
+    f = O.frequency_grid(10000.0, 3, 4096)
+    assert f.size == 682
+    assert f[0] == np.float32(math.pi / 2) and f[-1] == np.float32(10000.0 * math.pi / 2)
+    # video: 2 leading identity channels (3*682 = 2046 < 2048), in head 0 only
+    cos, sin = O.rotaries(25, 192, 320)["videoSelf"]
+    c0 = O.bf16_bits_to_f32(cos[0])
+    s0 = O.bf16_bits_to_f32(sin[0])
+    assert np.all(c0[:, :2] == 1.0) and np.all(s0[:, :2] == 0.0)
+    assert not np.all(c0[:, 2] == 1.0)
+    assert not np.all(O.bf16_bits_to_f32(cos[31])[:, -2:] == 1.0)
+    # audio token bounds: [0, 0.01) then [0.01, 0.05) (DiTForward.swift:600-602)
+    a = O.audio_positions(3)
+    np.testing.assert_allclose(a[0, 0, 0], [0.0, 0.01], rtol=1e-6)
+    np.testing.assert_allclose(a[0, 0, 1], [0.01, 0.05], rtol=1e-6)
+    # video: first token's time bounds are [0, 1) pixel frames / fps
+    v = O.video_positions(2, 1, 2)
+    np.testing.assert_allclose(v[0, 0, 0], [0.0, np.float32(1.0) / np.float32(24.0)])
+    np.testing.assert_allclose(v[0, 0, 2], [np.float32(1.0) / np.float32(24.0),
+                                            np.float32(9.0) / np.float32(24.0)])
+    np.testing.assert_allclose(v[0, 2, 1], [32.0, 64.0])   # x fastest, pixels
+
+
+# ---------------------------------------------------------------------------------------
+# The C restatement against the float64 restatement
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("mode", ["exact", "reference"])
+def test_c_oracle_matches_numpy_oracle(mode):
+    B, H, Lq, Lk, D = 2, 4, 70, 90, 64
+    q = O.randn_bf16_bits((B, Lq, H * D), 1)
+    k = O.randn_bf16_bits((B, Lk, H * D), 2)
+    v = O.randn_bf16_bits((B, Lk, H * D), 3)
+    wq = O.randn_bf16_bits((H * D,), 4, 1.0, 0.02)
+    wk = O.randn_bf16_bits((H * D,), 5, 1.0, 0.02)
+    cq, sq = O.rotary_tables(O.audio_positions(Lq), H * D, [20], H)
+    ck, sk = O.rotary_tables(O.audio_positions(Lk), H * D, [20], H)
+    kw = dict(q_norm_w=wq, k_norm_w=wk, q_cos=cq, q_sin=sq, k_cos=ck, k_sin=sk,
+              valid_len=[90, 33], mode=mode)
+    ref = O.attention(q, k, v, H, **kw)
+    got = O.c_attention(q, k, v, H, **kw).reshape(B, Lq, H * D)
+    cmp = O.compare(got, ref)
+    assert cmp["rel_rms"] < 2e-6 and cmp["max_abs"] < 1e-5
+    # head / query subsets agree with the full call
+    sub = O.c_attention(q, k, v, H, heads_range=(1, 3), q_range=(10, 40), **kw)
+    np.testing.assert_allclose(sub, got.reshape(B, Lq, H, D)[:, 10:40, 1:3], atol=1e-6)
+
+
+def test_reference_rounding_points_change_the_result():
+    """The reference's bf16 roundings (after the norm, after each RoPE op) are visible: the
+    two modes differ by more than fp32 noise but stay within a few bf16 ulps."""
+    B, H, L, D = 1, 2, 40, 64
+    q = O.randn_bf16_bits((B, L, H * D), 21)
+    k = O.randn_bf16_bits((B, L, H * D), 22)
+    v = O.randn_bf16_bits((B, L, H * D), 23)
+    w = O.randn_bf16_bits((H * D,), 24, 1.0, 0.02)
+    cq, sq = O.rotary_tables(O.audio_positions(L), H * D, [20], H)
+    kw = dict(q_norm_w=w, k_norm_w=w, q_cos=cq, q_sin=sq)
+    e = O.attention(q, k, v, H, mode="exact", **kw)
+    r = O.attention(q, k, v, H, mode="reference", **kw)
+    rel = O.compare(r, e)["rel_rms"]
+    assert 1e-4 < rel < 1e-2
+
+
+def test_golden_fixtures_reproduce():
+    """The committed golden vectors are reproduced by the oracle (regression pin)."""
+    path = os.path.join(GOLDEN, "fixtures.npz")
+    data = np.load(path, allow_pickle=False)
+    names = sorted({k.split("/")[0] for k in data.files})
+    assert names, "no fixtures"
+    for name in names:
+        g = {k.split("/", 1)[1]: data[k] for k in data.files if k.startswith(name + "/")}
+        meta = json.loads(str(g["meta"]))
+        kw = {}
+        for key in ("q_norm_w", "k_norm_w", "q_cos", "q_sin", "k_cos", "k_sin"):
+            if key in g:
+                kw[key] = g[key]
+        if "valid_len" in g:
+            kw["valid_len"] = g["valid_len"]
+        out = O.attention(g["q"], g["k"], g["v"], meta["heads"], mode="exact", **kw)
+        np.testing.assert_allclose(out.astype(np.float32), g["out_exact"], rtol=0, atol=1e-6,
+                                   err_msg=name)
