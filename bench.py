@@ -242,17 +242,20 @@ def cpu_baseline(x, budget_s):
     wq, wk = _host_bits(x["wq"]), _host_bits(x["wk"])
     kw = dict(q_norm_w=wq, k_norm_w=wk, q_cos=x["cos"], q_sin=x["sin"], mode="reference",
               threads=threads)
-    # calibrate on 64 queries of one head, then size the sample to the budget
-    t0 = time.perf_counter()
-    O.c_attention(qb, kb, vb, H, heads_range=(0, 1), q_range=(0, 64), **kw)
-    t_cal = time.perf_counter() - t0
-    per_row = t_cal / 64.0
-    rows_total = max(64, int(budget_s / max(per_row, 1e-9)))
-    nh = max(1, min(H, rows_total // T))
-    nq = T if rows_total >= T else max(64, rows_total)
-    t0 = time.perf_counter()
-    O.c_attention(qb, kb, vb, H, heads_range=(0, nh), q_range=(0, nq), **kw)
-    dt = time.perf_counter() - t0
+    # calibrate on two sample sizes (the K preparation is a fixed cost per call), then size
+    # the sample to the budget
+    def timed(nh_, nq_):
+        t0 = time.perf_counter()
+        O.c_attention(qb, kb, vb, H, heads_range=(0, nh_), q_range=(0, nq_), **kw)
+        return time.perf_counter() - t0
+
+    t_small = timed(1, 256)
+    t_big = timed(1, 1280)
+    per_row = max((t_big - t_small) / 1024.0, 1e-7)     # one query row of one head
+    rows = max(1280, int((budget_s - t_small) / per_row))
+    nh = max(1, min(H, rows // T))
+    nq = T if rows >= T else rows
+    dt = timed(nh, nq)
     flops = 4.0 * nq * T * nh * D
     cpu = "unknown"
     try:

@@ -30,6 +30,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "fmha_params.hpp"
 
 namespace ltx {
@@ -144,7 +146,7 @@ void fmha_fwd_kernel(const FmhaParams p) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 31;
     const int g = lane >> 5;
 
@@ -225,11 +227,11 @@ void fmha_fwd_kernel(const FmhaParams p) {
         }
     }
 
-    // ---- staging of one key tile (global -> registers -> LDS) -------------------------
+    // ---- staging (global -> registers -> LDS); K runs one tile ahead of V --------------
     // Buffer loads: the resource of tile t starts at key t*KT and ends at the last valid
     // key, so rows past it read as zero without a branch.
     const int64_t krow_bytes = p.k_rs * 2, vrow_bytes = p.v_rs * 2;
-    auto tile_rsrc = [&](const bf16 *base, int64_t row_elems, int tile) {
+    auto tile_rsrc = [&](const bf16 *base, int64_t row_elems, int tile) __attribute__((always_inline)) {
         const int rows = min(KT, n_valid - tile * KT);
         return make_rsrc(base + (int64_t)tile * KT * row_elems, (int64_t)rows * row_elems * 2);
     };
@@ -248,7 +250,7 @@ void fmha_fwd_kernel(const FmhaParams p) {
     const int vkg = tid & 15;
     const int vdc = tid >> 4;
 
-    auto stage_load = [&](int tile) {
+    auto load_k = [&](int tile) __attribute__((always_inline)) {
         const rsrc_t rk = tile_rsrc(Kb, p.k_rs, tile);
         if (!KFUSED) {
             const int c = tid % T::KCPR;
@@ -273,6 +275,8 @@ void fmha_fwd_kernel(const FmhaParams p) {
                 }
             }
         }
+    };
+    auto load_v = [&](int tile) __attribute__((always_inline)) {
         if (vthr) {
             const rsrc_t rv = tile_rsrc(Vb, p.v_rs, tile);
 #pragma unroll
@@ -280,10 +284,8 @@ void fmha_fwd_kernel(const FmhaParams p) {
                 vreg[i] = bload16(rv, (uint32_t)((4 * vkg + i) * vrow_bytes + 16 * vdc));
         }
     };
-
-    auto stage_store = [&](int buf) {
-        bf16 *Ks = smem + buf * T::STAGE;
-        bf16 *Vt = Ks + T::K_ELEMS;
+    auto store_k = [&](int tile) __attribute__((always_inline)) {
+        bf16 *Ks = smem + (tile & 1) * T::STAGE;
         if (!KFUSED) {
             const int c = tid % T::KCPR;
 #pragma unroll
@@ -321,6 +323,9 @@ void fmha_fwd_kernel(const FmhaParams p) {
                 *(u32x4 *)(Ks + row * KS + D / 2 + 8 * c) = pack8(x2);
             }
         }
+    };
+    auto store_v = [&](int tile) __attribute__((always_inline)) {
+        bf16 *Vt = smem + (tile & 1) * T::STAGE + T::K_ELEMS;
         if (vthr) {
             const int pos = vt_pos(4 * vkg);
 #pragma unroll
@@ -347,114 +352,208 @@ void fmha_fwd_kernel(const FmhaParams p) {
     float m[2] = {0.f, 0.f};   // running max (log2 units), identical in lanes l and l^32
     float l[2] = {0.f, 0.f};   // this lane's share of the row sum
     f32x16 negm[2] = {splat16(0.f), splat16(0.f)};
-    bool started = false;      // wave-uniform: a running max exists
 
-    // One 32-key half of a tile: S^T block, softmax, and its share of O^T.
-    auto compute_half = [&](const bf16 *Ks, const bf16 *Vt, int kb, int key0, bool masked) {
-        f32x16 s[2];
-        s[0] = started ? negm[0] : splat16(0.f);
-        s[1] = started ? negm[1] : splat16(0.f);
+    // Software pipeline over 32-key blocks. Block s covers keys [32s, 32s+32) of tile s/2.
+    // Step s issues S(s+1) = K.Q'^T - m and O += V^T.P(s-1) on the matrix cores while the
+    // VALU turns S(s) into P(s). K of tile t is read by steps 2t-1 and 2t, V of tile t by
+    // steps 2t+1 and 2t+2, so the window of steps {2t-1, 2t} (opened by one barrier) reads
+    // only K(t) and V(t-1) and writes K(t+1) and V(t) into the other halves of the double
+    // buffer.
+    const int blk_begin = 2 * t_begin;
+    const int blk_end = min(2 * t_end, (n_valid + 31) / 32);
+    const bool ragged = (n_valid & 31) != 0;   // block blk_end-1 is partly padding
+    f32x16 sc[2];            // S(s), waiting for the softmax
+    bf16x8 pp[2][2];         // P(s-1) [qb][half], waiting for P.V
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        sc[qb] = splat16(0.f);
+        pp[qb][0] = pp[qb][1] = __builtin_bit_cast(bf16x8, u32x4{0, 0, 0, 0});
+    }
+
+    auto qk_block = [&](int s, f32x16 (&sn)[2]) __attribute__((always_inline)) {
+        const bf16 *Ks = smem + ((s >> 1) & 1) * T::STAGE;
+        const int kb = s & 1;
+        sn[0] = negm[0];
+        sn[1] = negm[1];
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const bf16x8 a = *(const bf16x8 *)(Ks + (kb * 32 + r) * KS + 16 * c + 8 * g);
-            s[0] = mfma32(a, qf[0][c], s[0]);
-            s[1] = mfma32(a, qf[1][c], s[1]);
+            sn[0] = mfma32(a, qf[0][c], sn[0]);
+            sn[1] = mfma32(a, qf[1][c], sn[1]);
         }
-        if (masked) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int key = key0 + 8 * (i >> 2) + 4 * g + (i & 3);
-                if (key >= n_valid) s[0][i] = s[1][i] = -INFINITY;
-            }
-        }
-        if (!started) {
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                float mx = s[qb][0];
-#pragma unroll
-                for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[qb][i]);
-                mx = fmaxf(mx, xlane32(mx));
-                m[qb] = mx;
-                negm[qb] = splat16(-mx);
-                s[qb] -= splat16(mx);
-            }
-            started = true;
-        }
-        bf16x8 pb[2][2];   // [qb][half]
-        float ts[2];
-        const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
-        // At most two passes: the second only after a rebase, whose p are all <= 1.
-        for (int pass = 0; pass < 2; ++pass) {
-            ts[0] = ts[1] = 0.f;
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-                for (int hf = 0; hf < 2; ++hf) {
-                    float pv[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) pv[e] = __builtin_amdgcn_exp2f(s[qb][8 * hf + e]);
-                    const u32x4 w = pack8(pv);
-                    pb[qb][hf] = __builtin_bit_cast(bf16x8, w);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        ts[qb] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[e]),
-                                                                 ones, ts[qb], false);
-                }
-            const bool bad = !(ts[0] <= kRebaseBound) || !(ts[1] <= kRebaseBound);
-            if (!__any(bad)) break;
-            // A later block outgrew the running max: rebase to this block's max (exact).
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                float mx = s[qb][0];
-#pragma unroll
-                for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[qb][i]);
-                mx = fmaxf(mx, xlane32(mx));
-                const float d = mx > 0.f ? mx : 0.f;
-                const float f = __builtin_amdgcn_exp2f(-d);
-                m[qb] += d;
-                negm[qb] = splat16(-m[qb]);
-                l[qb] *= f;
-#pragma unroll
-                for (int db = 0; db < NDB; ++db) o[db][qb] *= splat16(f);
-                s[qb] -= splat16(d);
-            }
-        }
-        l[0] += ts[0];
-        l[1] += ts[1];
+    };
+    auto pv_block = [&](int s) __attribute__((always_inline)) {
+        const bf16 *Vt = smem + ((s >> 1) & 1) * T::STAGE + T::K_ELEMS;
+        const int kb = s & 1;
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
             const int t4 = 2 * kb + hf;
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
                 const bf16x8 a = *(const bf16x8 *)(Vt + (db * 32 + r) * VS + 16 * t4 + 8 * g);
-                o[db][0] = mfma32(a, pb[0][hf], o[db][0]);
-                o[db][1] = mfma32(a, pb[1][hf], o[db][1]);
+                o[db][0] = mfma32(a, pp[0][hf], o[db][0]);
+                o[db][1] = mfma32(a, pp[1][hf], o[db][1]);
+            }
+        }
+    };
+    // S(s) -> P(s) (bf16) and this lane's row-sum share ts.
+    auto softmax_block = [&](const f32x16 (&sx)[2], bf16x8 (&pn)[2][2], float (&ts)[2])
+        __attribute__((always_inline)) {
+        const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
+        ts[0] = ts[1] = 0.f;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                u32x4 w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bf16x2 pr = {(bf16)__builtin_amdgcn_exp2f(sx[qb][8 * hf + 2 * e]),
+                                       (bf16)__builtin_amdgcn_exp2f(sx[qb][8 * hf + 2 * e + 1])};
+                    // The row sum adds exactly the bf16 weights that feed P.V. (Each pair is
+                    // consumed as its own value: extracting it back out of the packed vector
+                    // has been miscompiled into a reuse of the first pair.)
+                    ts[qb] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ts[qb], false);
+                    w[e] = __builtin_bit_cast(uint32_t, pr);
+                }
+                pn[qb][hf] = __builtin_bit_cast(bf16x8, w);
+            }
+    };
+
+    // One pipeline step. GEN: first/last blocks, ragged padding and the pipeline's fill and
+    // drain; otherwise every part is present and the step is straight-line code.
+    // A block whose bf16 row sum exceeds 2^64 (or is not finite) has outgrown the running max;
+    // the step only records it, and the workgroup then recomputes its rows with the safe pass
+    // below, so the pipelined region carries no rescaling code.
+    bool overflow = false;    // wave-uniform
+    auto step = [&](auto gen, int s) __attribute__((always_inline)) {
+        constexpr bool GEN = decltype(gen)::value;
+        const bool do_sm = !GEN || (s >= blk_begin && s < blk_end);
+        const bool do_s = !GEN || (s + 1 >= blk_begin && s + 1 < blk_end);
+        const bool do_pv = !GEN || (s - 1 >= blk_begin && s - 1 < blk_end);
+        if (GEN && do_sm) {
+            if (ragged && s == blk_end - 1) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = 32 * s + 8 * (i >> 2) + 4 * g + (i & 3);
+                    if (key >= n_valid) sc[0][i] = sc[1][i] = -INFINITY;
+                }
+            }
+            if (s == blk_begin) {
+                // The first block of the range sets the running max.
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb) {
+                    float mx = sc[qb][0];
+#pragma unroll
+                    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sc[qb][i]);
+                    mx = fmaxf(mx, xlane32(mx));
+                    m[qb] = mx;
+                    negm[qb] = splat16(-mx);
+                    sc[qb] -= splat16(mx);
+                }
+            }
+        }
+        f32x16 sn[2];
+        if (do_s) qk_block(s + 1, sn);
+        if (do_pv) pv_block(s - 1);
+        bf16x8 pn[2][2];
+        if (do_sm) {
+            float ts[2];
+            softmax_block(sc, pn, ts);
+            overflow |= !(ts[0] <= kRebaseBound) || !(ts[1] <= kRebaseBound);
+            l[0] += ts[0];
+            l[1] += ts[1];
+        }
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            if (!GEN || do_s) sc[qb] = sn[qb];
+            if (!GEN || do_sm) {
+                pp[qb][0] = pn[qb][0];
+                pp[qb][1] = pn[qb][1];
             }
         }
     };
 
-    // ---- main loop ----------------------------------------------------------------------
+    // ---- main loop: one barrier per 64-key tile ---------------------------------------
+    // Window t = steps {2t-1, 2t}; it loads K(t+1) and V(t) and stores them after computing.
     if (t_begin < t_end) {
-        stage_load(t_begin);
-        stage_store(0);
+        load_k(t_begin);
+        store_k(t_begin);
+    }
+    const int t_last = t_begin < t_end ? t_end : t_begin - 1;
+    // Windows [t_begin, tf0) and [tf1, t_last] fill and drain the pipeline (and carry the first
+    // block, the ragged block and the split edges); the windows in between are straight-line.
+    int tf0 = max(t_begin, (blk_begin + 3) / 2);        // first t with 2t-2 >= blk_begin
+    int tf1 = max(tf0, blk_end / 2);                     // first t with 2t+1 >= blk_end
+    tf0 = min(tf0, t_last + 1);
+    tf1 = min(tf1, t_last + 1);
+    auto window = [&](auto gen, int t) __attribute__((always_inline)) {
+        __syncthreads();
+        const bool nk = t + 1 < t_end, nv = t < t_end;
+        if (nk) load_k(t + 1);
+        if (nv) load_v(t);
+        if (active) {
+            step(gen, 2 * t - 1);
+            step(gen, 2 * t);
+        }
+        if (nk) store_k(t + 1);
+        if (nv) store_v(t);
+    };
+    for (int t = t_begin; t < tf0; ++t) window(std::true_type{}, t);
+    for (int t = tf0; t < tf1; ++t) window(std::false_type{}, t);
+    for (int t = tf1; t <= t_last; ++t) window(std::true_type{}, t);
+
+    // ---- safe pass: only when some wave's running max was outgrown -------------------
+    // Tile by tile, K and V of one tile in LDS, each 32-key block rebasing O and l as soon
+    // as its weights would exceed 2^64. Pathological inputs only.
+    if (__syncthreads_or(overflow)) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) o[db][0] = o[db][1] = splat16(0.f);
+        m[0] = m[1] = l[0] = l[1] = 0.f;
+        negm[0] = negm[1] = splat16(0.f);
+        for (int t = t_begin; t < t_end; ++t) {
+            __syncthreads();
+            load_k(t);
+            load_v(t);
+            store_k(t);
+            store_v(t);
+            __syncthreads();
+            if (!active) continue;
+            for (int kb = 0; kb < 2; ++kb) {
+                const int s = 2 * t + kb;
+                if (s >= blk_end) break;
+                f32x16 sx[2];
+                qk_block(s, sx);           // negm is 0 until the first block sets the max
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = 32 * s + 8 * (i >> 2) + 4 * g + (i & 3);
+                    if (key >= n_valid) sx[0][i] = sx[1][i] = -INFINITY;
+                }
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb) {
+                    float mx = sx[qb][0];
+#pragma unroll
+                    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sx[qb][i]);
+                    mx = fmaxf(mx, xlane32(mx));
+                    // first block: take its max; later blocks: move up when it is exceeded
+                    const float d = (s == blk_begin) ? mx : (mx > 0.f ? mx : 0.f);
+                    const float f = (s == blk_begin) ? 1.0f : __builtin_amdgcn_exp2f(-d);
+                    m[qb] += d;
+                    negm[qb] = splat16(-m[qb]);
+                    l[qb] *= f;
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) o[db][qb] *= splat16(f);
+                    sx[qb] -= splat16(d);
+                }
+                float ts[2];
+                softmax_block(sx, pp, ts);
+                l[0] += ts[0];
+                l[1] += ts[1];
+                pv_block(s);
+            }
+        }
     }
     __syncthreads();
-    for (int t = t_begin; t < t_end; ++t) {
-        const int buf = (t - t_begin) & 1;
-        const bool has_next = t + 1 < t_end;
-        if (has_next) stage_load(t + 1);
-        if (active) {
-            const bf16 *Ks = smem + buf * T::STAGE;
-            const bf16 *Vt = Ks + T::K_ELEMS;
-            const int key0 = t * KT;
-            // Keys past n_valid are zero-filled in LDS and masked here; a half with no valid
-            // key is skipped outright.
-            compute_half(Ks, Vt, 0, key0, key0 + 32 > n_valid);
-            if (key0 + 32 < n_valid) compute_half(Ks, Vt, 1, key0 + 32, key0 + KT > n_valid);
-        }
-        if (has_next) stage_store(buf ^ 1);
-        __syncthreads();
-    }
 
     // ---- epilogue ---------------------------------------------------------------------
     float lt[2];
