@@ -219,3 +219,17 @@ def test_rope_builders_reject_bad_arguments():
         L.rope_frequency_grid(10000.0, 3, 4)      # one-element grid
     with pytest.raises(L.Failure):
         L.rope_tables(np.zeros((1, 4, 2), np.float32), 2048, [0], 32)   # maxPos 0
+
+
+def test_cpp_host_mirror_error_behaviour(tmp_path):
+    """The C++ DiTAttention mirror (ltx-2.5-swift_amd/host/dit_attention.hpp) throws the
+    reference's structural failures before anything reaches a device."""
+    src = os.path.join(ROOT, "tests", "cpp", "test_dit_attention.cpp")
+    exe = str(tmp_path / "test_dit_attention")
+    libdir = os.path.dirname(L.LIB_PATH)
+    subprocess.run(["g++", "-std=c++17", "-O1", src, "-o", exe, f"-L{libdir}", "-lltx_attn",
+                    f"-Wl,-rpath,{libdir}", "-L/opt/rocm/lib", "-Wl,-rpath-link,/opt/rocm/lib"],
+                   check=True, capture_output=True)
+    run = subprocess.run([exe], capture_output=True, text=True)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert "0 failure(s)" in run.stdout
