@@ -281,6 +281,9 @@ def main():
                     help="seconds of CPU work for the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB, --steps times "
+                         "(the known-size kernel that scales FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -298,6 +301,17 @@ def main():
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     hip = HipEvents()
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "launches": args.steps}), flush=True)
+        return
 
     x, c4 = bench_c4(device, args.steps, args.warmup, hip)
     print(f"# c4: {c4['ms_per_step']:.3f} ms/step, attention kernel {c4['kernel_ms']:.3f} ms "
@@ -328,7 +342,7 @@ def main():
     achieved = c4["kernel_tflops"]
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                "traffic": traffic, "kernel": "fmha_fwd_kernel<128,false>",
+                "traffic": traffic, "kernel": "fmha_dma_kernel<128>",
                 "kernel_avg_ms": round(c4["kernel_ms"], 4),
                 "flops_per_launch": c4["flops"]}
     cpu = None

@@ -1,0 +1,169 @@
+// Device-side helpers shared by the attention kernels (fmha_fwd.hip, fmha_dma.hip): bf16
+// packing, raw buffer resources, the gfx950 MFMA wrapper and the Q prologue that every
+// attention kernel applies in registers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "fmha_params.hpp"
+
+namespace ltx {
+namespace {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int KT = kKeyTile;
+constexpr int QW = kQueriesPerWave;
+constexpr int NW = kWavesPerGroup;
+constexpr int QT = kQueriesPerGroup;
+constexpr int NT = NW * 64;                 // threads per workgroup
+constexpr float kRebaseBound = 1.8446744e19f;  // 2^64: largest p a block may produce
+
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
+    bf16x2 v = {(bf16)a, (bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ void unpack8(const u32x4 w, float f[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = bf_lo(w[i]);
+        f[2 * i + 1] = bf_hi(w[i]);
+    }
+}
+
+__device__ __forceinline__ u32x4 pack8(const float f[8]) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = pack_bf2(f[2 * i], f[2 * i + 1]);
+    return w;
+}
+
+__device__ __forceinline__ u32x4 ldg16(const void *p) { return *(const u32x4 *)p; }
+
+// Raw buffer resource over [base, base + bytes): loads past the end return zero.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;   // 32-bit data format, no swizzle (gfx9 family)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
+    const int n = bytes <= 0 ? 0 : (bytes >= 0x7fffffff ? 0x7fffffff : (int)bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, kRsrcWord3);
+}
+
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ f32x16 splat16(float x) {
+    f32x16 v;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = x;
+    return v;
+}
+
+__device__ __forceinline__ float xlane32(float x) { return __shfl_xor(x, 32, 64); }
+
+// Position of key k (0..63) inside a 64-key row of V^T: bits 2 and 3 swapped. A lane's B
+// operand of O^T = V^T.P^T holds keys {16h + 4g + 0..3, 16h + 8 + 4g + 0..3} of the S
+// registers; with this order they are the 8 contiguous positions 16h + 8g + 0..7.
+__device__ __forceinline__ int vt_pos(int k) {
+    return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Q of one wave (64 queries from q0) as MFMA B operands: load, RMS-normalise with the
+// prologue's statistic and q_norm.weight (DiTAttention.swift:202-204), rotate (split-half
+// RoPE, :226-237), multiply by scale*log2(e) in fp32, round to bf16 once. Lane (r, g) holds
+// query 32*qb + r, channels 16c + 8g .. +7 in qf[qb][c]. Rows past Lq read as zero.
+template <int D>
+__device__ __forceinline__ void load_q(const FmhaParams &p, int b, int h, int q0, bool active,
+                                       int r, int g, bf16x8 (&qf)[2][D / 16]) {
+    constexpr int NC = D / 16;
+    const bf16 *Qb = (const bf16 *)p.q + (int64_t)b * p.q_bs + (int64_t)h * p.q_hs;
+    const int nq = max(0, min(QW, p.Lq - q0));   // valid queries of this wave
+    const rsrc_t rq = make_rsrc(Qb + (int64_t)(active ? q0 : 0) * p.q_rs,
+                                (int64_t)nq * p.q_rs * 2);
+    float wq[NC][8];
+    if (p.q_rstd) {
+        const bf16 *w = (const bf16 *)p.q_w + h * D;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) unpack8(ldg16(w + 16 * c + 8 * g), wq[c]);
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const int qi = 32 * qb + r;               // query within the wave
+        const int qc = min(q0 + qi, p.Lq - 1);     // clamped index for side tables
+        float x[NC][8];
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            unpack8(bload16(rq, (uint32_t)(qi * p.q_rs * 2 + (16 * c + 8 * g) * 2)), x[c]);
+        if (p.q_rstd) {
+            const float rs = p.q_rstd[(int64_t)b * p.Lq + qc];
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[c][e] = (x[c][e] * rs) * wq[c][e];
+        }
+        if (p.q_cos) {
+            const int64_t toff = ((int64_t)h * p.Lq + qc) * (D / 2);
+            const bf16 *cs = (const bf16 *)p.q_cos + toff;
+            const bf16 *sn = (const bf16 *)p.q_sin + toff;
+#pragma unroll
+            for (int c = 0; c < NC / 2; ++c) {
+                float fc[8], fs[8];
+                unpack8(ldg16(cs + 16 * c + 8 * g), fc);
+                unpack8(ldg16(sn + 16 * c + 8 * g), fs);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float x1 = x[c][e], x2 = x[c + NC / 2][e];
+                    x[c][e] = x1 * fc[e] - x2 * fs[e];
+                    x[c + NC / 2][e] = x2 * fc[e] + x1 * fs[e];
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[c][e] *= p.qk_scale_log2;
+            qf[qb][c] = __builtin_bit_cast(bf16x8, pack8(x[c]));
+        }
+    }
+}
+
+// Work item of a workgroup: consecutive items of one XCD (workgroup ids are dealt to the 8
+// XCDs round-robin) so that the query blocks sharing one (batch, head, split) share an L2.
+struct WorkItem {
+    int qblk, split, h, b;
+};
+
+__device__ __forceinline__ WorkItem work_item(const FmhaParams &p) {
+    const int N = p.total_groups;
+    const int bid = blockIdx.x;
+    const int xcd = bid & 7;
+    const int item = xcd * (N >> 3) + min(xcd, N & 7) + (bid >> 3);
+    WorkItem w;
+    w.qblk = item % p.nqblk;
+    int rest = item / p.nqblk;
+    w.split = rest % p.num_splits;
+    rest /= p.num_splits;
+    w.h = rest % p.H;
+    w.b = rest / p.H;
+    return w;
+}
+
+}  // namespace
+}  // namespace ltx

@@ -1,0 +1,519 @@
+// Attention kernel with K and V^T tiles copied HBM -> LDS by the buffer-load-to-LDS path
+// (gfx950 `buffer_load_dwordx4 ... lds`), for calls whose K was prepared by the prologue (or
+// needs no preparation) -- every call with two or more query blocks per (batch, head).
+//
+// Same arithmetic as fmha_fwd.hip's register-staged kernel (MFMA mapping, exp2 softmax with
+// the -m accumulator start, 2^64 overflow bound and safe pass, bf16 row sums); what changes
+// is the staging:
+//   * V is transposed once per call by vt_prep_kernel into V^T [B][H][D][ld] with keys in
+//     vt_pos order, so a V^T tile row is 128 contiguous bytes and each MFMA A operand of
+//     O^T = V^T.P^T is one 16-byte LDS read (as for K).
+//   * Each wave copies its share of the next K and V^T tiles straight into LDS; no staging
+//     registers, no LDS stores, no transposition in the loop. The 16-byte units of each LDS
+//     row are XOR-swizzled (swz) so the operand reads are free of bank conflicts; a lane
+//     fetches the global unit that belongs at the LDS position the copy writes it to.
+//   * The two K and two V^T buffers are four distinct LDS objects and the steady-state
+//     windows are unrolled by parity, so the compiler sees that the copies in flight never
+//     alias the operand reads and does not wait for them before reading.
+#include <type_traits>
+
+#include "fmha_device.hpp"
+
+namespace ltx {
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <int D>
+struct DmaTile {
+    static constexpr int NC = D / 16;                // 16-wide reduction chunks of Q.K^T
+    static constexpr int NDB = D / 32;               // 32-row blocks of O^T
+    static constexpr int KU = D / 8;                 // 16-byte units per K row
+    static constexpr int VU = KT / 8;                // 16-byte units per V^T row
+    static constexpr int ELEMS = KT * D;             // a K tile, a V^T tile, one wave's O
+    static constexpr int K_DMA = KT * KU / 64 / NW;  // copies (64 units each) per wave per tile
+    static constexpr int V_DMA = D * VU / 64 / NW;
+    static_assert(K_DMA >= 1 && V_DMA >= 1 && QW * D == ELEMS, "tile geometry");
+};
+
+// Unit swizzle for gfx950's LDS (64 four-byte banks; a 16-byte access is serviced 16 lanes
+// at a time): 16 consecutive rows reading the same logical unit hit 16 distinct bank groups.
+// Rows of 16 units span all banks (XOR with row & 15); rows of 8 units pair up per bank
+// window (XOR with (row >> 1) & 7). XOR makes the map its own inverse.
+template <int UNITS>
+__device__ __forceinline__ int swz(int row, int u) {
+    static_assert(UNITS == 16 || UNITS == 8, "row width");
+    return UNITS == 16 ? (u ^ (row & 15)) : (u ^ ((row >> 1) & 7));
+}
+
+// s_waitcnt vmcnt(0), expcnt and lgkmcnt left at their maxima: this wave's copies landed.
+__device__ __forceinline__ void wait_copies() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+template <int D>
+__global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(1, 1)))
+void fmha_dma_kernel(const FmhaParams p) {
+    using T = DmaTile<D>;
+    constexpr int NC = T::NC, NDB = T::NDB, KU = T::KU, VU = T::VU;
+    __shared__ __attribute__((aligned(16))) bf16 sK0[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) bf16 sK1[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) bf16 sV0[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) bf16 sV1[T::ELEMS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 31;
+    const int g = lane >> 5;
+
+    const WorkItem wi = work_item(p);
+    const int qblk = wi.qblk, split = wi.split, h = wi.h, b = wi.b;
+    const int n_valid = p.valid[b];
+    const int ntiles = (n_valid + KT - 1) / KT;
+    const int t_begin = split * p.tiles_per_split;
+    const int t_end = min(t_begin + p.tiles_per_split, ntiles);
+    const int q0 = qblk * QT + wave * QW;
+    const bool active = q0 < p.Lq;
+
+    bf16x8 qf[2][NC];
+    load_q<D>(p, b, h, q0, active, r, g, qf);
+
+    // ---- copies HBM -> LDS -----------------------------------------------------------
+    const bf16 *Kb = (const bf16 *)p.k + (int64_t)b * p.k_bs + (int64_t)h * p.k_hs;
+    const int64_t krow_bytes = p.k_rs * 2;
+    const int64_t vrow_bytes = p.vt_ld * 2;
+    const rsrc_t rvt = make_rsrc((const bf16 *)p.vt + ((int64_t)b * p.H + h) * D * p.vt_ld,
+                                 (int64_t)D * vrow_bytes);
+    // K tile t: keys [64t, 64t+64); the resource ends at the last valid key so the rows past
+    // it arrive as zeros.
+    auto copy_k = [&](int tile, bf16 *dst) __attribute__((always_inline)) {
+        const int rows = min(KT, n_valid - tile * KT);
+        const rsrc_t rk = make_rsrc(Kb + (int64_t)tile * KT * p.k_rs, (int64_t)rows * krow_bytes);
+#pragma unroll
+        for (int j = 0; j < T::K_DMA; ++j) {
+            const int blk = wave * T::K_DMA + j;
+            const int q = blk * 64 + lane;
+            const int row = q / KU, u = swz<KU>(row, q % KU);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(dst + blk * 512), 16,
+                                                     (int)(row * krow_bytes + 16 * u), 0, 0, 0);
+        }
+    };
+    // V^T tile t: D rows of key positions [64t, 64t+64) (zero past the valid keys).
+    auto copy_v = [&](int tile, bf16 *dst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < T::V_DMA; ++j) {
+            const int blk = wave * T::V_DMA + j;
+            const int q = blk * 64 + lane;
+            const int row = q / VU, u = swz<VU>(row, q % VU);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rvt, (lds_void *)(dst + blk * 512), 16,
+                (int)(row * vrow_bytes + tile * KT * 2 + 16 * u), 0, 0, 0);
+        }
+    };
+    // Operand reads: K rows kb*32 + r, unit 2c + g; V^T rows db*32 + r, unit 2*t4 + g.
+    auto k_opnd = [&](const bf16 *Ks, int kb, int c) __attribute__((always_inline)) {
+        const int row = kb * 32 + r;
+        return *(const bf16x8 *)(Ks + row * D + 8 * swz<KU>(row, 2 * c + g));
+    };
+    auto v_opnd = [&](const bf16 *Vs, int t4, int db) __attribute__((always_inline)) {
+        const int row = db * 32 + r;
+        return *(const bf16x8 *)(Vs + row * KT + 8 * swz<VU>(row, 2 * t4 + g));
+    };
+
+    // ---- running state ----------------------------------------------------------------
+    f32x16 o[NDB][2];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) o[db][0] = o[db][1] = splat16(0.f);
+    float m[2] = {0.f, 0.f};   // running max (log2 units), identical in lanes l and l^32
+    float l[2] = {0.f, 0.f};   // this lane's share of the row sum
+    f32x16 negm[2] = {splat16(0.f), splat16(0.f)};
+
+    // Software pipeline over 32-key blocks (block s = keys [32s, 32s+32) of tile s/2):
+    // step s issues S(s+1) = K.Q'^T - m and O += V^T.P(s-1) on the matrix cores while the
+    // VALU turns S(s) into P(s). Window t = steps {2t-1, 2t} reads K(t) and V(t-1) and copies
+    // K(t+1) and V(t) into the other buffers; one barrier per window.
+    const int blk_begin = 2 * t_begin;
+    const int blk_end = min(2 * t_end, (n_valid + 31) / 32);
+    const bool ragged = (n_valid & 31) != 0;   // block blk_end-1 is partly padding
+    f32x16 sc[2];            // S(s), waiting for the softmax
+    bf16x8 pp[2][2];         // P(s-1) [qb][half], waiting for P.V
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        sc[qb] = splat16(0.f);
+        pp[qb][0] = pp[qb][1] = __builtin_bit_cast(bf16x8, u32x4{0, 0, 0, 0});
+    }
+
+    auto qk_block = [&](const bf16 *Ks, int kb, f32x16 (&sn)[2]) __attribute__((always_inline)) {
+        sn[0] = negm[0];
+        sn[1] = negm[1];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const bf16x8 a = k_opnd(Ks, kb, c);
+            sn[0] = mfma32(a, qf[0][c], sn[0]);
+            sn[1] = mfma32(a, qf[1][c], sn[1]);
+        }
+    };
+    auto pv_block = [&](const bf16 *Vs, int kb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const bf16x8 a = v_opnd(Vs, 2 * kb + hf, db);
+                o[db][0] = mfma32(a, pp[0][hf], o[db][0]);
+                o[db][1] = mfma32(a, pp[1][hf], o[db][1]);
+            }
+    };
+    // S(s) -> P(s) (bf16) and this lane's row-sum share ts.
+    auto softmax_block = [&](const f32x16 (&sx)[2], bf16x8 (&pn)[2][2], float (&ts)[2])
+        __attribute__((always_inline)) {
+        const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
+        ts[0] = ts[1] = 0.f;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                u32x4 w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bf16x2 pr = {(bf16)__builtin_amdgcn_exp2f(sx[qb][8 * hf + 2 * e]),
+                                       (bf16)__builtin_amdgcn_exp2f(sx[qb][8 * hf + 2 * e + 1])};
+                    // Each pair feeds fdot2 as its own value (extracting it back out of the
+                    // packed vector has been miscompiled into a reuse of the first pair).
+                    ts[qb] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ts[qb], false);
+                    w[e] = __builtin_bit_cast(uint32_t, pr);
+                }
+                pn[qb][hf] = __builtin_bit_cast(bf16x8, w);
+            }
+    };
+
+    bool overflow = false;    // wave-uniform: some block's row sum passed the bound
+
+    // Steady-state step: the 2*(NC + 2*NDB) products are issued one at a time with a slice of
+    // the softmax of S(s) after every other one, and each LDS operand is read three operands
+    // ahead; the sched_barrier after each product keeps the compiler from regrouping them.
+    auto fast_step = [&](int s, const bf16 *Kc, const bf16 *Vp) __attribute__((always_inline)) {
+        constexpr int NOP = NC + 2 * NDB;              // LDS operands per step
+        constexpr int NPAIR = 16;                      // bf16 pairs of P(s) per lane
+        constexpr int PER = 2 * NOP <= NPAIR ? NPAIR / (2 * NOP) : (NPAIR + NOP - 1) / NOP;
+        const int kbn = (s + 1) & 1, kbp = (s - 1) & 1;
+        auto opnd = [&](int i) __attribute__((always_inline)) -> bf16x8 {
+            if (i < NC) return k_opnd(Kc, kbn, i);
+            const int j = i - NC;
+            return v_opnd(Vp, 2 * kbp + j / NDB, j % NDB);
+        };
+        const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
+        float ts[2] = {0.f, 0.f};
+        u32x4 w[2][2];
+        f32x16 sn[2];
+        bf16x8 a[NOP];
+        a[0] = opnd(0);
+        a[1] = opnd(1);
+        a[2] = opnd(2);
+        int pair = 0;
+        auto slice = [&](int n) __attribute__((always_inline)) {
+            for (int k = 0; k < n && pair < NPAIR; ++k, ++pair) {
+                const int qb = pair >> 3, hf = (pair >> 2) & 1, e = pair & 3;
+                const bf16x2 pr = {(bf16)__builtin_amdgcn_exp2f(sc[qb][8 * hf + 2 * e]),
+                                   (bf16)__builtin_amdgcn_exp2f(sc[qb][8 * hf + 2 * e + 1])};
+                ts[qb] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ts[qb], false);
+                w[qb][hf][e] = __builtin_bit_cast(uint32_t, pr);
+            }
+        };
+#pragma unroll
+        for (int i = 0; i < NOP; ++i) {
+            if (i + 3 < NOP) a[i + 3] = opnd(i + 3);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                if (i < NC) {
+                    sn[qb] = mfma32(a[i], qf[qb][i], i == 0 ? negm[qb] : sn[qb]);
+                } else {
+                    const int j = i - NC;
+                    o[j % NDB][qb] = mfma32(a[i], pp[qb][j / NDB], o[j % NDB][qb]);
+                }
+                if (qb == 1 || 2 * NOP <= NPAIR) slice(PER);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        overflow |= !(ts[0] <= kRebaseBound) || !(ts[1] <= kRebaseBound);
+        l[0] += ts[0];
+        l[1] += ts[1];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            sc[qb] = sn[qb];
+            pp[qb][0] = __builtin_bit_cast(bf16x8, w[qb][0]);
+            pp[qb][1] = __builtin_bit_cast(bf16x8, w[qb][1]);
+        }
+    };
+
+    // Edge step: the first block (sets the running max), the ragged last block, and the
+    // pipeline's fill and drain, where parts of the step are absent.
+    auto edge_step = [&](int s, const bf16 *Kc, const bf16 *Vp) __attribute__((always_inline)) {
+        const bool do_sm = s >= blk_begin && s < blk_end;
+        const bool do_s = s + 1 >= blk_begin && s + 1 < blk_end;
+        const bool do_pv = s - 1 >= blk_begin && s - 1 < blk_end;
+        if (do_sm) {
+            if (ragged && s == blk_end - 1) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = 32 * s + 8 * (i >> 2) + 4 * g + (i & 3);
+                    if (key >= n_valid) sc[0][i] = sc[1][i] = -INFINITY;
+                }
+            }
+            if (s == blk_begin) {
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb) {
+                    float mx = sc[qb][0];
+#pragma unroll
+                    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sc[qb][i]);
+                    mx = fmaxf(mx, xlane32(mx));
+                    m[qb] = mx;
+                    negm[qb] = splat16(-mx);
+                    sc[qb] -= splat16(mx);
+                }
+            }
+        }
+        f32x16 sn[2];
+        if (do_s) qk_block(Kc, (s + 1) & 1, sn);
+        if (do_pv) pv_block(Vp, (s - 1) & 1);
+        bf16x8 pn[2][2];
+        if (do_sm) {
+            float ts[2];
+            softmax_block(sc, pn, ts);
+            overflow |= !(ts[0] <= kRebaseBound) || !(ts[1] <= kRebaseBound);
+            l[0] += ts[0];
+            l[1] += ts[1];
+        }
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            if (do_s) sc[qb] = sn[qb];
+            if (do_sm) {
+                pp[qb][0] = pn[qb][0];
+                pp[qb][1] = pn[qb][1];
+            }
+        }
+    };
+
+    // ---- main loop --------------------------------------------------------------------
+    if (t_begin < t_end) copy_k(t_begin, (t_begin & 1) ? sK1 : sK0);
+    const int t_last = t_begin < t_end ? t_end : t_begin - 1;
+    // Windows [t_begin, tf0) and [tf1, t_last] fill and drain the pipeline (and carry the
+    // first block, the ragged block and the split edges); the windows in between are
+    // straight-line.
+    int tf0 = max(t_begin, (blk_begin + 3) / 2);        // first t with 2t-2 >= blk_begin
+    int tf1 = max(tf0, blk_end / 2);                     // first t with 2t+1 >= blk_end
+    tf0 = min(tf0, t_last + 1);
+    tf1 = min(tf1, t_last + 1);
+    // `par` is t & 1: a compile-time constant in the steady state, a value at the edges.
+    auto window = [&](auto fast, auto par, int t) __attribute__((always_inline)) {
+        const int P = par;
+        bf16 *Kc = P ? sK1 : sK0, *Kn = P ? sK0 : sK1;
+        bf16 *Vc = P ? sV1 : sV0, *Vp = P ? sV0 : sV1;
+        wait_copies();        // this wave's copies of K(t) and V(t-1) have landed
+        __syncthreads();      // everyone's have, and window t-1's reads are done
+        if (t + 1 < t_end) copy_k(t + 1, Kn);
+        if (t < t_end) copy_v(t, Vc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (active) {
+            if constexpr (decltype(fast)::value) {
+                fast_step(2 * t - 1, Kc, Vp);
+                fast_step(2 * t, Kc, Vp);
+            } else {
+                edge_step(2 * t - 1, Kc, Vp);
+                edge_step(2 * t, Kc, Vp);
+            }
+        }
+    };
+    using even = std::integral_constant<int, 0>;
+    using odd = std::integral_constant<int, 1>;
+    for (int t = t_begin; t < tf0; ++t) window(std::false_type{}, t & 1, t);
+    {
+        int t = tf0;
+        if (t < tf1 && (t & 1)) window(std::true_type{}, odd{}, t++);
+        for (; t + 1 < tf1; t += 2) {
+            window(std::true_type{}, even{}, t);
+            window(std::true_type{}, odd{}, t + 1);
+        }
+        if (t < tf1) window(std::true_type{}, even{}, t);
+    }
+    for (int t = tf1; t <= t_last; ++t) window(std::false_type{}, t & 1, t);
+    wait_copies();
+
+    // ---- safe pass: only when some wave's running max was outgrown -------------------
+    // Tile by tile, each 32-key block rebasing O and l as soon as its weights would exceed
+    // 2^64. Pathological inputs only.
+    if (__syncthreads_or(overflow)) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) o[db][0] = o[db][1] = splat16(0.f);
+        m[0] = m[1] = l[0] = l[1] = 0.f;
+        negm[0] = negm[1] = splat16(0.f);
+        for (int t = t_begin; t < t_end; ++t) {
+            __syncthreads();
+            copy_k(t, sK0);
+            copy_v(t, sV0);
+            wait_copies();
+            __syncthreads();
+            if (!active) continue;
+            for (int kb = 0; kb < 2; ++kb) {
+                const int s = 2 * t + kb;
+                if (s >= blk_end) break;
+                f32x16 sx[2];
+                qk_block(sK0, kb, sx);     // negm is 0 until the first block sets the max
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = 32 * s + 8 * (i >> 2) + 4 * g + (i & 3);
+                    if (key >= n_valid) sx[0][i] = sx[1][i] = -INFINITY;
+                }
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb) {
+                    float mx = sx[qb][0];
+#pragma unroll
+                    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sx[qb][i]);
+                    mx = fmaxf(mx, xlane32(mx));
+                    // first block: take its max; later blocks: move up when it is exceeded
+                    const float d = (s == blk_begin) ? mx : (mx > 0.f ? mx : 0.f);
+                    const float f = (s == blk_begin) ? 1.0f : __builtin_amdgcn_exp2f(-d);
+                    m[qb] += d;
+                    negm[qb] = splat16(-m[qb]);
+                    l[qb] *= f;
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) o[db][qb] *= splat16(f);
+                    sx[qb] -= splat16(d);
+                }
+                float ts[2];
+                softmax_block(sx, pp, ts);
+                l[0] += ts[0];
+                l[1] += ts[1];
+                pv_block(sV0, kb);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- epilogue ---------------------------------------------------------------------
+    float lt[2];
+    lt[0] = l[0] + xlane32(l[0]);
+    lt[1] = l[1] + xlane32(l[1]);
+
+    if (p.num_splits > 1) {
+        if (!active) return;
+        const bool empty = t_begin >= t_end;
+        const int64_t rowbase = (((int64_t)split * p.B + b) * p.H + h) * p.Lq;
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int q = q0 + 32 * qb + r;
+            if (q >= p.Lq) continue;
+            float *po = p.part_o + (rowbase + q) * D;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    f32x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = o[db][qb][4 * i4 + e];
+                    *(f32x4 *)(po + db * 32 + 8 * i4 + 4 * g) = v;
+                }
+            if (g == 0) {
+                float *ml = p.part_ml + (rowbase + q) * 2;
+                ml[0] = empty ? -INFINITY : m[qb];
+                ml[1] = empty ? 0.f : lt[qb];
+            }
+        }
+        return;
+    }
+
+    // Unsplit: normalise, stage the wave's O [64 queries][D] in one of the four tile
+    // buffers (swizzled like K), store coalesced 16-byte units.
+    bf16 *Os = wave == 0 ? sK0 : wave == 1 ? sK1 : wave == 2 ? sV0 : sV1;
+    if (active) {
+        const float inv0 = 1.0f / lt[0], inv1 = 1.0f / lt[1];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const float inv = qb ? inv1 : inv0;
+                    const int row = 32 * qb + r;
+                    u32x2 w;
+                    w[0] = pack_bf2(o[db][qb][4 * i4 + 0] * inv, o[db][qb][4 * i4 + 1] * inv);
+                    w[1] = pack_bf2(o[db][qb][4 * i4 + 2] * inv, o[db][qb][4 * i4 + 3] * inv);
+                    *(u32x2 *)(Os + row * D + 8 * swz<KU>(row, 4 * db + i4) + 4 * g) = w;
+                }
+    }
+    __syncthreads();
+    if (active) {
+        bf16 *Ob = (bf16 *)p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs;
+#pragma unroll
+        for (int it = 0; it < QW * KU / 64; ++it) {
+            const int u = lane + 64 * it;
+            const int row = u / KU, c = u % KU;
+            const int q = q0 + row;
+            if (q < p.Lq)
+                *(u32x4 *)(Ob + (int64_t)q * p.o_rs + 8 * c) =
+                    *(const u32x4 *)(Os + row * D + 8 * swz<KU>(row, c));
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// V^T prologue: one workgroup per (batch, head, 64-key tile). The tile goes through LDS so
+// both the reads (key rows of D channels) and the writes (channel rows of 64 key positions)
+// are whole 16-byte units. Keys at or past the valid length are written as zeros, so padded
+// positions contribute 0 * 0 to P.V.
+// ------------------------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void vt_prep_kernel(const VtParams p) {
+    constexpr int U = D / 8;                  // 16-byte units per V row
+    constexpr int RS = D + 8;                 // LDS row stride (elements)
+    __shared__ __attribute__((aligned(16))) bf16 tile[KT * RS];
+    const int tid = threadIdx.x;
+    const int t = blockIdx.x % p.ntiles;
+    const int bh = blockIdx.x / p.ntiles;
+    const int h = bh % p.H, b = bh / p.H;
+    const int n_valid = p.masked ? p.valid[b] : p.Lk;
+    const bf16 *Vb = (const bf16 *)p.v + (int64_t)b * p.v_bs + (int64_t)h * p.v_hs;
+#pragma unroll
+    for (int i = 0; i < KT * U / 256; ++i) {
+        const int unit = tid + 256 * i;
+        const int row = unit / U, u = unit % U;
+        const int key = t * KT + row;
+        u32x4 w = {0u, 0u, 0u, 0u};
+        if (key < n_valid) w = ldg16(Vb + (int64_t)key * p.v_rs + 8 * u);
+        *(u32x4 *)(tile + row * RS + 8 * u) = w;
+    }
+    __syncthreads();
+    const uint16_t *tb = (const uint16_t *)tile;
+    bf16 *Out = (bf16 *)p.vt + ((int64_t)b * p.H + h) * D * p.ld + (int64_t)t * KT;
+#pragma unroll
+    for (int i = 0; i < D * (KT / 8) / 256; ++i) {
+        const int unit = tid + 256 * i;
+        const int d = unit / (KT / 8), c = unit % (KT / 8);
+        u32x4 w;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t lo = tb[vt_pos(8 * c + 2 * j) * RS + d];
+            const uint32_t hi = tb[vt_pos(8 * c + 2 * j + 1) * RS + d];
+            w[j] = lo | (hi << 16);
+        }
+        *(u32x4 *)(Out + (int64_t)d * p.ld + 8 * c) = w;
+    }
+}
+
+}  // namespace
+
+int launch_fmha_dma(const FmhaParams &p, int D, void *stream) {
+    const dim3 grid(p.total_groups), block(NT);
+    hipStream_t st = (hipStream_t)stream;
+    if (D == 128) hipLaunchKernelGGL(fmha_dma_kernel<128>, grid, block, 0, st, p);
+    else hipLaunchKernelGGL(fmha_dma_kernel<64>, grid, block, 0, st, p);
+    return (int)hipGetLastError();
+}
+
+int launch_vt(const VtParams &p, int D, void *stream) {
+    const dim3 grid((unsigned)((int64_t)p.B * p.H * p.ntiles)), block(256);
+    hipStream_t st = (hipStream_t)stream;
+    if (D == 128) hipLaunchKernelGGL(vt_prep_kernel<128>, grid, block, 0, st, p);
+    else hipLaunchKernelGGL(vt_prep_kernel<64>, grid, block, 0, st, p);
+    return (int)hipGetLastError();
+}
+
+}  // namespace ltx

@@ -26,87 +26,12 @@
 //   overflow the bound the wave rebases (rescales O and l) and recomputes that tile's p --
 //   exact, and rare. The row sum is accumulated from the bf16-rounded p that feed P.V, so the
 //   weights applied are exactly the weights normalised.
-#include <hip/hip_runtime.h>
-#include <math.h>
-#include <stdint.h>
-
 #include <type_traits>
 
-#include "fmha_params.hpp"
+#include "fmha_device.hpp"
 
 namespace ltx {
 namespace {
-
-typedef __bf16 bf16;
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-constexpr int KT = kKeyTile;
-constexpr int QW = kQueriesPerWave;
-constexpr int NW = kWavesPerGroup;
-constexpr int QT = kQueriesPerGroup;
-constexpr int NT = NW * 64;                 // threads per workgroup
-constexpr float kRebaseBound = 1.8446744e19f;  // 2^64: largest p a tile may produce
-
-__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-
-__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
-    bf16x2 v = {(bf16)a, (bf16)b};
-    return __builtin_bit_cast(uint32_t, v);
-}
-
-__device__ __forceinline__ void unpack8(const u32x4 w, float f[8]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f[2 * i] = bf_lo(w[i]);
-        f[2 * i + 1] = bf_hi(w[i]);
-    }
-}
-
-__device__ __forceinline__ u32x4 pack8(const float f[8]) {
-    u32x4 w;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = pack_bf2(f[2 * i], f[2 * i + 1]);
-    return w;
-}
-
-__device__ __forceinline__ u32x4 ldg16(const void *p) { return *(const u32x4 *)p; }
-
-// Raw buffer resource over [base, base + bytes): loads past the end return zero.
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-constexpr int kRsrcWord3 = 0x00020000;   // 32-bit data format, no swizzle (gfx9 family)
-
-__device__ __forceinline__ rsrc_t make_rsrc(const void *base, int64_t bytes) {
-    const int n = bytes <= 0 ? 0 : (bytes >= 0x7fffffff ? 0x7fffffff : (int)bytes);
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, kRsrcWord3);
-}
-
-__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-}
-
-__device__ __forceinline__ f32x16 splat16(float x) {
-    f32x16 v;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = x;
-    return v;
-}
-
-__device__ __forceinline__ float xlane32(float x) { return __shfl_xor(x, 32, 64); }
-
-// Position of key k (0..63) inside an LDS row of V^T: bits 2 and 3 swapped.
-__device__ __forceinline__ int vt_pos(int k) {
-    return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
-}
-
-__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
 
 // ------------------------------------------------------------------------------------------
 // Main kernel
@@ -150,17 +75,8 @@ void fmha_fwd_kernel(const FmhaParams p) {
     const int r = lane & 31;
     const int g = lane >> 5;
 
-    // ---- work item: consecutive items of one XCD share (batch, head, split) -------------
-    const int N = p.total_groups;
-    const int bid = blockIdx.x;
-    const int xcd = bid & 7;
-    const int item = xcd * (N >> 3) + min(xcd, N & 7) + (bid >> 3);
-    const int qblk = item % p.nqblk;
-    int rest = item / p.nqblk;
-    const int split = rest % p.num_splits;
-    rest /= p.num_splits;
-    const int h = rest % p.H;
-    const int b = rest / p.H;
+    const WorkItem wi = work_item(p);
+    const int qblk = wi.qblk, split = wi.split, h = wi.h, b = wi.b;
 
     const int n_valid = p.valid[b];
     const int ntiles = (n_valid + KT - 1) / KT;
@@ -175,57 +91,7 @@ void fmha_fwd_kernel(const FmhaParams p) {
 
     // ---- Q: load, normalise, rotate, scale, round once -------------------------------
     bf16x8 qf[2][NC];
-    {
-        const bf16 *Qb = (const bf16 *)p.q + (int64_t)b * p.q_bs + (int64_t)h * p.q_hs;
-        const int nq = max(0, min(QW, p.Lq - q0));   // valid queries of this wave
-        const rsrc_t rq = make_rsrc(Qb + (int64_t)(active ? q0 : 0) * p.q_rs,
-                                    (int64_t)nq * p.q_rs * 2);
-        float wq[NC][8];
-        if (p.q_rstd) {
-            const bf16 *w = (const bf16 *)p.q_w + h * D;
-#pragma unroll
-            for (int c = 0; c < NC; ++c) unpack8(ldg16(w + 16 * c + 8 * g), wq[c]);
-        }
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            const int qi = 32 * qb + r;               // query within the wave
-            const int qc = min(q0 + qi, p.Lq - 1);     // clamped index for side tables
-            float x[NC][8];
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-                unpack8(bload16(rq, (uint32_t)(qi * p.q_rs * 2 + (16 * c + 8 * g) * 2)), x[c]);
-            if (p.q_rstd) {
-                const float rs = p.q_rstd[(int64_t)b * p.Lq + qc];
-#pragma unroll
-                for (int c = 0; c < NC; ++c)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) x[c][e] = (x[c][e] * rs) * wq[c][e];
-            }
-            if (p.q_cos) {
-                const int64_t toff = ((int64_t)h * p.Lq + qc) * (D / 2);
-                const bf16 *cs = (const bf16 *)p.q_cos + toff;
-                const bf16 *sn = (const bf16 *)p.q_sin + toff;
-#pragma unroll
-                for (int c = 0; c < NC / 2; ++c) {
-                    float fc[8], fs[8];
-                    unpack8(ldg16(cs + 16 * c + 8 * g), fc);
-                    unpack8(ldg16(sn + 16 * c + 8 * g), fs);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float x1 = x[c][e], x2 = x[c + NC / 2][e];
-                        x[c][e] = x1 * fc[e] - x2 * fs[e];
-                        x[c + NC / 2][e] = x2 * fc[e] + x1 * fs[e];
-                    }
-                }
-            }
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[c][e] *= p.qk_scale_log2;
-                qf[qb][c] = __builtin_bit_cast(bf16x8, pack8(x[c]));
-            }
-        }
-    }
+    load_q<D>(p, b, h, q0, active, r, g, qf);
 
     // ---- staging (global -> registers -> LDS); K runs one tile ahead of V --------------
     // Buffer loads: the resource of tile t starts at key t*KT and ends at the last valid
@@ -426,8 +292,72 @@ void fmha_fwd_kernel(const FmhaParams p) {
     // the step only records it, and the workgroup then recomputes its rows with the safe pass
     // below, so the pipelined region carries no rescaling code.
     bool overflow = false;    // wave-uniform
+    // Fast step (every part present): the 2*(NC+2*NDB) matrix-core products of the step are
+    // issued one at a time with a slice of the softmax of S(s) between them, and each LDS
+    // operand is read two operands ahead, so the VALU work runs under the matrix cores.
+    // The sched_barrier after each slice keeps the compiler from regrouping them.
+    auto fast_step = [&](int s) __attribute__((always_inline)) {
+        constexpr int NOP = NC + 2 * NDB;              // LDS operands per step
+        constexpr int NPAIR = 16;                      // bf16 pairs of P(s) per lane
+        const bf16 *Ks = smem + (((s + 1) >> 1) & 1) * T::STAGE + (((s + 1) & 1) * 32 + r) * KS + 8 * g;
+        const bf16 *Vt = smem + (((s - 1) >> 1) & 1) * T::STAGE + T::K_ELEMS + r * VS
+                         + 16 * (2 * ((s - 1) & 1)) + 8 * g;
+        auto opnd = [&](int i) __attribute__((always_inline)) -> bf16x8 {
+            if (i < NC) return *(const bf16x8 *)(Ks + 16 * i);
+            const int j = i - NC, hf = j / NDB, db = j % NDB;
+            return *(const bf16x8 *)(Vt + db * 32 * VS + 16 * hf);
+        };
+        const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
+        float ts[2] = {0.f, 0.f};
+        u32x4 w[2][2];
+        f32x16 sn[2];
+        bf16x8 a[NOP];
+        a[0] = opnd(0);
+        a[1] = opnd(1);
+        a[2] = opnd(2);
+        int pair = 0;
+        auto slice = [&](int n) __attribute__((always_inline)) {
+            for (int k = 0; k < n && pair < NPAIR; ++k, ++pair) {
+                const int qb = pair >> 3, hf = (pair >> 2) & 1, e = pair & 3;
+                const bf16x2 pr = {(bf16)__builtin_amdgcn_exp2f(sc[qb][8 * hf + 2 * e]),
+                                   (bf16)__builtin_amdgcn_exp2f(sc[qb][8 * hf + 2 * e + 1])};
+                ts[qb] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ts[qb], false);
+                w[qb][hf][e] = __builtin_bit_cast(uint32_t, pr);
+            }
+        };
+        constexpr int PER = 2 * NOP <= NPAIR ? NPAIR / (2 * NOP) : (NPAIR + NOP - 1) / NOP;
+#pragma unroll
+        for (int i = 0; i < NOP; ++i) {
+            if (i + 3 < NOP) a[i + 3] = opnd(i + 3);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                if (i < NC) {
+                    sn[qb] = mfma32(a[i], qf[qb][i], i == 0 ? negm[qb] : sn[qb]);
+                } else {
+                    const int j = i - NC, hf = j / NDB, db = j % NDB;
+                    o[db][qb] = mfma32(a[i], pp[qb][hf], o[db][qb]);
+                }
+                if (qb == 1 || 2 * NOP <= NPAIR) slice(PER);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        overflow |= !(ts[0] <= kRebaseBound) || !(ts[1] <= kRebaseBound);
+        l[0] += ts[0];
+        l[1] += ts[1];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            sc[qb] = sn[qb];
+            pp[qb][0] = __builtin_bit_cast(bf16x8, w[qb][0]);
+            pp[qb][1] = __builtin_bit_cast(bf16x8, w[qb][1]);
+        }
+    };
+
     auto step = [&](auto gen, int s) __attribute__((always_inline)) {
         constexpr bool GEN = decltype(gen)::value;
+        if constexpr (!GEN) {
+            fast_step(s);
+            return;
+        }
         const bool do_sm = !GEN || (s >= blk_begin && s < blk_end);
         const bool do_s = !GEN || (s + 1 >= blk_begin && s + 1 < blk_end);
         const bool do_pv = !GEN || (s - 1 >= blk_begin && s - 1 < blk_end);
@@ -734,9 +664,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineParams p) {
 
 }  // namespace
 
-int launch_fmha(const FmhaParams &p, int D, bool k_fused, void *stream) {
+int launch_fmha(const FmhaParams &p, int D, int kind, void *stream) {
+    if (kind == kDma) return launch_fmha_dma(p, D, stream);
     const dim3 grid(p.total_groups), block(NT);
     hipStream_t st = (hipStream_t)stream;
+    const bool k_fused = kind == kRegFused;
     if (D == 128) {
         if (k_fused) hipLaunchKernelGGL((fmha_fwd_kernel<128, true>), grid, block, 0, st, p);
         else hipLaunchKernelGGL((fmha_fwd_kernel<128, false>), grid, block, 0, st, p);

@@ -37,14 +37,17 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 struct Plan {
     bool q_norm = false, k_norm = false;
     bool q_rope = false, k_rope = false;
+    bool dma = false;          // LDS-DMA kernel (V^T prologue; K prologue when K needs work)
     bool k_prologue = false;   // K normalised/rotated by a separate pass into the workspace
     bool k_fused = false;      // K normalised/rotated while staging into LDS
+    int64_t vt_ld = 0;         // key positions per V^T row (DMA kernel)
     int nqblk = 0;
     int ntiles_max = 0;
     int splits = 1;
     int tiles_per_split = 0;
     // workspace layout (byte offsets)
-    size_t off_qrstd = 0, off_krstd = 0, off_kprep = 0, off_part_o = 0, off_part_ml = 0;
+    size_t off_qrstd = 0, off_krstd = 0, off_kprep = 0, off_vt = 0, off_part_o = 0,
+           off_part_ml = 0;
     size_t bytes = 0;
 };
 
@@ -135,14 +138,24 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
         pl->ntiles_max = (nmax + ltx::kKeyTile - 1) / ltx::kKeyTile;
     }
 
-    // K strategy: a separate prologue pays one extra read+write of K; fusing pays the
-    // norm/RoPE arithmetic once per query block that re-reads K.
+    // Kernel: with two or more query blocks per (batch, head) the LDS-DMA kernel reads K
+    // (prepared by the K prologue when it needs norm/RoPE) and V^T (from the V^T prologue)
+    // straight into LDS; each prologue pays one extra read+write of its tensor. A single
+    // query block takes the register-staged kernel, fusing K's norm/RoPE into its staging.
+    // The DMA kernel's 32-bit buffer offsets bound a K tile (64 rows) and a V^T head
+    // (D rows of the padded key length); calls past them take the register-staged kernel.
     const bool k_work = pl->k_norm || pl->k_rope;
-    if (k_work) {
-        if (a->kprep == LTX_ATTN_KPREP_PROLOGUE) pl->k_prologue = true;
-        else if (a->kprep == LTX_ATTN_KPREP_FUSED) pl->k_fused = true;
-        else if (pl->nqblk >= 2) pl->k_prologue = true;
-        else pl->k_fused = true;
+    const int64_t vt_ld = ((int64_t)a->Lk + ltx::kKeyTile - 1) / ltx::kKeyTile * ltx::kKeyTile;
+    const int64_t k_rs_eff = k_work ? (int64_t)H * D : a->k_rs;
+    const bool dma_fits = (int64_t)D * vt_ld * 2 < 0x7fffffff &&
+                          (int64_t)ltx::kKeyTile * k_rs_eff * 2 < 0x7fffffff;
+    if (a->kprep == LTX_ATTN_KPREP_PROLOGUE) pl->dma = dma_fits;
+    else if (a->kprep == LTX_ATTN_KPREP_AUTO) pl->dma = dma_fits && pl->nqblk >= 2;
+    if (pl->dma) {
+        pl->k_prologue = k_work;
+        pl->vt_ld = vt_ld;
+    } else {
+        pl->k_fused = k_work;
     }
 
     // Split-KV when (batch, head, query block) items alone cannot fill the chip.
@@ -175,6 +188,10 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
     if (pl->k_prologue) {
         pl->off_kprep = off;
         off = align_up(off + 2 * (size_t)B * a->Lk * H * D, 256);
+    }
+    if (pl->dma) {
+        pl->off_vt = off;
+        off = align_up(off + 2 * (size_t)B * H * D * pl->vt_ld, 256);
     }
     if (pl->splits > 1) {
         const size_t rows = (size_t)pl->splits * B * H * a->Lq;
@@ -259,6 +276,21 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
         }
     }
 
+    if (pl.dma) {
+        ltx::VtParams vp{};
+        vp.v = a->v; vp.v_bs = a->v_bs; vp.v_rs = a->v_rs; vp.v_hs = a->v_hs;
+        vp.B = B; vp.H = H; vp.Lk = a->Lk;
+        vp.ld = pl.vt_ld;
+        vp.ntiles = (int32_t)(pl.vt_ld / ltx::kKeyTile);
+        vp.vt = ws + pl.off_vt;
+        vp.masked = a->k_valid_len != nullptr;
+        if (a->k_valid_len)
+            for (int b = 0; b < B; ++b) vp.valid[b] = a->k_valid_len[b];
+        if (int e = ltx::launch_vt(vp, D, stream))
+            return fail(LTX_ATTN_EHIP, "v prologue launch: %s", hipGetErrorString((hipError_t)e));
+    }
+    const int kind = pl.dma ? ltx::kDma : pl.k_fused ? ltx::kRegFused : ltx::kRegPlain;
+
     // 2. attention
     ltx::FmhaParams fp{};
     fp.q = a->q; fp.q_bs = a->q_bs; fp.q_rs = a->q_rs; fp.q_hs = a->q_hs;
@@ -274,6 +306,10 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
             fp.k_cos = a->k_cos ? a->k_cos : a->q_cos;
             fp.k_sin = a->k_sin ? a->k_sin : a->q_sin;
         }
+    }
+    if (pl.dma) {
+        fp.vt = ws + pl.off_vt;
+        fp.vt_ld = pl.vt_ld;
     }
     fp.qk_scale_log2 = (float)((double)a->scale * 1.4426950408889634);
     fp.nqblk = pl.nqblk;
@@ -295,6 +331,7 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
             sp.q = (const char *)a->q + 2 * (int64_t)b0 * a->q_bs;
             sp.k = (const char *)kptr + 2 * (int64_t)b0 * k_bs;
             sp.v = (const char *)a->v + 2 * (int64_t)b0 * a->v_bs;
+            if (pl.dma) sp.vt = (const char *)fp.vt + 2 * (int64_t)b0 * H * D * pl.vt_ld;
             sp.o = (char *)a->out + 2 * (int64_t)b0 * a->o_bs;
             if (sp.q_rstd) sp.q_rstd += (int64_t)b0 * a->Lq;
             if (sp.k_rstd) sp.k_rstd += (int64_t)b0 * a->Lk;
@@ -302,7 +339,7 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
             if (a->ev_attn_start && b0 == 0)
                 if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_start, (hipStream_t)stream))
                     return fail(LTX_ATTN_EHIP, "event record: %s", hipGetErrorString(e));
-            if (int e = ltx::launch_fmha(sp, D, pl.k_fused, stream))
+            if (int e = ltx::launch_fmha(sp, D, kind, stream))
                 return fail(LTX_ATTN_EHIP, "attention launch: %s", hipGetErrorString((hipError_t)e));
         }
         if (a->ev_attn_stop)
@@ -313,7 +350,7 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     if (a->ev_attn_start)
         if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_start, (hipStream_t)stream))
             return fail(LTX_ATTN_EHIP, "event record: %s", hipGetErrorString(e));
-    if (int e = ltx::launch_fmha(fp, D, pl.k_fused, stream))
+    if (int e = ltx::launch_fmha(fp, D, kind, stream))
         return fail(LTX_ATTN_EHIP, "attention launch: %s", hipGetErrorString((hipError_t)e));
     if (a->ev_attn_stop)
         if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_stop, (hipStream_t)stream))
@@ -345,8 +382,8 @@ const char *ltx_attn_status_string(ltx_attn_status s) {
 const char *ltx_attn_last_error(void) { return g_err; }
 
 const char *ltx_attn_provenance(void) {
-    return "hip-gfx950 fused flash attention v1 (bf16 mfma_f32_32x32x16, online fp32 softmax, "
-           "QK-RMSNorm+RoPE fused)";
+    return "hip-gfx950 fused flash attention v2 (bf16 mfma_f32_32x32x16, online fp32 softmax, "
+           "QK-RMSNorm+RoPE fused; K/V^T tiles by LDS DMA for multi-block queries)";
 }
 
 int32_t ltx_attn_abi_version(void) { return LTX_ATTN_ABI_VERSION; }

@@ -27,7 +27,8 @@ from typing import Optional, Sequence
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(os.path.dirname(_HERE), "lib", "libltx_attn.so")
+LIB_PATH = os.environ.get("LTX_ATTN_LIBRARY",
+                          os.path.join(os.path.dirname(_HERE), "lib", "libltx_attn.so"))
 
 OK, EINVAL, EUNSUPPORTED, EHIP, EWORKSPACE = 0, 1, 2, 3, 4
 KPREP_AUTO, KPREP_FUSED, KPREP_PROLOGUE = 0, 1, 2

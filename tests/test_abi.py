@@ -54,7 +54,9 @@ def test_struct_layout_and_version():
 FAKE = 0x7F0000000000   # 256-byte aligned fake device address (never dereferenced)
 
 
-def _args(B=1, H=32, Lq=3120, Lk=3120, D=128, **kw):
+def _args(B=1, H=32, Lq=3120, Lk=3120, D=128, ws=True, **kw):
+    """Arguments of a plausible call; `ws` attaches a (fake) workspace large enough for any
+    plan, so that validation reaches the field under test."""
     a = L.Args()
     L.load_library().ltx_attn_args_init(ctypes.byref(a))
     a.B, a.H, a.Lq, a.Lk, a.D = B, H, Lq, Lk, D
@@ -65,6 +67,8 @@ def _args(B=1, H=32, Lq=3120, Lk=3120, D=128, **kw):
     a.v_bs, a.v_rs, a.v_hs = Lk * inner, inner, D
     a.o_bs, a.o_rs, a.o_hs = Lq * inner, inner, D
     a.scale = 1.0 / np.sqrt(D)
+    if ws:
+        a.workspace, a.workspace_bytes = FAKE + (4 << 32), 1 << 40
     for k, v in kw.items():
         setattr(a, k, v)
     return a
@@ -77,6 +81,12 @@ def _validate(a):
 
 
 def test_valid_arguments_pass():
+    # register-staged kernel without K work: no workspace
+    st, msg = _validate(_args(kprep=L.KPREP_FUSED, ws=False))
+    assert st == L.OK, msg
+    # LDS-DMA kernel: the V^T buffer must be provided
+    st, msg = _validate(_args(ws=False))
+    assert st == L.EWORKSPACE, msg
     st, msg = _validate(_args())
     assert st == L.OK, msg
 
@@ -114,7 +124,7 @@ def test_rotary_rules():
     st, msg = _validate(_args(Lq=3120, Lk=126, D=64, H=32, q_cos=FAKE, q_sin=FAKE))
     assert st == L.EINVAL and "Lq" in msg
     st, msg = _validate(_args(Lq=3120, Lk=126, D=64, H=32, q_cos=FAKE, q_sin=FAKE,
-                              k_cos=FAKE, k_sin=FAKE))
+                              k_cos=FAKE, k_sin=FAKE, ws=False))
     assert st == L.EWORKSPACE, msg      # arguments fine; the K prologue needs scratch
 
 
@@ -138,15 +148,20 @@ def test_key_padding_rules():
 
 def test_workspace_sizing_and_check():
     lib = L.load_library()
-    # plain attention, enough work to fill the chip: no workspace
+    # plain attention over 13 query blocks: the LDS-DMA kernel's V^T, keys padded to 64
     a = _args()
+    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == 2 * 32 * 128 * 3136
+    # the same on the register-staged kernel: no workspace
+    a = _args(kprep=L.KPREP_FUSED)
     assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == 0
-    # 12480-token self-attention with norm + RoPE: q statistic + prepared K
-    a = _args(Lq=12480, Lk=12480, q_norm_w=FAKE, k_norm_w=FAKE, q_cos=FAKE, q_sin=FAKE)
+    # 12480-token self-attention with norm + RoPE: q statistic + prepared K + V^T
+    a = _args(Lq=12480, Lk=12480, q_norm_w=FAKE, k_norm_w=FAKE, q_cos=FAKE, q_sin=FAKE,
+              ws=False)
     need = lib.ltx_attn_workspace_bytes(ctypes.byref(a))
     rstd = (12480 * 4 + 255) // 256 * 256
     kprep = (12480 * 4096 * 2 + 255) // 256 * 256
-    assert need == rstd + kprep
+    vt = 2 * 32 * 128 * 12480
+    assert need == rstd + kprep + vt
     st, msg = _validate(a)
     assert st == L.EWORKSPACE and str(need) in msg
     a.workspace, a.workspace_bytes = FAKE, need - 1
