@@ -144,24 +144,47 @@ __device__ __forceinline__ void load_q(const FmhaParams &p, int b, int h, int q0
     }
 }
 
-// Work item of a workgroup: consecutive items of one XCD (workgroup ids are dealt to the 8
-// XCDs round-robin) so that the query blocks sharing one (batch, head, split) share an L2.
+// Work item of a workgroup. Workgroup ids are dealt to the 8 XCDs round-robin; within each
+// region of the grid (whole items, then tail splits) an XCD receives a contiguous range, so
+// the query blocks (and splits) sharing one (batch, head) share an L2.
 struct WorkItem {
-    int qblk, split, h, b;
+    int qblk, h, b;
+    int tail;          // -1 for a whole item, else the tail item's index (0-based)
+    int split;         // key range of a tail item
+    int t_begin, t_end;
 };
 
+__device__ __forceinline__ int xcd_major(int local, int count) {
+    const int xcd = local & 7;
+    return xcd * (count >> 3) + min(xcd, count & 7) + (local >> 3);
+}
+
 __device__ __forceinline__ WorkItem work_item(const FmhaParams &p) {
-    const int N = p.total_groups;
     const int bid = blockIdx.x;
-    const int xcd = bid & 7;
-    const int item = xcd * (N >> 3) + min(xcd, N & 7) + (bid >> 3);
     WorkItem w;
+    int item;
+    if (bid < p.n_full) {
+        item = xcd_major(bid, p.n_full);
+        w.tail = -1;
+        w.split = 0;
+    } else {
+        const int sub = xcd_major(bid - p.n_full, p.grid - p.n_full);
+        w.tail = sub / p.num_splits;
+        w.split = sub % p.num_splits;
+        item = p.n_full + w.tail;
+    }
     w.qblk = item % p.nqblk;
-    int rest = item / p.nqblk;
-    w.split = rest % p.num_splits;
-    rest /= p.num_splits;
-    w.h = rest % p.H;
-    w.b = rest / p.H;
+    const int bh = item / p.nqblk;
+    w.h = bh % p.H;
+    w.b = bh / p.H;
+    const int ntiles = (p.valid[w.b] + kKeyTile - 1) / kKeyTile;
+    if (w.tail < 0) {
+        w.t_begin = 0;
+        w.t_end = ntiles;
+    } else {
+        w.t_begin = w.split * p.tiles_per_split;
+        w.t_end = min(w.t_begin + p.tiles_per_split, ntiles);
+    }
     return w;
 }
 

@@ -66,11 +66,9 @@ void fmha_dma_kernel(const FmhaParams p) {
     const int g = lane >> 5;
 
     const WorkItem wi = work_item(p);
-    const int qblk = wi.qblk, split = wi.split, h = wi.h, b = wi.b;
+    const int qblk = wi.qblk, h = wi.h, b = wi.b;
     const int n_valid = p.valid[b];
-    const int ntiles = (n_valid + KT - 1) / KT;
-    const int t_begin = split * p.tiles_per_split;
-    const int t_end = min(t_begin + p.tiles_per_split, ntiles);
+    const int t_begin = wi.t_begin, t_end = wi.t_end;
     const int q0 = qblk * QT + wave * QW;
     const bool active = q0 < p.Lq;
 
@@ -393,15 +391,19 @@ void fmha_dma_kernel(const FmhaParams p) {
     lt[0] = l[0] + xlane32(l[0]);
     lt[1] = l[1] + xlane32(l[1]);
 
-    if (p.num_splits > 1) {
+    if (wi.tail >= 0) {
+        // Tail split: fp32 partial O (unnormalised), running max and row sum, for the
+        // combine kernel. An empty key range leaves max -inf and sum 0.
         if (!active) return;
         const bool empty = t_begin >= t_end;
-        const int64_t rowbase = (((int64_t)split * p.B + b) * p.H + h) * p.Lq;
+        const int64_t rowbase =
+            ((int64_t)wi.split * (p.n_items - p.n_full) + wi.tail) * QT + wave * QW;
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
             const int q = q0 + 32 * qb + r;
             if (q >= p.Lq) continue;
-            float *po = p.part_o + (rowbase + q) * D;
+            const int64_t row = rowbase + 32 * qb + r;
+            float *po = p.part_o + row * D;
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -412,7 +414,7 @@ void fmha_dma_kernel(const FmhaParams p) {
                     *(f32x4 *)(po + db * 32 + 8 * i4 + 4 * g) = v;
                 }
             if (g == 0) {
-                float *ml = p.part_ml + (rowbase + q) * 2;
+                float *ml = p.part_ml + row * 2;
                 ml[0] = empty ? -INFINITY : m[qb];
                 ml[1] = empty ? 0.f : lt[qb];
             }
@@ -501,7 +503,7 @@ __global__ __launch_bounds__(256) void vt_prep_kernel(const VtParams p) {
 }  // namespace
 
 int launch_fmha_dma(const FmhaParams &p, int D, void *stream) {
-    const dim3 grid(p.total_groups), block(NT);
+    const dim3 grid(p.grid), block(NT);
     hipStream_t st = (hipStream_t)stream;
     if (D == 128) hipLaunchKernelGGL(fmha_dma_kernel<128>, grid, block, 0, st, p);
     else hipLaunchKernelGGL(fmha_dma_kernel<64>, grid, block, 0, st, p);

@@ -76,12 +76,9 @@ void fmha_fwd_kernel(const FmhaParams p) {
     const int g = lane >> 5;
 
     const WorkItem wi = work_item(p);
-    const int qblk = wi.qblk, split = wi.split, h = wi.h, b = wi.b;
-
+    const int qblk = wi.qblk, h = wi.h, b = wi.b;
     const int n_valid = p.valid[b];
-    const int ntiles = (n_valid + KT - 1) / KT;
-    const int t_begin = split * p.tiles_per_split;
-    const int t_end = min(t_begin + p.tiles_per_split, ntiles);
+    const int t_begin = wi.t_begin, t_end = wi.t_end;
 
     const int q0 = qblk * QT + wave * QW;
     const bool active = q0 < p.Lq;
@@ -490,15 +487,19 @@ void fmha_fwd_kernel(const FmhaParams p) {
     lt[0] = l[0] + xlane32(l[0]);
     lt[1] = l[1] + xlane32(l[1]);
 
-    if (p.num_splits > 1) {
+    if (wi.tail >= 0) {
+        // Tail split: fp32 partial O (unnormalised), running max and row sum, for the
+        // combine kernel. An empty key range leaves max -inf and sum 0.
         if (!active) return;
         const bool empty = t_begin >= t_end;
-        const int64_t rowbase = (((int64_t)split * p.B + b) * p.H + h) * p.Lq;
+        const int64_t rowbase =
+            ((int64_t)wi.split * (p.n_items - p.n_full) + wi.tail) * QT + wave * QW;
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
             const int q = q0 + 32 * qb + r;
             if (q >= p.Lq) continue;
-            float *po = p.part_o + (rowbase + q) * D;
+            const int64_t row = rowbase + 32 * qb + r;
+            float *po = p.part_o + row * D;
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -509,7 +510,7 @@ void fmha_fwd_kernel(const FmhaParams p) {
                     *(f32x4 *)(po + db * 32 + 8 * i4 + 4 * g) = v;
                 }
             if (g == 0) {
-                float *ml = p.part_ml + (rowbase + q) * 2;
+                float *ml = p.part_ml + row * 2;
                 ml[0] = empty ? -INFINITY : m[qb];
                 ml[1] = empty ? 0.f : lt[qb];
             }
@@ -635,9 +636,15 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineParams p) {
     constexpr int TPR = D / 4;                 // threads per row (4 channels each)
     constexpr int RPB = 256 / TPR;             // rows per block
     const int tid = threadIdx.x;
-    const int64_t row = (int64_t)blockIdx.x * RPB + tid / TPR;
-    const int64_t rows = (int64_t)p.B * p.H * p.Lq;
+    const int64_t row = (int64_t)blockIdx.x * RPB + tid / TPR;   // (tail item, query in block)
+    const int64_t rows = (int64_t)p.n_tail * QT;
     if (row >= rows) return;
+    const int ti = (int)(row / QT), qi = (int)(row % QT);
+    const int item = p.n_full + ti;
+    const int q = (item % p.nqblk) * QT + qi;
+    if (q >= p.Lq) return;
+    const int bh = item / p.nqblk;
+    const int hh = bh % p.H, b = bh / p.H;
     const int d = 4 * (tid % TPR);
     const int S = p.num_splits;
     float M = -INFINITY;
@@ -652,9 +659,6 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineParams p) {
         acc += w * *(const f32x4 *)(p.part_o + (s * rows + row) * D + d);
     }
     const float inv = 1.0f / den;
-    const int q = (int)(row % p.Lq);
-    const int hb = (int)(row / p.Lq);
-    const int hh = hb % p.H, b = hb / p.H;
     u32x2 w;
     w[0] = pack_bf2(acc[0] * inv, acc[1] * inv);
     w[1] = pack_bf2(acc[2] * inv, acc[3] * inv);
@@ -666,7 +670,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineParams p) {
 
 int launch_fmha(const FmhaParams &p, int D, int kind, void *stream) {
     if (kind == kDma) return launch_fmha_dma(p, D, stream);
-    const dim3 grid(p.total_groups), block(NT);
+    const dim3 grid(p.grid), block(NT);
     hipStream_t st = (hipStream_t)stream;
     const bool k_fused = kind == kRegFused;
     if (D == 128) {
@@ -688,7 +692,7 @@ int launch_prep(const PrepParams &p, int D, void *stream) {
 }
 
 int launch_combine(const CombineParams &p, int D, void *stream) {
-    const int64_t rows = (int64_t)p.B * p.H * p.Lq;
+    const int64_t rows = (int64_t)p.n_tail * QT;
     const int rpb = 256 / (D / 4);
     const dim3 grid((unsigned)((rows + rpb - 1) / rpb)), block(256);
     hipStream_t st = (hipStream_t)stream;

@@ -35,15 +35,18 @@ struct FmhaParams {
     const void *k_cos, *k_sin;       // bf16 [H][Lk][D/2] or null
 
     float qk_scale_log2;             // softmax scale * log2(e), folded into Q
-
     int32_t nqblk;                   // ceil(Lq / 256)
-    int32_t num_splits;              // >= 1
+    // Work items are (batch, head, query block), item = (b*H + h)*nqblk + qblk. Items
+    // [0, n_full) run over all their keys; each of the n_items - n_full tail items is split
+    // into num_splits key ranges of tiles_per_split tiles, whose partial results the combine
+    // kernel merges. The grid is n_full + (n_items - n_full) * num_splits workgroups.
+    int32_t n_items;
+    int32_t n_full;
+    int32_t num_splits;              // >= 1 (tail items only)
     int32_t tiles_per_split;         // key tiles per split
-    int32_t total_groups;            // B * H * num_splits * nqblk
-
-    float *part_o;                   // split-KV partials [S][B][H][Lq][D] fp32 (num_splits > 1)
-    float *part_ml;                  // [S][B][H][Lq][2]: running max (log2 units), row sum
-
+    int32_t grid;
+    float *part_o;                   // tail partials [S][n_tail][256][D] fp32
+    float *part_ml;                  // [S][n_tail][256][2]: running max (log2 units), row sum
     const void *vt;                  // LDS-DMA kernel: bf16 V^T [B][H][D][vt_ld], keys in
                                      // vt_pos order per 64, zero past the valid keys
     int64_t vt_ld;                   // key positions per V^T row (Lk rounded up to 64)
@@ -75,13 +78,14 @@ struct VtParams {
     int32_t valid[kMaxBatch];
 };
 
-// Split-KV combine.
+// Split-KV combine over the tail items' rows.
 struct CombineParams {
     const float *part_o;
     const float *part_ml;
     void *o;
     int64_t o_bs, o_rs, o_hs;
-    int32_t B, H, Lq, num_splits;
+    int32_t H, Lq, nqblk;
+    int32_t n_full, n_tail, num_splits;
 };
 
 // Launchers (fmha_fwd.hip). Return the hipError_t of the launch as int.

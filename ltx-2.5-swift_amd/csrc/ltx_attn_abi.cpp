@@ -33,6 +33,12 @@ bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Workgroups resident at once on an MI355X: 256 CUs, one 256-thread attention workgroup each.
+constexpr int64_t kConcurrentGroups = 256;
+// Charge per extra split of a tail item, in rounds: its fp32 partial O is written and read
+// back by the combine kernel.
+constexpr double kSplitCharge = 0.02;
+
 // Everything ltx_attn_fwd decides from the arguments alone.
 struct Plan {
     bool q_norm = false, k_norm = false;
@@ -43,8 +49,11 @@ struct Plan {
     int64_t vt_ld = 0;         // key positions per V^T row (DMA kernel)
     int nqblk = 0;
     int ntiles_max = 0;
+    int64_t n_items = 0;       // (batch, head, query block) work items
+    int64_t n_full = 0;        // items run whole; the rest are split into key ranges
     int splits = 1;
     int tiles_per_split = 0;
+    int64_t grid = 0;
     // workspace layout (byte offsets)
     size_t off_qrstd = 0, off_krstd = 0, off_kprep = 0, off_vt = 0, off_part_o = 0,
            off_part_ml = 0;
@@ -158,22 +167,42 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
         pl->k_fused = k_work;
     }
 
-    // Split-KV when (batch, head, query block) items alone cannot fill the chip.
-    const int64_t base = (int64_t)B * H * pl->nqblk;
-    int splits = a->num_splits;
-    if (splits == 0) {
-        splits = 1;
-        if (base < 256) {
-            splits = (int)((320 + base - 1) / base);
-            splits = std::min(splits, ltx::kMaxSplits);
-            splits = std::min(splits, std::max(1, pl->ntiles_max / 2));
+    // Work decomposition. 256 workgroups run at once (one per CU). The whole rounds of
+    // items run unsplit; the items of the last, partial round are split into key ranges so
+    // that they finish in a fraction of a round (split-KV, merged by the combine kernel).
+    // A split count S costs ceil(rem*S/256)/S rounds for the rem tail items plus a small
+    // per-split charge for the partial results. A caller-fixed num_splits splits every item.
+    // Calls beyond one argument table of batches (B > kMaxBatch, sliced launches) run whole.
+    const int64_t N = (int64_t)B * H * pl->nqblk;
+    int64_t n_full = N;
+    int splits = 1;
+    if (a->num_splits > 0) {
+        splits = a->num_splits;
+        n_full = 0;
+    } else if (B <= ltx::kMaxBatch) {
+        const int64_t rounds = N / kConcurrentGroups, rem = N - rounds * kConcurrentGroups;
+        if (rem > 0) {
+            double best = 1.0;
+            for (int sp = 2; sp <= ltx::kMaxSplits && sp <= pl->ntiles_max; ++sp) {
+                const double c =
+                    (double)((rem * sp + kConcurrentGroups - 1) / kConcurrentGroups) / sp +
+                    kSplitCharge * (sp - 1);
+                if (c < best - 1e-9) {
+                    best = c;
+                    splits = sp;
+                }
+            }
+            if (splits > 1) n_full = rounds * kConcurrentGroups;
         }
     }
     splits = std::max(1, std::min(splits, pl->ntiles_max));
-    if (B > ltx::kMaxBatch) splits = 1;   // batches beyond one argument table run unsplit
     pl->tiles_per_split = (pl->ntiles_max + splits - 1) / splits;
     pl->splits = (pl->ntiles_max + pl->tiles_per_split - 1) / pl->tiles_per_split;
-    if (base * pl->splits > 0x7fffffff)
+    if (pl->splits == 1) n_full = N;
+    pl->n_items = N;
+    pl->n_full = n_full;
+    pl->grid = n_full + (N - n_full) * pl->splits;
+    if (pl->grid > 0x7fffffff)
         return fail(LTX_ATTN_EUNSUPPORTED, "grid too large");
 
     size_t off = 0;
@@ -193,8 +222,8 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
         pl->off_vt = off;
         off = align_up(off + 2 * (size_t)B * H * D * pl->vt_ld, 256);
     }
-    if (pl->splits > 1) {
-        const size_t rows = (size_t)pl->splits * B * H * a->Lq;
+    if (pl->n_full < pl->n_items) {
+        const size_t rows = (size_t)pl->splits * (pl->n_items - pl->n_full) * ltx::kQueriesPerGroup;
         pl->off_part_o = off;
         off = align_up(off + sizeof(float) * rows * D, 256);
         pl->off_part_ml = off;
@@ -313,10 +342,12 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     }
     fp.qk_scale_log2 = (float)((double)a->scale * 1.4426950408889634);
     fp.nqblk = pl.nqblk;
+    fp.n_items = (int32_t)pl.n_items;
+    fp.n_full = (int32_t)pl.n_full;
     fp.num_splits = pl.splits;
     fp.tiles_per_split = pl.tiles_per_split;
-    fp.total_groups = B * H * pl.splits * pl.nqblk;
-    if (pl.splits > 1) {
+    fp.grid = (int32_t)pl.grid;
+    if (pl.n_full < pl.n_items) {
         fp.part_o = (float *)(ws + pl.off_part_o);
         fp.part_ml = (float *)(ws + pl.off_part_ml);
     }
@@ -335,7 +366,8 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
             sp.o = (char *)a->out + 2 * (int64_t)b0 * a->o_bs;
             if (sp.q_rstd) sp.q_rstd += (int64_t)b0 * a->Lq;
             if (sp.k_rstd) sp.k_rstd += (int64_t)b0 * a->Lk;
-            sp.total_groups = nb * H * pl.splits * pl.nqblk;
+            sp.n_items = sp.n_full = sp.grid = nb * H * pl.nqblk;
+            sp.num_splits = 1;
             if (a->ev_attn_start && b0 == 0)
                 if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_start, (hipStream_t)stream))
                     return fail(LTX_ATTN_EHIP, "event record: %s", hipGetErrorString(e));
@@ -357,11 +389,14 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
             return fail(LTX_ATTN_EHIP, "event record: %s", hipGetErrorString(e));
 
     // 3. split-KV combine
-    if (pl.splits > 1) {
+    if (pl.n_full < pl.n_items) {
         ltx::CombineParams cp{};
         cp.part_o = fp.part_o; cp.part_ml = fp.part_ml;
         cp.o = a->out; cp.o_bs = a->o_bs; cp.o_rs = a->o_rs; cp.o_hs = a->o_hs;
-        cp.B = B; cp.H = H; cp.Lq = a->Lq; cp.num_splits = pl.splits;
+        cp.H = H; cp.Lq = a->Lq; cp.nqblk = pl.nqblk;
+        cp.n_full = (int32_t)pl.n_full;
+        cp.n_tail = (int32_t)(pl.n_items - pl.n_full);
+        cp.num_splits = pl.splits;
         if (int e = ltx::launch_combine(cp, D, stream))
             return fail(LTX_ATTN_EHIP, "combine launch: %s", hipGetErrorString((hipError_t)e));
     }

@@ -305,6 +305,22 @@ def test_c2_text_cross_masked(device, B, valid):
                   {"k_valid_len": valid}, [(0, 64), (3056, 3120)], [0, 13], "c2")
 
 
+@pytest.mark.parametrize("kprep", [L.KPREP_PROLOGUE, L.KPREP_FUSED])
+def test_whole_and_tail_items_ragged(device, kprep):
+    """2 x 32 heads x 9 query blocks = 576 items: two whole rounds of 256 items run over all
+    their keys, the last 64 items (batch 1, heads 24-31) are split into key ranges of 12 tiles
+    and merged by the combine kernel. Batch 1 has 700 valid keys (11 tiles), so three of the
+    four ranges of each of its tail items are empty."""
+    _say(f"whole + tail items, ragged keys, kprep={kprep}")
+    B, H, Lq, Lk, valid = 2, 32, 2100, 3000, [3000, 700]
+    tq, qb = _gpu_bits((B, Lq, H * 128), 0x5EED + 40, device)
+    tk, kb = _gpu_bits((B, Lk, H * 128), 0x5EED + 41, device)
+    tv, vb = _gpu_bits((B, Lk, H * 128), 0x5EED + 42, device)
+    _sample_check(device, tq, tk, tv, H, (qb, kb, vb), {"valid_len": valid},
+                  {"k_valid_len": valid}, [(0, 64), (2036, 2100)], [0, 24, 31],
+                  "whole+tail", kprep=kprep)
+
+
 @pytest.mark.parametrize("direction", ["video_q", "audio_q"])
 def test_c3_cross_modal(device, direction):
     _say(f"c3 cross-modal {direction}")
