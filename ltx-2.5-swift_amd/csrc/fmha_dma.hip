@@ -46,6 +46,38 @@ __device__ __forceinline__ int swz(int row, int u) {
     return UNITS == 16 ? (u ^ (row & 15)) : (u ^ ((row >> 1) & 7));
 }
 
+// S products with VGPR results. The builtin MFMA puts every result of this kernel in AGPRs
+// (the O accumulators need them), so S would reach the softmax through one v_accvgpr_read
+// per element; these are written as inline assembly instead:
+//   mfma_s_first  S = K.Q'^T + C (C = -m)     mfma_s_next  S += K.Q'^T     s_ready  S usable
+// The compiler does not see that they are MFMAs, so the hazards it would pad are handled
+// here and verified on the generated code by check_mfma_hazards.py at build time:
+//   * s_ready after the last product of a chain redefines S behind 20 wait states, so no
+//     instruction the compiler places afterwards (a use, a copy, a spill) touches S while
+//     the MFMA is still writing it; it also keeps C allocated until then, so C is not
+//     overwritten while the first product may still read it. Within a chain S is only the
+//     exactly overlapping SrcC of the next product, which the hardware forwards.
+//   * an input written by VALU needs two wait states before the product reads it: the first
+//     product of a chain (which reads -m, set by VALU) has an s_nop 1 in front; the others
+//     read LDS data, Q (AGPRs, written once) and their own forwarded result. The check
+//     rejects any product that the compiler places closer to a VALU write of an input.
+// Each statement names its registers in an assembly comment for the check.
+__device__ __forceinline__ f32x16 mfma_s_first(bf16x8 a, bf16x8 b, const f32x16 &c) {
+    f32x16 d;
+    asm("; mfma_s %0 src %3\n\ts_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %3"
+        : "=&v"(d) : "v"(a), "a"(b), "v"(c));
+    return d;
+}
+__device__ __forceinline__ void mfma_s_next(f32x16 &acc, bf16x8 a, bf16x8 b) {
+    asm("; mfma_s %0 src %0\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+        : "+v"(acc) : "v"(a), "a"(b));
+}
+__device__ __forceinline__ void s_ready(f32x16 &x, f32x16 &y, const f32x16 &c0,
+                                        const f32x16 &c1) {
+    asm volatile("; s_ready %0 %1\n\ts_nop 7\n\ts_nop 7\n\ts_nop 3"
+                 : "+v"(x), "+v"(y) : "v"(c0), "v"(c1));
+}
+
 // s_waitcnt vmcnt(0), expcnt and lgkmcnt left at their maxima: this wave's copies landed.
 __device__ __forceinline__ void wait_copies() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -74,6 +106,11 @@ void fmha_dma_kernel(const FmhaParams p) {
 
     bf16x8 qf[2][NC];
     load_q<D>(p, b, h, q0, active, r, g, qf);
+    // Q is only an MFMA operand: home it in AGPRs, leaving the VGPRs to S and P.
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) asm volatile("" : "+a"(qf[qb][c]));
 
     // ---- copies HBM -> LDS -----------------------------------------------------------
     const bf16 *Kb = (const bf16 *)p.k + (int64_t)b * p.k_bs + (int64_t)h * p.k_hs;
@@ -141,14 +178,16 @@ void fmha_dma_kernel(const FmhaParams p) {
     }
 
     auto qk_block = [&](const bf16 *Ks, int kb, f32x16 (&sn)[2]) __attribute__((always_inline)) {
-        sn[0] = negm[0];
-        sn[1] = negm[1];
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const bf16x8 a = k_opnd(Ks, kb, c);
-            sn[0] = mfma32(a, qf[0][c], sn[0]);
-            sn[1] = mfma32(a, qf[1][c], sn[1]);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                if (c == 0) sn[qb] = mfma_s_first(a, qf[qb][0], negm[qb]);
+                else mfma_s_next(sn[qb], a, qf[qb][c]);
+            }
         }
+        s_ready(sn[0], sn[1], negm[0], negm[1]);
     };
     auto pv_block = [&](const bf16 *Vs, int kb) __attribute__((always_inline)) {
 #pragma unroll
@@ -222,7 +261,9 @@ void fmha_dma_kernel(const FmhaParams p) {
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
                 if (i < NC) {
-                    sn[qb] = mfma32(a[i], qf[qb][i], i == 0 ? negm[qb] : sn[qb]);
+                    if (i == 0) sn[qb] = mfma_s_first(a[i], qf[qb][i], negm[qb]);
+                    else mfma_s_next(sn[qb], a[i], qf[qb][i]);
+                    if (i == NC - 1 && qb == 1) s_ready(sn[0], sn[1], negm[0], negm[1]);
                 } else {
                     const int j = i - NC;
                     o[j % NDB][qb] = mfma32(a[i], pp[qb][j / NDB], o[j % NDB][qb]);
