@@ -12,9 +12,12 @@
 //     registers, no LDS stores, no transposition in the loop. The 16-byte units of each LDS
 //     row are XOR-swizzled (swz) so the operand reads are free of bank conflicts; a lane
 //     fetches the global unit that belongs at the LDS position the copy writes it to.
-//   * The two K and two V^T buffers are four distinct LDS objects and the steady-state
-//     windows are unrolled by parity, so the compiler sees that the copies in flight never
-//     alias the operand reads and does not wait for them before reading.
+//   * Three K and three V^T buffers (tile % 3): window t reads K(t) and V(t-1) while K(t+2)
+//     and V(t+1) are copied, so a copy has a whole window to land. In the steady state each
+//     wave's copies are spread over the window (one after every fourth product pair) as
+//     inline-assembly loads the compiler does not track; the window waits for this wave's
+//     copies of two windows back (vmcnt) and a barrier makes everyone's visible. The edge
+//     windows use the builtin copies, drained before the steady state begins.
 #include <type_traits>
 
 #include "fmha_device.hpp"
@@ -23,6 +26,7 @@ namespace ltx {
 namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) bf16 lds_bf16;
 
 template <int D>
 struct DmaTile {
@@ -81,6 +85,32 @@ __device__ __forceinline__ void s_ready(f32x16 &x, f32x16 &y, const f32x16 &c0,
 // s_waitcnt vmcnt(0), expcnt and lgkmcnt left at their maxima: this wave's copies landed.
 __device__ __forceinline__ void wait_copies() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// s_waitcnt vmcnt(n) (n < 64), expcnt and lgkmcnt left at their maxima.
+template <int N>
+__device__ __forceinline__ void wait_copies_but() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// A partial copy: the lanes of mask PART move 16 bytes each HBM -> LDS, to M0 + 16*lane. One
+// statement: exec is narrowed for the load and set back to all lanes after it (the
+// steady-state windows run with every lane enabled), so the compiler sees neither a branch
+// nor a memory load (its waits never account for these; the kernel waits for them
+// explicitly). The exec write gives M0 the one wait state the load needs.
+template <int PART, int PARTS>
+__device__ __forceinline__ void copy_part(u32x4 rs, uint32_t lds_byte, int voff) {
+    constexpr int W = 64 / PARTS;
+    constexpr uint64_t mask = (W == 64 ? ~0ull : ((1ull << W) - 1)) << (W * PART);
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_mov_b64 exec, %2\n\t"
+        "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
+        "s_mov_b64 exec, -1"
+        :
+        : "s"(lds_byte), "v"(voff), "s"(mask), "s"(rs)
+        : "m0", "memory");
+}
+
 template <int D>
 __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(1, 1)))
 void fmha_dma_kernel(const FmhaParams p) {
@@ -88,8 +118,10 @@ void fmha_dma_kernel(const FmhaParams p) {
     constexpr int NC = T::NC, NDB = T::NDB, KU = T::KU, VU = T::VU;
     __shared__ __attribute__((aligned(16))) bf16 sK0[T::ELEMS];
     __shared__ __attribute__((aligned(16))) bf16 sK1[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) bf16 sK2[T::ELEMS];
     __shared__ __attribute__((aligned(16))) bf16 sV0[T::ELEMS];
     __shared__ __attribute__((aligned(16))) bf16 sV1[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) bf16 sV2[T::ELEMS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -118,22 +150,31 @@ void fmha_dma_kernel(const FmhaParams p) {
     const int64_t vrow_bytes = p.vt_ld * 2;
     const rsrc_t rvt = make_rsrc((const bf16 *)p.vt + ((int64_t)b * p.H + h) * D * p.vt_ld,
                                  (int64_t)D * vrow_bytes);
-    // K tile t: keys [64t, 64t+64); the resource ends at the last valid key so the rows past
-    // it arrive as zeros.
-    auto copy_k = [&](int tile, bf16 *dst) __attribute__((always_inline)) {
-        const int rows = min(KT, n_valid - tile * KT);
-        const rsrc_t rk = make_rsrc(Kb + (int64_t)tile * KT * p.k_rs, (int64_t)rows * krow_bytes);
+    // K of this (batch, head): the resource ends at the last valid key, so rows past it
+    // arrive as zeros; a tile's offset goes into the per-lane offset.
+    const rsrc_t rkh = make_rsrc(Kb, (int64_t)n_valid * krow_bytes);
+    // The same two resources as four words, for the inline-assembly copies.
+    auto rsrc_words = [&](const void *base, int64_t bytes) __attribute__((always_inline)) {
+        const uint64_t a = (uint64_t)base;
+        const uint32_t n = bytes <= 0 ? 0u : (bytes >= 0x7fffffff ? 0x7fffffffu : (uint32_t)bytes);
+        return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, n, (uint32_t)kRsrcWord3};
+    };
+    const u32x4 rkw = rsrc_words(Kb, (int64_t)n_valid * krow_bytes);
+    const u32x4 rvw = rsrc_words((const bf16 *)p.vt + ((int64_t)b * p.H + h) * D * p.vt_ld,
+                                 (int64_t)D * vrow_bytes);
+    auto copy_k = [&](int tile, lds_bf16 *dst) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < T::K_DMA; ++j) {
             const int blk = wave * T::K_DMA + j;
             const int q = blk * 64 + lane;
             const int row = q / KU, u = swz<KU>(row, q % KU);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void *)(dst + blk * 512), 16,
-                                                     (int)(row * krow_bytes + 16 * u), 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rkh, (lds_void *)(dst + blk * 512), 16,
+                (int)((tile * KT + row) * krow_bytes + 16 * u), 0, 0, 0);
         }
     };
     // V^T tile t: D rows of key positions [64t, 64t+64) (zero past the valid keys).
-    auto copy_v = [&](int tile, bf16 *dst) __attribute__((always_inline)) {
+    auto copy_v = [&](int tile, lds_bf16 *dst) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < T::V_DMA; ++j) {
             const int blk = wave * T::V_DMA + j;
@@ -144,14 +185,29 @@ void fmha_dma_kernel(const FmhaParams p) {
                 (int)(row * vrow_bytes + tile * KT * 2 + 16 * u), 0, 0, 0);
         }
     };
-    // Operand reads: K rows kb*32 + r, unit 2c + g; V^T rows db*32 + r, unit 2*t4 + g.
-    auto k_opnd = [&](const bf16 *Ks, int kb, int c) __attribute__((always_inline)) {
-        const int row = kb * 32 + r;
-        return *(const bf16x8 *)(Ks + row * D + 8 * swz<KU>(row, 2 * c + g));
+    // One 64-unit block of a tile (a tile is K_DMA * NW blocks of K, V_DMA * NW of V^T).
+    auto copy_k_blk = [&](int tile, lds_bf16 *dst, int blk) __attribute__((always_inline)) {
+        const int q = blk * 64 + lane;
+        const int row = q / KU, u = swz<KU>(row, q % KU);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rkh, (lds_void *)(dst + blk * 512), 16,
+            (int)((tile * KT + row) * krow_bytes + 16 * u), 0, 0, 0);
     };
-    auto v_opnd = [&](const bf16 *Vs, int t4, int db) __attribute__((always_inline)) {
+    auto copy_v_blk = [&](int tile, lds_bf16 *dst, int blk) __attribute__((always_inline)) {
+        const int q = blk * 64 + lane;
+        const int row = q / VU, u = swz<VU>(row, q % VU);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rvt, (lds_void *)(dst + blk * 512), 16,
+            (int)(row * vrow_bytes + tile * KT * 2 + 16 * u), 0, 0, 0);
+    };
+    // Operand reads: K rows kb*32 + r, unit 2c + g; V^T rows db*32 + r, unit 2*t4 + g.
+    auto k_opnd = [&](const lds_bf16 *Ks, int kb, int c) __attribute__((always_inline)) {
+        const int row = kb * 32 + r;
+        return *(const __attribute__((address_space(3))) bf16x8 *)(Ks + row * D + 8 * swz<KU>(row, 2 * c + g));
+    };
+    auto v_opnd = [&](const lds_bf16 *Vs, int t4, int db) __attribute__((always_inline)) {
         const int row = db * 32 + r;
-        return *(const bf16x8 *)(Vs + row * KT + 8 * swz<VU>(row, 2 * t4 + g));
+        return *(const __attribute__((address_space(3))) bf16x8 *)(Vs + row * KT + 8 * swz<VU>(row, 2 * t4 + g));
     };
 
     // ---- running state ----------------------------------------------------------------
@@ -177,7 +233,7 @@ void fmha_dma_kernel(const FmhaParams p) {
         pp[qb][0] = pp[qb][1] = __builtin_bit_cast(bf16x8, u32x4{0, 0, 0, 0});
     }
 
-    auto qk_block = [&](const bf16 *Ks, int kb, f32x16 (&sn)[2]) __attribute__((always_inline)) {
+    auto qk_block = [&](const lds_bf16 *Ks, int kb, f32x16 (&sn)[2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const bf16x8 a = k_opnd(Ks, kb, c);
@@ -189,7 +245,7 @@ void fmha_dma_kernel(const FmhaParams p) {
         }
         s_ready(sn[0], sn[1], negm[0], negm[1]);
     };
-    auto pv_block = [&](const bf16 *Vs, int kb) __attribute__((always_inline)) {
+    auto pv_block = [&](const lds_bf16 *Vs, int kb) __attribute__((always_inline)) {
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
@@ -227,7 +283,7 @@ void fmha_dma_kernel(const FmhaParams p) {
     // Steady-state step: the 2*(NC + 2*NDB) products are issued one at a time with a slice of
     // the softmax of S(s) after every other one, and each LDS operand is read three operands
     // ahead; the sched_barrier after each product keeps the compiler from regrouping them.
-    auto fast_step = [&](int s, const bf16 *Kc, const bf16 *Vp) __attribute__((always_inline)) {
+    auto fast_step = [&](int s, const lds_bf16 *Kc, const lds_bf16 *Vp, auto hook) __attribute__((always_inline)) {
         constexpr int NOP = NC + 2 * NDB;              // LDS operands per step
         constexpr int NPAIR = 16;                      // bf16 pairs of P(s) per lane
         constexpr int PER = 2 * NOP <= NPAIR ? NPAIR / (2 * NOP) : (NPAIR + NOP - 1) / NOP;
@@ -268,6 +324,7 @@ void fmha_dma_kernel(const FmhaParams p) {
                     const int j = i - NC;
                     o[j % NDB][qb] = mfma32(a[i], pp[qb][j / NDB], o[j % NDB][qb]);
                 }
+                if (qb == 0) hook(i);
                 if (qb == 1 || 2 * NOP <= NPAIR) slice(PER);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -285,7 +342,7 @@ void fmha_dma_kernel(const FmhaParams p) {
 
     // Edge step: the first block (sets the running max), the ragged last block, and the
     // pipeline's fill and drain, where parts of the step are absent.
-    auto edge_step = [&](int s, const bf16 *Kc, const bf16 *Vp) __attribute__((always_inline)) {
+    auto edge_step = [&](int s, const lds_bf16 *Kc, const lds_bf16 *Vp) __attribute__((always_inline)) {
         const bool do_sm = s >= blk_begin && s < blk_end;
         const bool do_s = s + 1 >= blk_begin && s + 1 < blk_end;
         const bool do_pv = s - 1 >= blk_begin && s - 1 < blk_end;
@@ -332,48 +389,101 @@ void fmha_dma_kernel(const FmhaParams p) {
     };
 
     // ---- main loop --------------------------------------------------------------------
-    if (t_begin < t_end) copy_k(t_begin, (t_begin & 1) ? sK1 : sK0);
+    // Three K and three V^T buffers (tile % 3): window t reads K(t) and V(t-1) while K(t+2)
+    // and V(t+1) are copied, so a copy has a whole window to land and may be issued
+    // anywhere in the window.
+    auto kbuf = [&](int i) __attribute__((always_inline)) {
+        return i == 0 ? (lds_bf16 *)sK0 : i == 1 ? (lds_bf16 *)sK1 : (lds_bf16 *)sK2;
+    };
+    auto vbuf = [&](int i) __attribute__((always_inline)) {
+        return i == 0 ? (lds_bf16 *)sV0 : i == 1 ? (lds_bf16 *)sV1 : (lds_bf16 *)sV2;
+    };
+    if (t_begin < t_end) {
+        copy_k(t_begin, kbuf(t_begin % 3));
+        if (t_begin + 1 < t_end) copy_k(t_begin + 1, kbuf((t_begin + 1) % 3));
+        copy_v(t_begin, vbuf(t_begin % 3));
+    }
     const int t_last = t_begin < t_end ? t_end : t_begin - 1;
-    // Windows [t_begin, tf0) and [tf1, t_last] fill and drain the pipeline (and carry the
-    // first block, the ragged block and the split edges); the windows in between are
-    // straight-line.
-    int tf0 = max(t_begin, (blk_begin + 3) / 2);        // first t with 2t-2 >= blk_begin
-    int tf1 = max(tf0, blk_end / 2);                     // first t with 2t+1 >= blk_end
-    tf0 = min(tf0, t_last + 1);
-    tf1 = min(tf1, t_last + 1);
-    // `par` is t & 1: a compile-time constant in the steady state, a value at the edges.
-    auto window = [&](auto fast, auto par, int t) __attribute__((always_inline)) {
-        const int P = par;
-        bf16 *Kc = P ? sK1 : sK0, *Kn = P ? sK0 : sK1;
-        bf16 *Vc = P ? sV1 : sV0, *Vp = P ? sV0 : sV1;
-        wait_copies();        // this wave's copies of K(t) and V(t-1) have landed
-        __syncthreads();      // everyone's have, and window t-1's reads are done
-        if (t + 1 < t_end) copy_k(t + 1, Kn);
-        if (t < t_end) copy_v(t, Vc);
-        __builtin_amdgcn_sched_barrier(0);
-        if (active) {
-            if constexpr (decltype(fast)::value) {
-                fast_step(2 * t - 1, Kc, Vp);
-                fast_step(2 * t, Kc, Vp);
+    // Steady-state windows: every part of both steps present and both copies of the window
+    // in range; a whole number of triples starting at t = 0 (mod 3), so the buffers of each
+    // are compile-time. The others (fill, drain, ragged block, split edges) are generic.
+    int tf0 = max(t_begin + 1, (blk_begin + 3) / 2);
+    tf0 = (tf0 + 2) / 3 * 3;
+    int tf1 = min(blk_end / 2, t_end - 2);
+    tf1 = tf1 > tf0 ? tf0 + (tf1 - tf0) / 3 * 3 : tf0;
+    const int wave_v = (int)(threadIdx.x >> 6);   // per-lane wave index: tests on it mask lanes
+    auto window = [&](auto fast, auto res, int t) __attribute__((always_inline)) {
+        const int R = res;                          // t % 3
+        lds_bf16 *Kc = kbuf(R), *Kn2 = kbuf((R + 2) % 3);
+        lds_bf16 *Vp = vbuf((R + 2) % 3), *Vn1 = vbuf((R + 1) % 3);
+        if constexpr (decltype(fast)::value) {
+            // This wave's copies of the previous window (K(t+1), V(t)) may still be in
+            // flight; the older ones, K(t) and V(t-1), have landed.
+            wait_copies_but<(NC + 2 * NDB) / 2>();
+            __syncthreads();
+            // The copies go out in halves (32 lanes, 512 bytes), one after every other product
+            // pair of both steps: slot k copies half (k/2)%2 of this wave's block (k/4) of K
+            // (k even) or V^T (k odd).
+            auto slot = [&](int k) __attribute__((always_inline)) {
+                const int j = k >> 1, hf = 0;
+                int voff;
+                const lds_bf16 *dst;
+                u32x4 rs;
+                if ((k & 1) == 0) {
+                    const int blk = wave * T::K_DMA + j;
+                    const int q = blk * 64 + lane;
+                    const int row = q / KU, u = swz<KU>(row, q % KU);
+                    voff = (int)(((t + 2) * KT + row) * krow_bytes + 16 * u);
+                    dst = Kn2 + blk * 512;
+                    rs = rkw;
+                } else {
+                    const int blk = wave * T::V_DMA + j;
+                    const int q = blk * 64 + lane;
+                    const int row = q / VU, u = swz<VU>(row, q % VU);
+                    voff = (int)(row * vrow_bytes + (t + 1) * KT * 2 + 16 * u);
+                    dst = Vn1 + blk * 512;
+                    rs = rvw;
+                }
+                copy_part<0, 1>(rs, (uint32_t)(uintptr_t)dst, voff);
+            };
+            constexpr int NOPS = NC + 2 * NDB;
+            static_assert(NOPS == 4 * (T::K_DMA + T::V_DMA) / 2, "one copy per four product pairs");
+            if (active) {
+                fast_step(2 * t - 1, Kc, Vp, [&](int i) __attribute__((always_inline)) {
+                    if ((i & 3) == 0) slot(i >> 2);
+                });
+                fast_step(2 * t, Kc, Vp, [&](int i) __attribute__((always_inline)) {
+                    if ((i & 3) == 0) slot(NOPS / 4 + (i >> 2));
+                });
             } else {
+#pragma unroll
+                for (int k = 0; k < NOPS / 2; ++k) slot(k);
+            }
+        } else {
+            wait_copies();
+            __syncthreads();
+            if (t + 2 < t_end) copy_k(t + 2, Kn2);
+            if (t + 1 < t_end) copy_v(t + 1, Vn1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (active) {
                 edge_step(2 * t - 1, Kc, Vp);
                 edge_step(2 * t, Kc, Vp);
             }
         }
     };
-    using even = std::integral_constant<int, 0>;
-    using odd = std::integral_constant<int, 1>;
-    for (int t = t_begin; t < tf0; ++t) window(std::false_type{}, t & 1, t);
-    {
-        int t = tf0;
-        if (t < tf1 && (t & 1)) window(std::true_type{}, odd{}, t++);
-        for (; t + 1 < tf1; t += 2) {
-            window(std::true_type{}, even{}, t);
-            window(std::true_type{}, odd{}, t + 1);
-        }
-        if (t < tf1) window(std::true_type{}, even{}, t);
+    using r0 = std::integral_constant<int, 0>;
+    using r1 = std::integral_constant<int, 1>;
+    using r2 = std::integral_constant<int, 2>;
+    for (int t = t_begin; t < tf0 && t <= t_last; ++t) window(std::false_type{}, t % 3, t);
+    // Entering the steady state with no copy of unknown destination in flight lets the
+    // compiler track the remaining ones by buffer (no wait before the operand reads).
+    if (tf0 < tf1) wait_copies();
+    for (int t = tf0; t < tf1; t += 3) {
+        window(std::true_type{}, r0{}, t);
+        window(std::true_type{}, r1{}, t + 1);
+        window(std::true_type{}, r2{}, t + 2);
     }
-    for (int t = tf1; t <= t_last; ++t) window(std::false_type{}, t & 1, t);
+    for (int t = max(tf1, tf0); t <= t_last; ++t) window(std::false_type{}, t % 3, t);
     wait_copies();
 
     // ---- safe pass: only when some wave's running max was outgrown -------------------
@@ -386,8 +496,8 @@ void fmha_dma_kernel(const FmhaParams p) {
         negm[0] = negm[1] = splat16(0.f);
         for (int t = t_begin; t < t_end; ++t) {
             __syncthreads();
-            copy_k(t, sK0);
-            copy_v(t, sV0);
+            copy_k(t, (lds_bf16 *)sK0);
+            copy_v(t, (lds_bf16 *)sV0);
             wait_copies();
             __syncthreads();
             if (!active) continue;
@@ -395,7 +505,7 @@ void fmha_dma_kernel(const FmhaParams p) {
                 const int s = 2 * t + kb;
                 if (s >= blk_end) break;
                 f32x16 sx[2];
-                qk_block(sK0, kb, sx);     // negm is 0 until the first block sets the max
+                qk_block((lds_bf16 *)sK0, kb, sx);     // negm is 0 until the first block sets the max
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int key = 32 * s + 8 * (i >> 2) + 4 * g + (i & 3);
@@ -421,7 +531,7 @@ void fmha_dma_kernel(const FmhaParams p) {
                 softmax_block(sx, pp, ts);
                 l[0] += ts[0];
                 l[1] += ts[1];
-                pv_block(sV0, kb);
+                pv_block((lds_bf16 *)sV0, kb);
             }
         }
     }

@@ -151,13 +151,13 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
     // (prepared by the K prologue when it needs norm/RoPE) and V^T (from the V^T prologue)
     // straight into LDS; each prologue pays one extra read+write of its tensor. A single
     // query block takes the register-staged kernel, fusing K's norm/RoPE into its staging.
-    // The DMA kernel's 32-bit buffer offsets bound a K tile (64 rows) and a V^T head
-    // (D rows of the padded key length); calls past them take the register-staged kernel.
+    // The DMA kernel's 32-bit buffer offsets bound one head's K (Lk rows) and V^T (D rows of
+    // the padded key length); calls past them take the register-staged kernel.
     const bool k_work = pl->k_norm || pl->k_rope;
     const int64_t vt_ld = ((int64_t)a->Lk + ltx::kKeyTile - 1) / ltx::kKeyTile * ltx::kKeyTile;
     const int64_t k_rs_eff = k_work ? (int64_t)H * D : a->k_rs;
     const bool dma_fits = (int64_t)D * vt_ld * 2 < 0x7fffffff &&
-                          (int64_t)ltx::kKeyTile * k_rs_eff * 2 < 0x7fffffff;
+                          (int64_t)a->Lk * k_rs_eff * 2 < 0x7fffffff;
     if (a->kprep == LTX_ATTN_KPREP_PROLOGUE) pl->dma = dma_fits;
     else if (a->kprep == LTX_ATTN_KPREP_AUTO) pl->dma = dma_fits && pl->nqblk >= 2;
     if (pl->dma) {
