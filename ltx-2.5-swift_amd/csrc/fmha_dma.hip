@@ -12,12 +12,14 @@
 //     registers, no LDS stores, no transposition in the loop. The 16-byte units of each LDS
 //     row are XOR-swizzled (swz) so the operand reads are free of bank conflicts; a lane
 //     fetches the global unit that belongs at the LDS position the copy writes it to.
-//   * Three K and three V^T buffers (tile % 3): window t reads K(t) and V(t-1) while K(t+2)
-//     and V(t+1) are copied, so a copy has a whole window to land. In the steady state each
-//     wave's copies are spread over the window (one after every fourth product pair) as
-//     inline-assembly loads the compiler does not track; the window waits for this wave's
-//     copies of two windows back (vmcnt) and a barrier makes everyone's visible. The edge
-//     windows use the builtin copies, drained before the steady state begins.
+//   * Windows of two 64-key tiles (one barrier per 128 keys) over four K and four V^T buffers:
+//     window w reads K(T0), K(T0+1), V(T0-1), V(T0) while the next window's four tiles are
+//     copied into the buffers window w-1 read, so a copy has a whole window to land. In the
+//     steady state each wave's copies are spread over the window (one after every fourth
+//     product pair) as inline-assembly loads the compiler does not track; the next window
+//     waits for them (vmcnt) and a barrier makes everyone's visible. The edge windows use
+//     the builtin copies. The two parities of the steady state are unrolled so every buffer
+//     is a compile-time LDS object.
 #include <type_traits>
 
 #include "fmha_device.hpp"
@@ -119,9 +121,11 @@ void fmha_dma_kernel(const FmhaParams p) {
     __shared__ __attribute__((aligned(16))) bf16 sK0[T::ELEMS];
     __shared__ __attribute__((aligned(16))) bf16 sK1[T::ELEMS];
     __shared__ __attribute__((aligned(16))) bf16 sK2[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) bf16 sK3[T::ELEMS];
     __shared__ __attribute__((aligned(16))) bf16 sV0[T::ELEMS];
     __shared__ __attribute__((aligned(16))) bf16 sV1[T::ELEMS];
     __shared__ __attribute__((aligned(16))) bf16 sV2[T::ELEMS];
+    __shared__ __attribute__((aligned(16))) bf16 sV3[T::ELEMS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -389,101 +393,104 @@ void fmha_dma_kernel(const FmhaParams p) {
     };
 
     // ---- main loop --------------------------------------------------------------------
-    // Three K and three V^T buffers (tile % 3): window t reads K(t) and V(t-1) while K(t+2)
-    // and V(t+1) are copied, so a copy has a whole window to land and may be issued
-    // anywhere in the window.
+    // Windows of two tiles (128 keys), one barrier each. Four K and four V^T buffers, slot =
+    // (tile - t_begin) % 4: window w (first K tile T0 = t_begin + 2w, steps 2*T0-1 ..
+    // 2*T0+2) reads K(T0), K(T0+1), V(T0-1), V(T0) and copies K(T0+2), K(T0+3), V(T0+1),
+    // V(T0+2) for window w+1 into the slots window w-1 read.
     auto kbuf = [&](int i) __attribute__((always_inline)) {
-        return i == 0 ? (lds_bf16 *)sK0 : i == 1 ? (lds_bf16 *)sK1 : (lds_bf16 *)sK2;
+        return i == 0 ? (lds_bf16 *)sK0 : i == 1 ? (lds_bf16 *)sK1
+             : i == 2 ? (lds_bf16 *)sK2 : (lds_bf16 *)sK3;
     };
     auto vbuf = [&](int i) __attribute__((always_inline)) {
-        return i == 0 ? (lds_bf16 *)sV0 : i == 1 ? (lds_bf16 *)sV1 : (lds_bf16 *)sV2;
+        return i == 0 ? (lds_bf16 *)sV0 : i == 1 ? (lds_bf16 *)sV1
+             : i == 2 ? (lds_bf16 *)sV2 : (lds_bf16 *)sV3;
     };
     if (t_begin < t_end) {
-        copy_k(t_begin, kbuf(t_begin % 3));
-        if (t_begin + 1 < t_end) copy_k(t_begin + 1, kbuf((t_begin + 1) % 3));
-        copy_v(t_begin, vbuf(t_begin % 3));
+        copy_k(t_begin, kbuf(0));
+        if (t_begin + 1 < t_end) copy_k(t_begin + 1, kbuf(1));
+        copy_v(t_begin, vbuf(0));
     }
-    const int t_last = t_begin < t_end ? t_end : t_begin - 1;
-    // Steady-state windows: every part of both steps present and both copies of the window
-    // in range; a whole number of triples starting at t = 0 (mod 3), so the buffers of each
-    // are compile-time. The others (fill, drain, ragged block, split edges) are generic.
-    int tf0 = max(t_begin + 1, (blk_begin + 3) / 2);
-    tf0 = (tf0 + 2) / 3 * 3;
-    int tf1 = min(blk_end / 2, t_end - 2);
-    tf1 = tf1 > tf0 ? tf0 + (tf1 - tf0) / 3 * 3 : tf0;
-    const int wave_v = (int)(threadIdx.x >> 6);   // per-lane wave index: tests on it mask lanes
-    auto window = [&](auto fast, auto res, int t) __attribute__((always_inline)) {
-        const int R = res;                          // t % 3
-        lds_bf16 *Kc = kbuf(R), *Kn2 = kbuf((R + 2) % 3);
-        lds_bf16 *Vp = vbuf((R + 2) % 3), *Vn1 = vbuf((R + 1) % 3);
+    // Steps blk_begin-1 .. blk_end (the last one only finishes P.V) in windows of four.
+    const int nwin = t_begin < t_end ? (blk_end - blk_begin + 2 + 3) / 4 : 0;
+    // Steady-state windows: all four steps complete (not the first block, whose step sets
+    // the running max, nor the ragged last one) and all four copies in range.
+    const int lim_s = blk_end - blk_begin - 3;          // window w needs 4w < lim_s
+    const int lim_c = t_end - t_begin - 3;              // and 2w < lim_c
+    const int wf0 = 1;
+    const int wf1 = min(nwin, min(lim_s > 0 ? (lim_s + 3) / 4 : 0, lim_c > 0 ? (lim_c + 1) / 2 : 0));
+    constexpr int NOPS = NC + 2 * NDB;                  // product pairs per step
+    static_assert(NOPS == 2 * (T::K_DMA + T::V_DMA), "one copy per four product pairs");
+    // `par` is w & 1: a compile-time constant in the steady state, a value at the edges.
+    auto window = [&](auto fast, auto par, int w) __attribute__((always_inline)) {
+        const int a = 2 * (int)par;                     // slot of K(T0)
+        const int T0 = t_begin + 2 * w;
+        wait_copies();        // this wave's copies for this window have landed
+        __syncthreads();      // everyone's have, and window w-1's reads are done
         if constexpr (decltype(fast)::value) {
-            // This wave's copies of the previous window (K(t+1), V(t)) may still be in
-            // flight; the older ones, K(t) and V(t-1), have landed.
-            wait_copies_but<(NC + 2 * NDB) / 2>();
-            __syncthreads();
-            // The copies go out in halves (32 lanes, 512 bytes), one after every other product
-            // pair of both steps: slot k copies half (k/2)%2 of this wave's block (k/4) of K
-            // (k even) or V^T (k odd).
-            auto slot = [&](int k) __attribute__((always_inline)) {
-                const int j = k >> 1, hf = 0;
+            // Each wave issues its copies one at a time after every fourth product pair, so
+            // an issue overlaps the running product instead of queueing behind the other
+            // waves' at the start of the window.
+            auto slot = [&](int c) __attribute__((always_inline)) {
                 int voff;
                 const lds_bf16 *dst;
                 u32x4 rs;
-                if ((k & 1) == 0) {
+                if (c < 2 * T::K_DMA) {
+                    const int tt = c / T::K_DMA, j = c % T::K_DMA;
                     const int blk = wave * T::K_DMA + j;
                     const int q = blk * 64 + lane;
                     const int row = q / KU, u = swz<KU>(row, q % KU);
-                    voff = (int)(((t + 2) * KT + row) * krow_bytes + 16 * u);
-                    dst = Kn2 + blk * 512;
+                    voff = (int)(((T0 + 2 + tt) * KT + row) * krow_bytes + 16 * u);
+                    dst = kbuf((a + 2 + tt) & 3) + blk * 512;
                     rs = rkw;
                 } else {
+                    const int c2 = c - 2 * T::K_DMA;
+                    const int tt = c2 / T::V_DMA, j = c2 % T::V_DMA;
                     const int blk = wave * T::V_DMA + j;
                     const int q = blk * 64 + lane;
                     const int row = q / VU, u = swz<VU>(row, q % VU);
-                    voff = (int)(row * vrow_bytes + (t + 1) * KT * 2 + 16 * u);
-                    dst = Vn1 + blk * 512;
+                    voff = (int)(row * vrow_bytes + (T0 + 1 + tt) * KT * 2 + 16 * u);
+                    dst = vbuf((a + 1 + tt) & 3) + blk * 512;
                     rs = rvw;
                 }
                 copy_part<0, 1>(rs, (uint32_t)(uintptr_t)dst, voff);
             };
-            constexpr int NOPS = NC + 2 * NDB;
-            static_assert(NOPS == 4 * (T::K_DMA + T::V_DMA) / 2, "one copy per four product pairs");
             if (active) {
-                fast_step(2 * t - 1, Kc, Vp, [&](int i) __attribute__((always_inline)) {
-                    if ((i & 3) == 0) slot(i >> 2);
-                });
-                fast_step(2 * t, Kc, Vp, [&](int i) __attribute__((always_inline)) {
-                    if ((i & 3) == 0) slot(NOPS / 4 + (i >> 2));
-                });
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    fast_step(2 * T0 - 1 + k, kbuf((a + (k >> 1)) & 3), vbuf((a + 3 + (k >> 1)) & 3),
+                              [&](int i) __attribute__((always_inline)) {
+                                  if ((i & 3) == 0) slot(k * (NOPS / 4) + (i >> 2));
+                              });
             } else {
 #pragma unroll
-                for (int k = 0; k < NOPS / 2; ++k) slot(k);
+                for (int c = 0; c < NOPS; ++c) slot(c);
             }
         } else {
-            wait_copies();
-            __syncthreads();
-            if (t + 2 < t_end) copy_k(t + 2, Kn2);
-            if (t + 1 < t_end) copy_v(t + 1, Vn1);
+            if (T0 + 2 < t_end) copy_k(T0 + 2, kbuf((a + 2) & 3));
+            if (T0 + 3 < t_end) copy_k(T0 + 3, kbuf((a + 3) & 3));
+            if (T0 + 1 < t_end) copy_v(T0 + 1, vbuf((a + 1) & 3));
+            if (T0 + 2 < t_end) copy_v(T0 + 2, vbuf((a + 2) & 3));
             __builtin_amdgcn_sched_barrier(0);
             if (active) {
-                edge_step(2 * t - 1, Kc, Vp);
-                edge_step(2 * t, Kc, Vp);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    edge_step(2 * T0 - 1 + k, kbuf((a + (k >> 1)) & 3), vbuf((a + 3 + (k >> 1)) & 3));
             }
         }
     };
-    using r0 = std::integral_constant<int, 0>;
-    using r1 = std::integral_constant<int, 1>;
-    using r2 = std::integral_constant<int, 2>;
-    for (int t = t_begin; t < tf0 && t <= t_last; ++t) window(std::false_type{}, t % 3, t);
-    // Entering the steady state with no copy of unknown destination in flight lets the
-    // compiler track the remaining ones by buffer (no wait before the operand reads).
-    if (tf0 < tf1) wait_copies();
-    for (int t = tf0; t < tf1; t += 3) {
-        window(std::true_type{}, r0{}, t);
-        window(std::true_type{}, r1{}, t + 1);
-        window(std::true_type{}, r2{}, t + 2);
+    using even = std::integral_constant<int, 0>;
+    using odd = std::integral_constant<int, 1>;
+    int w = 0;
+    for (; w < min(wf0, nwin); ++w) window(std::false_type{}, w & 1, w);
+    if (wf0 < wf1) {                                    // here w == wf0
+        if (w & 1) window(std::true_type{}, odd{}, w++);
+        for (; w + 1 < wf1; w += 2) {
+            window(std::true_type{}, even{}, w);
+            window(std::true_type{}, odd{}, w + 1);
+        }
+        if (w < wf1) window(std::true_type{}, even{}, w++);
     }
-    for (int t = max(tf1, tf0); t <= t_last; ++t) window(std::false_type{}, t % 3, t);
+    for (; w < nwin; ++w) window(std::false_type{}, w & 1, w);
     wait_copies();
 
     // ---- safe pass: only when some wave's running max was outgrown -------------------
