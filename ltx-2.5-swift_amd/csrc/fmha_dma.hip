@@ -1,25 +1,27 @@
-// Attention kernel with K and V^T tiles copied HBM -> LDS by the buffer-load-to-LDS path
+// Attention kernel with K and V tiles copied HBM -> LDS by the buffer-load-to-LDS path
 // (gfx950 `buffer_load_dwordx4 ... lds`), for calls whose K was prepared by the prologue (or
 // needs no preparation) -- every call with two or more query blocks per (batch, head).
 //
 // Same arithmetic as fmha_fwd.hip's register-staged kernel (MFMA mapping, exp2 softmax with
 // the -m accumulator start, 2^64 overflow bound and safe pass, bf16 row sums); what changes
 // is the staging:
-//   * V is transposed once per call by vt_prep_kernel into V^T [B][H][D][ld] with keys in
-//     vt_pos order, so a V^T tile row is 128 contiguous bytes and each MFMA A operand of
-//     O^T = V^T.P^T is one 16-byte LDS read (as for K).
-//   * Each wave copies its share of the next K and V^T tiles straight into LDS; no staging
-//     registers, no LDS stores, no transposition in the loop. The 16-byte units of each LDS
-//     row are XOR-swizzled (swz) so the operand reads are free of bank conflicts; a lane
-//     fetches the global unit that belongs at the LDS position the copy writes it to.
-//   * Windows of two 64-key tiles (one barrier per 128 keys) over four K and four V^T buffers:
+//   * Each wave copies its share of the next K and V tiles straight from the caller's
+//     tensors into LDS, row-major; no staging registers, no LDS stores, no prologue for V.
+//     The 16-byte units of each LDS row are XOR-swizzled (swz for K, vswz for V) so the
+//     operand reads are free of bank conflicts; a lane fetches the global unit that belongs
+//     at the LDS position the copy writes it to.
+//   * K operands of S^T = K.Q'^T are single 16-byte reads; V^T operands of O^T = V^T.P^T
+//     come from two transposing reads (ds_read_b64_tr_b16) that hand each lane four keys of
+//     one channel, in the key order of P's registers.
+//   * Windows of two 64-key tiles (one barrier per 128 keys) over four K and four V buffers:
 //     window w reads K(T0), K(T0+1), V(T0-1), V(T0) while the next window's four tiles are
 //     copied into the buffers window w-1 read, so a copy has a whole window to land. In the
 //     steady state each wave's copies are spread over the window (one after every fourth
-//     product pair) as inline-assembly loads the compiler does not track; the next window
-//     waits for them (vmcnt) and a barrier makes everyone's visible. The edge windows use
-//     the builtin copies. The two parities of the steady state are unrolled so every buffer
-//     is a compile-time LDS object.
+//     product pair). Every copy is inline assembly the compiler does not track (it would
+//     otherwise wait for all copies in flight before each transposing read); the kernel
+//     waits for them itself (vmcnt) at the next window, and a barrier makes everyone's
+//     visible. The two parities of the steady state are unrolled so every buffer is a
+//     compile-time LDS object.
 #include <type_traits>
 
 #include "fmha_device.hpp"
@@ -34,11 +36,10 @@ template <int D>
 struct DmaTile {
     static constexpr int NC = D / 16;                // 16-wide reduction chunks of Q.K^T
     static constexpr int NDB = D / 32;               // 32-row blocks of O^T
-    static constexpr int KU = D / 8;                 // 16-byte units per K row
-    static constexpr int VU = KT / 8;                // 16-byte units per V^T row
-    static constexpr int ELEMS = KT * D;             // a K tile, a V^T tile, one wave's O
+    static constexpr int KU = D / 8;                 // 16-byte units per K or V row
+    static constexpr int ELEMS = KT * D;             // a K tile, a V tile, one wave's O
     static constexpr int K_DMA = KT * KU / 64 / NW;  // copies (64 units each) per wave per tile
-    static constexpr int V_DMA = D * VU / 64 / NW;
+    static constexpr int V_DMA = K_DMA;
     static_assert(K_DMA >= 1 && V_DMA >= 1 && QW * D == ELEMS, "tile geometry");
 };
 
@@ -50,6 +51,22 @@ template <int UNITS>
 __device__ __forceinline__ int swz(int row, int u) {
     static_assert(UNITS == 16 || UNITS == 8, "row width");
     return UNITS == 16 ? (u ^ (row & 15)) : (u ^ ((row >> 1) & 7));
+}
+
+// V tiles stay row-major (key rows of D channels) and are read through the transposing LDS
+// read: 32 lanes of a ds_read_b64_tr_b16 read 4 consecutive rows x 64 bytes, so the units of
+// rows r and r+1..r+3 must fall in distinct bank windows (XOR the unit with row & 3 scaled to
+// a quarter row; rows of 64 channels pair up, so rows r and r+2 differ instead).
+template <int UNITS>
+__device__ __forceinline__ int vswz(int row, int u) {
+    static_assert(UNITS == 16 || UNITS == 8, "row width");
+    return UNITS == 16 ? (u ^ ((row & 3) << 2)) : (u ^ (((row >> 1) & 1) << 2));
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 ds_read_tr(const __attribute__((address_space(3))) bf16 *p) {
+    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4 *)p);
+    return __builtin_bit_cast(u32x2, v);
 }
 
 // S products with VGPR results. The builtin MFMA puts every result of this kernel in AGPRs
@@ -113,11 +130,22 @@ __device__ __forceinline__ void copy_part(u32x4 rs, uint32_t lds_byte, int voff)
         : "m0", "memory");
 }
 
+// A full-wave copy (every lane enabled, as everywhere the kernel copies): 16 bytes per lane.
+__device__ __forceinline__ void copy_all(u32x4 rs, uint32_t lds_byte, int voff) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen lds"
+        :
+        : "s"(lds_byte), "v"(voff), "s"(rs)
+        : "m0", "memory");
+}
+
 template <int D>
 __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(1, 1)))
 void fmha_dma_kernel(const FmhaParams p) {
     using T = DmaTile<D>;
-    constexpr int NC = T::NC, NDB = T::NDB, KU = T::KU, VU = T::VU;
+    constexpr int NC = T::NC, NDB = T::NDB, KU = T::KU;
     __shared__ __attribute__((aligned(16))) bf16 sK0[T::ELEMS];
     __shared__ __attribute__((aligned(16))) bf16 sK1[T::ELEMS];
     __shared__ __attribute__((aligned(16))) bf16 sK2[T::ELEMS];
@@ -151,67 +179,67 @@ void fmha_dma_kernel(const FmhaParams p) {
     // ---- copies HBM -> LDS -----------------------------------------------------------
     const bf16 *Kb = (const bf16 *)p.k + (int64_t)b * p.k_bs + (int64_t)h * p.k_hs;
     const int64_t krow_bytes = p.k_rs * 2;
-    const int64_t vrow_bytes = p.vt_ld * 2;
-    const rsrc_t rvt = make_rsrc((const bf16 *)p.vt + ((int64_t)b * p.H + h) * D * p.vt_ld,
-                                 (int64_t)D * vrow_bytes);
-    // K of this (batch, head): the resource ends at the last valid key, so rows past it
-    // arrive as zeros; a tile's offset goes into the per-lane offset.
-    const rsrc_t rkh = make_rsrc(Kb, (int64_t)n_valid * krow_bytes);
-    // The same two resources as four words, for the inline-assembly copies.
+    const bf16 *Vb = (const bf16 *)p.v + (int64_t)b * p.v_bs + (int64_t)h * p.v_hs;
+    const int64_t vrow_bytes = p.v_rs * 2;
+    // Resources over this (batch, head)'s valid keys: rows past them arrive as zeros; a tile's
+    // offset goes into the per-lane offset.
     auto rsrc_words = [&](const void *base, int64_t bytes) __attribute__((always_inline)) {
         const uint64_t a = (uint64_t)base;
         const uint32_t n = bytes <= 0 ? 0u : (bytes >= 0x7fffffff ? 0x7fffffffu : (uint32_t)bytes);
         return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, n, (uint32_t)kRsrcWord3};
     };
     const u32x4 rkw = rsrc_words(Kb, (int64_t)n_valid * krow_bytes);
-    const u32x4 rvw = rsrc_words((const bf16 *)p.vt + ((int64_t)b * p.H + h) * D * p.vt_ld,
-                                 (int64_t)D * vrow_bytes);
+    const u32x4 rvw = rsrc_words(Vb, (int64_t)n_valid * vrow_bytes);
+    // Copy j of this wave's share of a K (V) tile: the per-lane offset, and the element offset
+    // of the wave's 64 units in the LDS buffer.
+    auto k_src = [&](int tile, int j, int &voff) __attribute__((always_inline)) {
+        const int blk = wave * T::K_DMA + j;
+        const int q = blk * 64 + lane;
+        const int row = q / KU, u = swz<KU>(row, q % KU);
+        voff = (int)((tile * KT + row) * krow_bytes + 16 * u);
+        return blk * 512;
+    };
+    auto v_src = [&](int tile, int j, int &voff) __attribute__((always_inline)) {
+        const int blk = wave * T::V_DMA + j;
+        const int q = blk * 64 + lane;
+        const int row = q / KU, u = vswz<KU>(row, q % KU);
+        voff = (int)((tile * KT + row) * vrow_bytes + 16 * u);
+        return blk * 512;
+    };
     auto copy_k = [&](int tile, lds_bf16 *dst) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < T::K_DMA; ++j) {
-            const int blk = wave * T::K_DMA + j;
-            const int q = blk * 64 + lane;
-            const int row = q / KU, u = swz<KU>(row, q % KU);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rkh, (lds_void *)(dst + blk * 512), 16,
-                (int)((tile * KT + row) * krow_bytes + 16 * u), 0, 0, 0);
+            int voff;
+            const int e = k_src(tile, j, voff);
+            copy_all(rkw, (uint32_t)(uintptr_t)(dst + e), voff);
         }
     };
-    // V^T tile t: D rows of key positions [64t, 64t+64) (zero past the valid keys).
     auto copy_v = [&](int tile, lds_bf16 *dst) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < T::V_DMA; ++j) {
-            const int blk = wave * T::V_DMA + j;
-            const int q = blk * 64 + lane;
-            const int row = q / VU, u = swz<VU>(row, q % VU);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rvt, (lds_void *)(dst + blk * 512), 16,
-                (int)(row * vrow_bytes + tile * KT * 2 + 16 * u), 0, 0, 0);
+            int voff;
+            const int e = v_src(tile, j, voff);
+            copy_all(rvw, (uint32_t)(uintptr_t)(dst + e), voff);
         }
     };
-    // One 64-unit block of a tile (a tile is K_DMA * NW blocks of K, V_DMA * NW of V^T).
-    auto copy_k_blk = [&](int tile, lds_bf16 *dst, int blk) __attribute__((always_inline)) {
-        const int q = blk * 64 + lane;
-        const int row = q / KU, u = swz<KU>(row, q % KU);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rkh, (lds_void *)(dst + blk * 512), 16,
-            (int)((tile * KT + row) * krow_bytes + 16 * u), 0, 0, 0);
-    };
-    auto copy_v_blk = [&](int tile, lds_bf16 *dst, int blk) __attribute__((always_inline)) {
-        const int q = blk * 64 + lane;
-        const int row = q / VU, u = swz<VU>(row, q % VU);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rvt, (lds_void *)(dst + blk * 512), 16,
-            (int)(row * vrow_bytes + tile * KT * 2 + 16 * u), 0, 0, 0);
-    };
-    // Operand reads: K rows kb*32 + r, unit 2c + g; V^T rows db*32 + r, unit 2*t4 + g.
+    // Operand reads. K: rows kb*32 + r, unit 2c + g.
     auto k_opnd = [&](const lds_bf16 *Ks, int kb, int c) __attribute__((always_inline)) {
         const int row = kb * 32 + r;
         return *(const __attribute__((address_space(3))) bf16x8 *)(Ks + row * D + 8 * swz<KU>(row, 2 * c + g));
     };
+    // V^T operand of keys 16*t4 .. +15, channels 32*db .. +31, in the key order of P's
+    // registers (lane (r, g): keys 16*t4 + 4g + 0..3, then + 8). Lane i of each 16-lane group
+    // reads 4 channels of key row 16*t4 + 4g + i/4 (then + 8); the transpose hands every lane
+    // 4 keys of channel 32*db + r.
+    const int i16 = lane & 15;
+    const int hsel = (lane >> 4) & 1;
     auto v_opnd = [&](const lds_bf16 *Vs, int t4, int db) __attribute__((always_inline)) {
-        const int row = db * 32 + r;
-        return *(const __attribute__((address_space(3))) bf16x8 *)(Vs + row * KT + 8 * swz<VU>(row, 2 * t4 + g));
+        const int row0 = 16 * t4 + 4 * g + (i16 >> 2);
+        const int u = 4 * db + 2 * hsel + ((i16 & 3) >> 1);
+        const int half = 4 * (i16 & 1);
+        const u32x2 lo = ds_read_tr(Vs + row0 * D + 8 * vswz<KU>(row0, u) + half);
+        const u32x2 hi = ds_read_tr(Vs + (row0 + 8) * D + 8 * vswz<KU>(row0 + 8, u) + half);
+        return __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
     };
 
     // ---- running state ----------------------------------------------------------------
@@ -224,8 +252,7 @@ void fmha_dma_kernel(const FmhaParams p) {
 
     // Software pipeline over 32-key blocks (block s = keys [32s, 32s+32) of tile s/2):
     // step s issues S(s+1) = K.Q'^T - m and O += V^T.P(s-1) on the matrix cores while the
-    // VALU turns S(s) into P(s). Window t = steps {2t-1, 2t} reads K(t) and V(t-1) and copies
-    // K(t+1) and V(t) into the other buffers; one barrier per window.
+    // VALU turns S(s) into P(s). Steps 2t-1 and 2t read K(t) and V(t-1).
     const int blk_begin = 2 * t_begin;
     const int blk_end = min(2 * t_end, (n_valid + 31) / 32);
     const bool ragged = (n_valid & 31) != 0;   // block blk_end-1 is partly padding
@@ -393,7 +420,7 @@ void fmha_dma_kernel(const FmhaParams p) {
     };
 
     // ---- main loop --------------------------------------------------------------------
-    // Windows of two tiles (128 keys), one barrier each. Four K and four V^T buffers, slot =
+    // Windows of two tiles (128 keys), one barrier each. Four K and four V buffers, slot =
     // (tile - t_begin) % 4: window w (first K tile T0 = t_begin + 2w, steps 2*T0-1 ..
     // 2*T0+2) reads K(T0), K(T0+1), V(T0-1), V(T0) and copies K(T0+2), K(T0+3), V(T0+1),
     // V(T0+2) for window w+1 into the slots window w-1 read.
@@ -431,28 +458,22 @@ void fmha_dma_kernel(const FmhaParams p) {
             // an issue overlaps the running product instead of queueing behind the other
             // waves' at the start of the window.
             auto slot = [&](int c) __attribute__((always_inline)) {
-                int voff;
+                int voff, e;
                 const lds_bf16 *dst;
                 u32x4 rs;
                 if (c < 2 * T::K_DMA) {
-                    const int tt = c / T::K_DMA, j = c % T::K_DMA;
-                    const int blk = wave * T::K_DMA + j;
-                    const int q = blk * 64 + lane;
-                    const int row = q / KU, u = swz<KU>(row, q % KU);
-                    voff = (int)(((T0 + 2 + tt) * KT + row) * krow_bytes + 16 * u);
-                    dst = kbuf((a + 2 + tt) & 3) + blk * 512;
+                    const int tt = c / T::K_DMA;
+                    e = k_src(T0 + 2 + tt, c % T::K_DMA, voff);
+                    dst = kbuf((a + 2 + tt) & 3);
                     rs = rkw;
                 } else {
                     const int c2 = c - 2 * T::K_DMA;
-                    const int tt = c2 / T::V_DMA, j = c2 % T::V_DMA;
-                    const int blk = wave * T::V_DMA + j;
-                    const int q = blk * 64 + lane;
-                    const int row = q / VU, u = swz<VU>(row, q % VU);
-                    voff = (int)(row * vrow_bytes + (T0 + 1 + tt) * KT * 2 + 16 * u);
-                    dst = vbuf((a + 1 + tt) & 3) + blk * 512;
+                    const int tt = c2 / T::V_DMA;
+                    e = v_src(T0 + 1 + tt, c2 % T::V_DMA, voff);
+                    dst = vbuf((a + 1 + tt) & 3);
                     rs = rvw;
                 }
-                copy_part<0, 1>(rs, (uint32_t)(uintptr_t)dst, voff);
+                copy_part<0, 1>(rs, (uint32_t)(uintptr_t)(dst + e), voff);
             };
             if (active) {
 #pragma unroll
@@ -614,50 +635,6 @@ void fmha_dma_kernel(const FmhaParams p) {
     }
 }
 
-// ------------------------------------------------------------------------------------------
-// V^T prologue: one workgroup per (batch, head, 64-key tile). The tile goes through LDS so
-// both the reads (key rows of D channels) and the writes (channel rows of 64 key positions)
-// are whole 16-byte units. Keys at or past the valid length are written as zeros, so padded
-// positions contribute 0 * 0 to P.V.
-// ------------------------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(256) void vt_prep_kernel(const VtParams p) {
-    constexpr int U = D / 8;                  // 16-byte units per V row
-    constexpr int RS = D + 8;                 // LDS row stride (elements)
-    __shared__ __attribute__((aligned(16))) bf16 tile[KT * RS];
-    const int tid = threadIdx.x;
-    const int t = blockIdx.x % p.ntiles;
-    const int bh = blockIdx.x / p.ntiles;
-    const int h = bh % p.H, b = bh / p.H;
-    const int n_valid = p.masked ? p.valid[b] : p.Lk;
-    const bf16 *Vb = (const bf16 *)p.v + (int64_t)b * p.v_bs + (int64_t)h * p.v_hs;
-#pragma unroll
-    for (int i = 0; i < KT * U / 256; ++i) {
-        const int unit = tid + 256 * i;
-        const int row = unit / U, u = unit % U;
-        const int key = t * KT + row;
-        u32x4 w = {0u, 0u, 0u, 0u};
-        if (key < n_valid) w = ldg16(Vb + (int64_t)key * p.v_rs + 8 * u);
-        *(u32x4 *)(tile + row * RS + 8 * u) = w;
-    }
-    __syncthreads();
-    const uint16_t *tb = (const uint16_t *)tile;
-    bf16 *Out = (bf16 *)p.vt + ((int64_t)b * p.H + h) * D * p.ld + (int64_t)t * KT;
-#pragma unroll
-    for (int i = 0; i < D * (KT / 8) / 256; ++i) {
-        const int unit = tid + 256 * i;
-        const int d = unit / (KT / 8), c = unit % (KT / 8);
-        u32x4 w;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t lo = tb[vt_pos(8 * c + 2 * j) * RS + d];
-            const uint32_t hi = tb[vt_pos(8 * c + 2 * j + 1) * RS + d];
-            w[j] = lo | (hi << 16);
-        }
-        *(u32x4 *)(Out + (int64_t)d * p.ld + 8 * c) = w;
-    }
-}
-
 }  // namespace
 
 int launch_fmha_dma(const FmhaParams &p, int D, void *stream) {
@@ -665,14 +642,6 @@ int launch_fmha_dma(const FmhaParams &p, int D, void *stream) {
     hipStream_t st = (hipStream_t)stream;
     if (D == 128) hipLaunchKernelGGL(fmha_dma_kernel<128>, grid, block, 0, st, p);
     else hipLaunchKernelGGL(fmha_dma_kernel<64>, grid, block, 0, st, p);
-    return (int)hipGetLastError();
-}
-
-int launch_vt(const VtParams &p, int D, void *stream) {
-    const dim3 grid((unsigned)((int64_t)p.B * p.H * p.ntiles)), block(256);
-    hipStream_t st = (hipStream_t)stream;
-    if (D == 128) hipLaunchKernelGGL(vt_prep_kernel<128>, grid, block, 0, st, p);
-    else hipLaunchKernelGGL(vt_prep_kernel<64>, grid, block, 0, st, p);
     return (int)hipGetLastError();
 }
 

@@ -16,7 +16,7 @@ constexpr int kMaxSplits = 16;
 
 // Main attention kernel.
 struct FmhaParams {
-    const void *q, *k, *v;           // bf16 (v unused by the LDS-DMA kernel, which reads vt)
+    const void *q, *k, *v;           // bf16
     int64_t q_bs, q_rs, q_hs;
     int64_t k_bs, k_rs, k_hs;
     int64_t v_bs, v_rs, v_hs;
@@ -47,9 +47,6 @@ struct FmhaParams {
     int32_t grid;
     float *part_o;                   // tail partials [S][n_tail][256][D] fp32
     float *part_ml;                  // [S][n_tail][256][2]: running max (log2 units), row sum
-    const void *vt;                  // LDS-DMA kernel: bf16 V^T [B][H][D][vt_ld], keys in
-                                     // vt_pos order per 64, zero past the valid keys
-    int64_t vt_ld;                   // key positions per V^T row (Lk rounded up to 64)
     int32_t valid[kMaxBatch];        // keys valid per batch row (Lk when unmasked)
 };
 
@@ -66,18 +63,6 @@ struct PrepParams {
     void *out;                       // bf16 [B][L][H*D] contiguous or null
 };
 
-// V^T prologue of the LDS-DMA kernel: V [B][Lk][H][D] (strided) -> bf16 [B][H][D][ld].
-struct VtParams {
-    const void *v;
-    int64_t v_bs, v_rs, v_hs;
-    int32_t B, H, Lk;
-    int32_t ntiles;                  // ld / 64
-    int64_t ld;
-    void *vt;
-    int32_t masked;                  // valid[] applies (B <= kMaxBatch); else every key is valid
-    int32_t valid[kMaxBatch];
-};
-
 // Split-KV combine over the tail items' rows.
 struct CombineParams {
     const float *part_o;
@@ -92,11 +77,10 @@ struct CombineParams {
 // Attention kernels:
 //   kRegPlain  K and V staged through registers (V transposed on the way into LDS)
 //   kRegFused  the same, with QK-RMSNorm + RoPE applied to K while staging
-//   kDma       K (prepared or raw) and V^T (from the V^T prologue) copied HBM -> LDS by the
-//              buffer-load-to-LDS path; no staging registers
+//   kDma       K (prepared or raw) and V copied HBM -> LDS by the buffer-load-to-LDS path;
+//              no staging registers
 enum KernelKind { kRegPlain = 0, kRegFused = 1, kDma = 2 };
 int launch_fmha(const FmhaParams &p, int D, int kind, void *stream);
-int launch_vt(const VtParams &p, int D, void *stream);
 int launch_fmha_dma(const FmhaParams &p, int D, void *stream);   // fmha_dma.hip
 int launch_prep(const PrepParams &p, int D, void *stream);
 int launch_combine(const CombineParams &p, int D, void *stream);

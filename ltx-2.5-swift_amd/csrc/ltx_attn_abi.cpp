@@ -43,10 +43,9 @@ constexpr double kSplitCharge = 0.02;
 struct Plan {
     bool q_norm = false, k_norm = false;
     bool q_rope = false, k_rope = false;
-    bool dma = false;          // LDS-DMA kernel (V^T prologue; K prologue when K needs work)
+    bool dma = false;          // LDS-DMA kernel (K prologue when K needs work)
     bool k_prologue = false;   // K normalised/rotated by a separate pass into the workspace
     bool k_fused = false;      // K normalised/rotated while staging into LDS
-    int64_t vt_ld = 0;         // key positions per V^T row (DMA kernel)
     int nqblk = 0;
     int ntiles_max = 0;
     int64_t n_items = 0;       // (batch, head, query block) work items
@@ -55,8 +54,7 @@ struct Plan {
     int tiles_per_split = 0;
     int64_t grid = 0;
     // workspace layout (byte offsets)
-    size_t off_qrstd = 0, off_krstd = 0, off_kprep = 0, off_vt = 0, off_part_o = 0,
-           off_part_ml = 0;
+    size_t off_qrstd = 0, off_krstd = 0, off_kprep = 0, off_part_o = 0, off_part_ml = 0;
     size_t bytes = 0;
 };
 
@@ -148,24 +146,19 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
     }
 
     // Kernel: with two or more query blocks per (batch, head) the LDS-DMA kernel reads K
-    // (prepared by the K prologue when it needs norm/RoPE) and V^T (from the V^T prologue)
-    // straight into LDS; each prologue pays one extra read+write of its tensor. A single
-    // query block takes the register-staged kernel, fusing K's norm/RoPE into its staging.
-    // The DMA kernel's 32-bit buffer offsets bound one head's K (Lk rows) and V^T (D rows of
-    // the padded key length); calls past them take the register-staged kernel.
+    // (prepared by the K prologue when it needs norm/RoPE, one extra read+write of K) and V
+    // straight into LDS. A single query block takes the register-staged kernel, fusing K's
+    // norm/RoPE into its staging. The DMA kernel addresses one head's K and V rows with
+    // 32-bit byte offsets up to the key length padded to whole tiles; calls past that take
+    // the register-staged kernel.
     const bool k_work = pl->k_norm || pl->k_rope;
-    const int64_t vt_ld = ((int64_t)a->Lk + ltx::kKeyTile - 1) / ltx::kKeyTile * ltx::kKeyTile;
+    const int64_t lk_pad = ((int64_t)a->Lk + ltx::kKeyTile - 1) / ltx::kKeyTile * ltx::kKeyTile;
     const int64_t k_rs_eff = k_work ? (int64_t)H * D : a->k_rs;
-    const bool dma_fits = (int64_t)D * vt_ld * 2 < 0x7fffffff &&
-                          (int64_t)a->Lk * k_rs_eff * 2 < 0x7fffffff;
+    const bool dma_fits = lk_pad * k_rs_eff * 2 < 0x7fffffff && lk_pad * a->v_rs * 2 < 0x7fffffff;
     if (a->kprep == LTX_ATTN_KPREP_PROLOGUE) pl->dma = dma_fits;
     else if (a->kprep == LTX_ATTN_KPREP_AUTO) pl->dma = dma_fits && pl->nqblk >= 2;
-    if (pl->dma) {
-        pl->k_prologue = k_work;
-        pl->vt_ld = vt_ld;
-    } else {
-        pl->k_fused = k_work;
-    }
+    if (pl->dma) pl->k_prologue = k_work;
+    else pl->k_fused = k_work;
 
     // Work decomposition. 256 workgroups run at once (one per CU). The whole rounds of
     // items run unsplit; the items of the last, partial round are split into key ranges so
@@ -217,10 +210,6 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
     if (pl->k_prologue) {
         pl->off_kprep = off;
         off = align_up(off + 2 * (size_t)B * a->Lk * H * D, 256);
-    }
-    if (pl->dma) {
-        pl->off_vt = off;
-        off = align_up(off + 2 * (size_t)B * H * D * pl->vt_ld, 256);
     }
     if (pl->n_full < pl->n_items) {
         const size_t rows = (size_t)pl->splits * (pl->n_items - pl->n_full) * ltx::kQueriesPerGroup;
@@ -305,19 +294,6 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
         }
     }
 
-    if (pl.dma) {
-        ltx::VtParams vp{};
-        vp.v = a->v; vp.v_bs = a->v_bs; vp.v_rs = a->v_rs; vp.v_hs = a->v_hs;
-        vp.B = B; vp.H = H; vp.Lk = a->Lk;
-        vp.ld = pl.vt_ld;
-        vp.ntiles = (int32_t)(pl.vt_ld / ltx::kKeyTile);
-        vp.vt = ws + pl.off_vt;
-        vp.masked = a->k_valid_len != nullptr;
-        if (a->k_valid_len)
-            for (int b = 0; b < B; ++b) vp.valid[b] = a->k_valid_len[b];
-        if (int e = ltx::launch_vt(vp, D, stream))
-            return fail(LTX_ATTN_EHIP, "v prologue launch: %s", hipGetErrorString((hipError_t)e));
-    }
     const int kind = pl.dma ? ltx::kDma : pl.k_fused ? ltx::kRegFused : ltx::kRegPlain;
 
     // 2. attention
@@ -335,10 +311,6 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
             fp.k_cos = a->k_cos ? a->k_cos : a->q_cos;
             fp.k_sin = a->k_sin ? a->k_sin : a->q_sin;
         }
-    }
-    if (pl.dma) {
-        fp.vt = ws + pl.off_vt;
-        fp.vt_ld = pl.vt_ld;
     }
     fp.qk_scale_log2 = (float)((double)a->scale * 1.4426950408889634);
     fp.nqblk = pl.nqblk;
@@ -362,7 +334,6 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
             sp.q = (const char *)a->q + 2 * (int64_t)b0 * a->q_bs;
             sp.k = (const char *)kptr + 2 * (int64_t)b0 * k_bs;
             sp.v = (const char *)a->v + 2 * (int64_t)b0 * a->v_bs;
-            if (pl.dma) sp.vt = (const char *)fp.vt + 2 * (int64_t)b0 * H * D * pl.vt_ld;
             sp.o = (char *)a->out + 2 * (int64_t)b0 * a->o_bs;
             if (sp.q_rstd) sp.q_rstd += (int64_t)b0 * a->Lq;
             if (sp.k_rstd) sp.k_rstd += (int64_t)b0 * a->Lk;
@@ -418,7 +389,7 @@ const char *ltx_attn_last_error(void) { return g_err; }
 
 const char *ltx_attn_provenance(void) {
     return "hip-gfx950 fused flash attention v2 (bf16 mfma_f32_32x32x16, online fp32 softmax, "
-           "QK-RMSNorm+RoPE fused; K/V^T tiles by LDS DMA for multi-block queries)";
+           "QK-RMSNorm+RoPE fused; K/V tiles by LDS DMA for multi-block queries)";
 }
 
 int32_t ltx_attn_abi_version(void) { return LTX_ATTN_ABI_VERSION; }

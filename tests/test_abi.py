@@ -85,7 +85,7 @@ def test_valid_arguments_pass():
     # blocks = 256): no workspace
     st, msg = _validate(_args(Lq=2048, kprep=L.KPREP_FUSED, ws=False))
     assert st == L.OK, msg
-    # LDS-DMA kernel: the V^T buffer must be provided
+    # LDS-DMA kernel over 13 query blocks: the tail split's partials must be provided
     st, msg = _validate(_args(ws=False))
     assert st == L.EWORKSPACE, msg
     st, msg = _validate(_args())
@@ -149,30 +149,28 @@ def test_key_padding_rules():
 
 def test_workspace_sizing_and_check():
     lib = L.load_library()
-    # plain attention over 13 query blocks: the LDS-DMA kernel's V^T (keys padded to 64),
-    # and the tail split: 416 items = one whole round of 256 + 160 items split into 3 key
+    # plain attention over 13 query blocks (LDS-DMA kernel, which reads K and V in place):
+    # the tail split only, 416 items = one whole round of 256 + 160 items split into 3 key
     # ranges of 17 tiles, each partial row 128 fp32 + (max, sum)
-    vt3120 = 2 * 32 * 128 * 3136
     rows = 3 * 160 * 256
     tail3120 = rows * 128 * 4 + rows * 2 * 4
     a = _args(ws=False)
-    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == vt3120 + tail3120
-    # the register-staged kernel: the same tail split, no V^T
+    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == tail3120
+    # the register-staged kernel: the same tail split
     a = _args(kprep=L.KPREP_FUSED, ws=False)
     assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == tail3120
     # whole rounds only (256 items): nothing
     a = _args(Lq=2048, kprep=L.KPREP_FUSED, ws=False)
     assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == 0
-    # 12480-token self-attention with norm + RoPE: q statistic + prepared K + V^T + the tail
+    # 12480-token self-attention with norm + RoPE: q statistic + prepared K + the tail
     # split (1568 items = 6 rounds of 256 + 32 items split into 7 ranges of 28 tiles)
     a = _args(Lq=12480, Lk=12480, q_norm_w=FAKE, k_norm_w=FAKE, q_cos=FAKE, q_sin=FAKE,
               ws=False)
     need = lib.ltx_attn_workspace_bytes(ctypes.byref(a))
     rstd = (12480 * 4 + 255) // 256 * 256
     kprep = (12480 * 4096 * 2 + 255) // 256 * 256
-    vt = 2 * 32 * 128 * 12480
     rows = 7 * 32 * 256
-    assert need == rstd + kprep + vt + rows * 128 * 4 + rows * 2 * 4
+    assert need == rstd + kprep + rows * 128 * 4 + rows * 2 * 4
     st, msg = _validate(a)
     assert st == L.EWORKSPACE and str(need) in msg
     a.workspace, a.workspace_bytes = FAKE, need - 1
@@ -184,7 +182,15 @@ def test_workspace_sizing_and_check():
     # fused K strategy: the statistics and the tail split
     a = _args(Lq=12480, Lk=12480, q_norm_w=FAKE, k_norm_w=FAKE, q_cos=FAKE, q_sin=FAKE,
               kprep=L.KPREP_FUSED)
-    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == 2 * rstd + rows * 128 * 4 + rows * 2 * 4
+    fused = 2 * rstd + rows * 128 * 4 + rows * 2 * 4
+    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == fused
+    # V rows too far apart for the LDS-DMA kernel's 32-bit offsets (12480 padded rows of
+    # 262144 bytes): the register-staged kernel takes the call, with its fused K work
+    a = _args(Lq=12480, Lk=12480, q_norm_w=FAKE, k_norm_w=FAKE, q_cos=FAKE, q_sin=FAKE,
+              v_rs=131072, v_bs=12480 * 131072)
+    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == fused
+    a.v_rs = 65536                          # 12480 * 131072 bytes fit: back to the DMA kernel
+    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == need
     # 126 audio queries over 3120 video keys (49 key tiles): split-KV partials for every
     # (head, query block) item, 256 rows each; 8 requested splits become 7 splits of 7 tiles
     # (no split is left empty)
