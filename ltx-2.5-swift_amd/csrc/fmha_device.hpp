@@ -35,6 +35,21 @@ __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// acc + both bf16 values of a packed pair, as two fp32 adds (a bf16 value is the fp32 value
+// with the same upper half). Row sums use this rather than v_dot2_f32_bf16 with (1, 1), which
+// is exact too but holds up the matrix cores' instruction stream several times longer.
+__device__ __forceinline__ float add_bf2(float acc, uint32_t w) {
+    return (acc + bf_lo(w)) + bf_hi(w);
+}
+
+// pack_bf2 whose result the compiler treats as opaque: it would otherwise rebuild the low
+// half for add_bf2 with a second conversion instead of shifting the packed word.
+__device__ __forceinline__ uint32_t pack_bf2_opaque(float a, float b) {
+    uint32_t w = pack_bf2(a, b);
+    asm volatile("" : "+v"(w));
+    return w;
+}
+
 __device__ __forceinline__ void unpack8(const u32x4 w, float f[8]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

@@ -72,7 +72,8 @@ __device__ __forceinline__ u32x2 ds_read_tr(const __attribute__((address_space(3
 // S products with VGPR results. The builtin MFMA puts every result of this kernel in AGPRs
 // (the O accumulators need them), so S would reach the softmax through one v_accvgpr_read
 // per element; these are written as inline assembly instead:
-//   mfma_s_first  S = K.Q'^T + C (C = -m)     mfma_s_next  S += K.Q'^T     s_ready  S usable
+//   mfma_s_first  S = K.Q'^T + C (C = -m)     mfma_s_next  S += K.Q'^T
+//   s_ready / s_defined  S usable from here on
 // The compiler does not see that they are MFMAs, so the hazards it would pad are handled
 // here and verified on the generated code by check_mfma_hazards.py at build time:
 //   * s_ready after the last product of a chain redefines S behind 20 wait states, so no
@@ -80,6 +81,8 @@ __device__ __forceinline__ u32x2 ds_read_tr(const __attribute__((address_space(3
 //     the MFMA is still writing it; it also keeps C allocated until then, so C is not
 //     overwritten while the first product may still read it. Within a chain S is only the
 //     exactly overlapping SrcC of the next product, which the hardware forwards.
+//   * s_defined is the same statement without the padding, for the steady-state step, which
+//     places it after the P.V products: the instructions in between are the wait states.
 //   * an input written by VALU needs two wait states before the product reads it: the first
 //     product of a chain (which reads -m, set by VALU) has an s_nop 1 in front; the others
 //     read LDS data, Q (AGPRs, written once) and their own forwarded result. The check
@@ -99,6 +102,10 @@ __device__ __forceinline__ void s_ready(f32x16 &x, f32x16 &y, const f32x16 &c0,
                                         const f32x16 &c1) {
     asm volatile("; s_ready %0 %1\n\ts_nop 7\n\ts_nop 7\n\ts_nop 3"
                  : "+v"(x), "+v"(y) : "v"(c0), "v"(c1));
+}
+__device__ __forceinline__ void s_defined(f32x16 &x, f32x16 &y, const f32x16 &c0,
+                                          const f32x16 &c1) {
+    asm volatile("; s_defined %0 %1" : "+v"(x), "+v"(y) : "v"(c0), "v"(c1));
 }
 
 // s_waitcnt vmcnt(0), expcnt and lgkmcnt left at their maxima: this wave's copies landed.
@@ -289,7 +296,6 @@ void fmha_dma_kernel(const FmhaParams p) {
     // S(s) -> P(s) (bf16) and this lane's row-sum share ts.
     auto softmax_block = [&](const f32x16 (&sx)[2], bf16x8 (&pn)[2][2], float (&ts)[2])
         __attribute__((always_inline)) {
-        const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
         ts[0] = ts[1] = 0.f;
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -298,12 +304,9 @@ void fmha_dma_kernel(const FmhaParams p) {
                 u32x4 w;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const bf16x2 pr = {(bf16)__builtin_amdgcn_exp2f(sx[qb][8 * hf + 2 * e]),
-                                       (bf16)__builtin_amdgcn_exp2f(sx[qb][8 * hf + 2 * e + 1])};
-                    // Each pair feeds fdot2 as its own value (extracting it back out of the
-                    // packed vector has been miscompiled into a reuse of the first pair).
-                    ts[qb] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ts[qb], false);
-                    w[e] = __builtin_bit_cast(uint32_t, pr);
+                    w[e] = pack_bf2_opaque(__builtin_amdgcn_exp2f(sx[qb][8 * hf + 2 * e]),
+                                    __builtin_amdgcn_exp2f(sx[qb][8 * hf + 2 * e + 1]));
+                    ts[qb] = add_bf2(ts[qb], w[e]);
                 }
                 pn[qb][hf] = __builtin_bit_cast(bf16x8, w);
             }
@@ -324,7 +327,6 @@ void fmha_dma_kernel(const FmhaParams p) {
             const int j = i - NC;
             return v_opnd(Vp, 2 * kbp + j / NDB, j % NDB);
         };
-        const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
         float ts[2] = {0.f, 0.f};
         u32x4 w[2][2];
         f32x16 sn[2];
@@ -332,14 +334,29 @@ void fmha_dma_kernel(const FmhaParams p) {
         a[0] = opnd(0);
         a[1] = opnd(1);
         a[2] = opnd(2);
-        int pair = 0;
+        // Softmax of S(s) as a three-stage pipeline over bf16 pairs: slice k takes the exps
+        // of its pairs, packs the previous slice's and adds the one before that to the row
+        // sums, so no stage waits for the result of an instruction just issued.
+        float ex[NPAIR][2];
+        uint32_t pk[NPAIR];
+        int pe = 0, pc = 0, pd = 0;
+        auto stage_c = [&](int n) __attribute__((always_inline)) {
+            for (int k = 0; k < n && pc < pe; ++k, ++pc) {
+                const int qb = pc >> 3, hf = (pc >> 2) & 1, e = pc & 3;
+                pk[pc] = pack_bf2_opaque(ex[pc][0], ex[pc][1]);
+                w[qb][hf][e] = pk[pc];
+            }
+        };
+        auto stage_d = [&](int n) __attribute__((always_inline)) {
+            for (int k = 0; k < n && pd < pc; ++k, ++pd) ts[pd >> 3] = add_bf2(ts[pd >> 3], pk[pd]);
+        };
         auto slice = [&](int n) __attribute__((always_inline)) {
-            for (int k = 0; k < n && pair < NPAIR; ++k, ++pair) {
-                const int qb = pair >> 3, hf = (pair >> 2) & 1, e = pair & 3;
-                const bf16x2 pr = {(bf16)__builtin_amdgcn_exp2f(sc[qb][8 * hf + 2 * e]),
-                                   (bf16)__builtin_amdgcn_exp2f(sc[qb][8 * hf + 2 * e + 1])};
-                ts[qb] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ts[qb], false);
-                w[qb][hf][e] = __builtin_bit_cast(uint32_t, pr);
+            stage_d(n);
+            stage_c(n);
+            for (int k = 0; k < n && pe < NPAIR; ++k, ++pe) {
+                const int qb = pe >> 3, hf = (pe >> 2) & 1, e = pe & 3;
+                ex[pe][0] = __builtin_amdgcn_exp2f(sc[qb][8 * hf + 2 * e]);
+                ex[pe][1] = __builtin_amdgcn_exp2f(sc[qb][8 * hf + 2 * e + 1]);
             }
         };
 #pragma unroll
@@ -350,7 +367,6 @@ void fmha_dma_kernel(const FmhaParams p) {
                 if (i < NC) {
                     if (i == 0) sn[qb] = mfma_s_first(a[i], qf[qb][i], negm[qb]);
                     else mfma_s_next(sn[qb], a[i], qf[qb][i]);
-                    if (i == NC - 1 && qb == 1) s_ready(sn[0], sn[1], negm[0], negm[1]);
                 } else {
                     const int j = i - NC;
                     o[j % NDB][qb] = mfma32(a[i], pp[qb][j / NDB], o[j % NDB][qb]);
@@ -360,6 +376,10 @@ void fmha_dma_kernel(const FmhaParams p) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        stage_d(NPAIR);
+        stage_c(NPAIR);
+        stage_d(NPAIR);
+        s_defined(sn[0], sn[1], negm[0], negm[1]);   // 16 products and the slices after S's last
         overflow |= !(ts[0] <= kRebaseBound) || !(ts[1] <= kRebaseBound);
         l[0] += ts[0];
         l[1] += ts[1];

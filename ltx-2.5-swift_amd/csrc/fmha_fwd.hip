@@ -262,7 +262,6 @@ void fmha_fwd_kernel(const FmhaParams p) {
     // S(s) -> P(s) (bf16) and this lane's row-sum share ts.
     auto softmax_block = [&](const f32x16 (&sx)[2], bf16x8 (&pn)[2][2], float (&ts)[2])
         __attribute__((always_inline)) {
-        const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
         ts[0] = ts[1] = 0.f;
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -271,13 +270,10 @@ void fmha_fwd_kernel(const FmhaParams p) {
                 u32x4 w;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const bf16x2 pr = {(bf16)__builtin_amdgcn_exp2f(sx[qb][8 * hf + 2 * e]),
-                                       (bf16)__builtin_amdgcn_exp2f(sx[qb][8 * hf + 2 * e + 1])};
-                    // The row sum adds exactly the bf16 weights that feed P.V. (Each pair is
-                    // consumed as its own value: extracting it back out of the packed vector
-                    // has been miscompiled into a reuse of the first pair.)
-                    ts[qb] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ts[qb], false);
-                    w[e] = __builtin_bit_cast(uint32_t, pr);
+                    // the row sum adds exactly the bf16 weights that feed P.V
+                    w[e] = pack_bf2_opaque(__builtin_amdgcn_exp2f(sx[qb][8 * hf + 2 * e]),
+                                    __builtin_amdgcn_exp2f(sx[qb][8 * hf + 2 * e + 1]));
+                    ts[qb] = add_bf2(ts[qb], w[e]);
                 }
                 pn[qb][hf] = __builtin_bit_cast(bf16x8, w);
             }
@@ -304,7 +300,6 @@ void fmha_fwd_kernel(const FmhaParams p) {
             const int j = i - NC, hf = j / NDB, db = j % NDB;
             return *(const bf16x8 *)(Vt + db * 32 * VS + 16 * hf);
         };
-        const bf16x2 ones = {(bf16)1.0f, (bf16)1.0f};
         float ts[2] = {0.f, 0.f};
         u32x4 w[2][2];
         f32x16 sn[2];
@@ -316,10 +311,9 @@ void fmha_fwd_kernel(const FmhaParams p) {
         auto slice = [&](int n) __attribute__((always_inline)) {
             for (int k = 0; k < n && pair < NPAIR; ++k, ++pair) {
                 const int qb = pair >> 3, hf = (pair >> 2) & 1, e = pair & 3;
-                const bf16x2 pr = {(bf16)__builtin_amdgcn_exp2f(sc[qb][8 * hf + 2 * e]),
-                                   (bf16)__builtin_amdgcn_exp2f(sc[qb][8 * hf + 2 * e + 1])};
-                ts[qb] = __builtin_amdgcn_fdot2_f32_bf16(pr, ones, ts[qb], false);
-                w[qb][hf][e] = __builtin_bit_cast(uint32_t, pr);
+                w[qb][hf][e] = pack_bf2_opaque(__builtin_amdgcn_exp2f(sc[qb][8 * hf + 2 * e]),
+                                        __builtin_amdgcn_exp2f(sc[qb][8 * hf + 2 * e + 1]));
+                ts[qb] = add_bf2(ts[qb], w[qb][hf][e]);
             }
         };
         constexpr int PER = 2 * NOP <= NPAIR ? NPAIR / (2 * NOP) : (NPAIR + NOP - 1) / NOP;
