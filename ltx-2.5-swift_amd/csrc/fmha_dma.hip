@@ -112,32 +112,12 @@ __device__ __forceinline__ void s_defined(f32x16 &x, f32x16 &y, const f32x16 &c0
 __device__ __forceinline__ void wait_copies() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // s_waitcnt vmcnt(n) (n < 64), expcnt and lgkmcnt left at their maxima.
-template <int N>
-__device__ __forceinline__ void wait_copies_but() {
-    static_assert(N >= 0 && N < 64, "vmcnt");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
 
-// A partial copy: the lanes of mask PART move 16 bytes each HBM -> LDS, to M0 + 16*lane. One
-// statement: exec is narrowed for the load and set back to all lanes after it (the
-// steady-state windows run with every lane enabled), so the compiler sees neither a branch
-// nor a memory load (its waits never account for these; the kernel waits for them
-// explicitly). The exec write gives M0 the one wait state the load needs.
-template <int PART, int PARTS>
-__device__ __forceinline__ void copy_part(u32x4 rs, uint32_t lds_byte, int voff) {
-    constexpr int W = 64 / PARTS;
-    constexpr uint64_t mask = (W == 64 ? ~0ull : ((1ull << W) - 1)) << (W * PART);
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_mov_b64 exec, %2\n\t"
-        "buffer_load_dwordx4 %1, %3, 0 offen lds\n\t"
-        "s_mov_b64 exec, -1"
-        :
-        : "s"(lds_byte), "v"(voff), "s"(mask), "s"(rs)
-        : "m0", "memory");
-}
-
-// A full-wave copy (every lane enabled, as everywhere the kernel copies): 16 bytes per lane.
+// A copy HBM -> LDS: every lane (all are enabled wherever the kernel copies) moves 16 bytes
+// from the buffer at its offset to M0 + 16*lane. As one assembly statement the compiler sees
+// no memory load, so its waits never account for these; the kernel waits for them itself
+// (vmcnt). The s_nop is the wait state an M0 write needs before the load. The compiler keeps
+// nothing in M0 in these kernels, so the clobber costs nothing.
 __device__ __forceinline__ void copy_all(u32x4 rs, uint32_t lds_byte, int voff) {
     asm volatile(
         "s_mov_b32 m0, %0\n\t"
@@ -327,31 +307,29 @@ void fmha_dma_kernel(const FmhaParams p) {
             const int j = i - NC;
             return v_opnd(Vp, 2 * kbp + j / NDB, j % NDB);
         };
-        float ts[2] = {0.f, 0.f};
+        float ts[2][2] = {{0.f, 0.f}, {0.f, 0.f}};   // [qb][even/odd key of a pair]
         u32x4 w[2][2];
         f32x16 sn[2];
         bf16x8 a[NOP];
         a[0] = opnd(0);
         a[1] = opnd(1);
         a[2] = opnd(2);
-        // Softmax of S(s) as a three-stage pipeline over bf16 pairs: slice k takes the exps
-        // of its pairs, packs the previous slice's and adds the one before that to the row
-        // sums, so no stage waits for the result of an instruction just issued.
+        // Softmax of S(s) as a two-stage pipeline over pairs of weights: slice k takes the
+        // exps of its pairs and packs the previous slice's to bf16, adding them in fp32 to the
+        // row sums, so no instruction waits for an exp just issued. (Summing the fp32 weights
+        // costs half the instructions of summing their bf16 roundings; the two sums differ by
+        // the unbiased rounding of the weights, far below the output's bf16 rounding.)
         float ex[NPAIR][2];
-        uint32_t pk[NPAIR];
-        int pe = 0, pc = 0, pd = 0;
+        int pe = 0, pc = 0;
         auto stage_c = [&](int n) __attribute__((always_inline)) {
             for (int k = 0; k < n && pc < pe; ++k, ++pc) {
                 const int qb = pc >> 3, hf = (pc >> 2) & 1, e = pc & 3;
-                pk[pc] = pack_bf2_opaque(ex[pc][0], ex[pc][1]);
-                w[qb][hf][e] = pk[pc];
+                w[qb][hf][e] = pack_bf2(ex[pc][0], ex[pc][1]);
+                ts[qb][0] += ex[pc][0];
+                ts[qb][1] += ex[pc][1];
             }
         };
-        auto stage_d = [&](int n) __attribute__((always_inline)) {
-            for (int k = 0; k < n && pd < pc; ++k, ++pd) ts[pd >> 3] = add_bf2(ts[pd >> 3], pk[pd]);
-        };
         auto slice = [&](int n) __attribute__((always_inline)) {
-            stage_d(n);
             stage_c(n);
             for (int k = 0; k < n && pe < NPAIR; ++k, ++pe) {
                 const int qb = pe >> 3, hf = (pe >> 2) & 1, e = pe & 3;
@@ -376,13 +354,12 @@ void fmha_dma_kernel(const FmhaParams p) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        stage_d(NPAIR);
         stage_c(NPAIR);
-        stage_d(NPAIR);
         s_defined(sn[0], sn[1], negm[0], negm[1]);   // 16 products and the slices after S's last
-        overflow |= !(ts[0] <= kRebaseBound) || !(ts[1] <= kRebaseBound);
-        l[0] += ts[0];
-        l[1] += ts[1];
+        const float ts0 = ts[0][0] + ts[0][1], ts1 = ts[1][0] + ts[1][1];
+        overflow |= !(ts0 <= kRebaseBound) || !(ts1 <= kRebaseBound);
+        l[0] += ts0;
+        l[1] += ts1;
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
             sc[qb] = sn[qb];
@@ -493,7 +470,7 @@ void fmha_dma_kernel(const FmhaParams p) {
                     dst = vbuf((a + 1 + tt) & 3);
                     rs = rvw;
                 }
-                copy_part<0, 1>(rs, (uint32_t)(uintptr_t)(dst + e), voff);
+                copy_all(rs, (uint32_t)(uintptr_t)(dst + e), voff);
             };
             if (active) {
 #pragma unroll
