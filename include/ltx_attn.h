@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define LTX_ATTN_ABI_VERSION 1
+#define LTX_ATTN_ABI_VERSION 2
 
 /* Status codes. The reference throws `DiTAttention.Failure` for structural errors
  * (DiTAttention.swift:107-121); a Swift wrapper maps these onto thrown errors. */
@@ -63,7 +63,7 @@ typedef enum {
  * [B, L, H*D] is q_bs = L*H*D, q_rs = H*D, q_hs = D; its split layout [B, H, L, D]
  * (DiTAttention.swift:346-349) is q_bs = H*L*D, q_hs = L*D, q_rs = D.
  * `out` uses the same scheme; the merged layout [B, Lq, H*D] is what `to_out` consumes
- * after the gate (DiTAttention.swift:402-404).
+ * after the gate (DiTAttention.swift:402-404), which the call can apply (gate_logits).
  */
 typedef struct ltx_attn_args {
     int32_t B, H, Lq, Lk, D;      /* D in {64, 128}; H*D = inner (4096 video, 2048 audio/cross) */
@@ -106,6 +106,14 @@ typedef struct ltx_attn_args {
      * before and after the attention kernel itself (not the norm/RoPE prologue or the
      * split-KV combine). NULL = not recorded. */
     void *ev_attn_start, *ev_attn_stop;
+
+    /* Per-head output gate (DiTAttention.swift:385-399): bf16 logits [B, Lq, H] from the
+     * caller's `to_gate_logits(x)` (x = the query stream, :387-391), element strides below
+     * (the linear's output [B, Lq, H] is g_bs = Lq*H, g_rs = H, g_hs = 1). Each output row of
+     * head h is multiplied by 2*sigmoid(logit) (the bf16 gate the reference builds at :396)
+     * before its bf16 rounding. NULL = no gate (the modules without to_gate_logits). */
+    const void *gate_logits;      /* bf16 device pointer, 2-byte aligned                     */
+    int64_t g_bs, g_rs, g_hs;     /* non-negative element strides                             */
 } ltx_attn_args;
 
 /* Fill `a` with defaults: zero sizes and pointers, norm_eps = 1e-6, kprep AUTO, splits auto. */
@@ -118,8 +126,9 @@ size_t ltx_attn_workspace_bytes(const ltx_attn_args *a);
 /* Check the arguments without launching anything (the first step of ltx_attn_fwd). */
 ltx_attn_status ltx_attn_validate(const ltx_attn_args *a);
 
-/* Run norm -> split -> RoPE -> SDPA asynchronously on `stream` (a hipStream_t or NULL).
- * Replaces DiTAttention.swift:360-381 (MLXFast.scaledDotProductAttention at :374-376). */
+/* Run norm -> split -> RoPE -> SDPA (-> gate) asynchronously on `stream` (a hipStream_t or
+ * NULL). Replaces DiTAttention.swift:360-381 (MLXFast.scaledDotProductAttention at :374-376)
+ * and, with gate_logits, the gate multiply of :395-399. */
 ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream);
 
 /* Static text for a status code. */

@@ -159,6 +159,18 @@ __device__ __forceinline__ void load_q(const FmhaParams &p, int b, int h, int q0
     }
 }
 
+// Output gate of (batch b, query q, head h): 2*sigmoid(logit) rounded to bf16, the gate
+// array the reference multiplies the attention output by (DiTAttention.swift:395-399).
+// 1 without a gate.
+__device__ __forceinline__ float gate_factor(const void *gate, int64_t g_bs, int64_t g_rs,
+                                             int64_t g_hs, int b, int q, int h) {
+    if (!gate) return 1.0f;
+    const float x = (float)((const bf16 *)gate)[(int64_t)b * g_bs + (int64_t)q * g_rs +
+                                                (int64_t)h * g_hs];
+    const float g = 2.0f / (1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+    return (float)(bf16)g;
+}
+
 // Work item of a workgroup. Workgroup ids are dealt to the 8 XCDs round-robin; within each
 // region of the grid (whole items, then tail splits) an XCD receives a contiguous range, so
 // the query blocks (and splits) sharing one (batch, head) share an L2.

@@ -602,7 +602,9 @@ void fmha_dma_kernel(const FmhaParams p) {
     // buffers (swizzled like K), store coalesced 16-byte units.
     bf16 *Os = wave == 0 ? sK0 : wave == 1 ? sK1 : wave == 2 ? sV0 : sV1;
     if (active) {
-        const float inv0 = 1.0f / lt[0], inv1 = 1.0f / lt[1];
+        // 1/l, times the head's output gate of the query (rows past Lq are not stored)
+        const float inv0 = gate_factor(p.gate, p.g_bs, p.g_rs, p.g_hs, b, min(q0 + r, p.Lq - 1), h) / lt[0];
+        const float inv1 = gate_factor(p.gate, p.g_bs, p.g_rs, p.g_hs, b, min(q0 + 32 + r, p.Lq - 1), h) / lt[1];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll

@@ -515,7 +515,9 @@ void fmha_fwd_kernel(const FmhaParams p) {
     // Unsplit: normalise, stage O through LDS, store coalesced 16-byte rows.
     bf16 *Os = smem + wave * QW * T::OS;
     if (active) {
-        const float inv0 = 1.0f / lt[0], inv1 = 1.0f / lt[1];
+        // 1/l, times the head's output gate of the query (rows past Lq are not stored)
+        const float inv0 = gate_factor(p.gate, p.g_bs, p.g_rs, p.g_hs, b, min(q0 + r, p.Lq - 1), h) / lt[0];
+        const float inv1 = gate_factor(p.gate, p.g_bs, p.g_rs, p.g_hs, b, min(q0 + 32 + r, p.Lq - 1), h) / lt[1];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
@@ -652,7 +654,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineParams p) {
         den += w * p.part_ml[(s * rows + row) * 2 + 1];
         acc += w * *(const f32x4 *)(p.part_o + (s * rows + row) * D + d);
     }
-    const float inv = 1.0f / den;
+    const float inv = gate_factor(p.gate, p.g_bs, p.g_rs, p.g_hs, b, q, hh) / den;
     u32x2 w;
     w[0] = pack_bf2(acc[0] * inv, acc[1] * inv);
     w[1] = pack_bf2(acc[2] * inv, acc[3] * inv);

@@ -48,6 +48,9 @@ struct FmhaParams {
     float *part_o;                   // tail partials [S][n_tail][256][D] fp32
     float *part_ml;                  // [S][n_tail][256][2]: running max (log2 units), row sum
     int32_t valid[kMaxBatch];        // keys valid per batch row (Lk when unmasked)
+    // Output gate: bf16 logits, element strides; output rows times 2*sigmoid(logit), or null.
+    const void *gate;
+    int64_t g_bs, g_rs, g_hs;
 };
 
 // Per-token RMS statistic over the inner dim, optionally writing the normalised and rotated
@@ -71,6 +74,8 @@ struct CombineParams {
     int64_t o_bs, o_rs, o_hs;
     int32_t H, Lq, nqblk;
     int32_t n_full, n_tail, num_splits;
+    const void *gate;                // as in FmhaParams
+    int64_t g_bs, g_rs, g_hs;
 };
 
 // Launchers (fmha_fwd.hip). Return the hipError_t of the launch as int.

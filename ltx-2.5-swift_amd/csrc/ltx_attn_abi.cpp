@@ -96,6 +96,12 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
     if ((s = check_tensor("out", a->out, a->o_bs, a->o_rs, a->o_hs, B, a->Lq, H, D))) return s;
     if (!(a->scale > 0.f) || !isfinite(a->scale))
         return fail(LTX_ATTN_EINVAL, "scale must be positive and finite");
+    if (a->gate_logits) {
+        if ((uintptr_t)a->gate_logits & 1u)
+            return fail(LTX_ATTN_EINVAL, "gate_logits is not 2-byte aligned");
+        if (a->g_bs < 0 || a->g_rs < 0 || a->g_hs < 0)
+            return fail(LTX_ATTN_EINVAL, "gate_logits has a negative stride");
+    }
 
     pl->q_norm = a->q_norm_w != nullptr;
     pl->k_norm = a->k_norm_w != nullptr;
@@ -313,6 +319,8 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
         }
     }
     fp.qk_scale_log2 = (float)((double)a->scale * 1.4426950408889634);
+    fp.gate = a->gate_logits;
+    fp.g_bs = a->g_bs; fp.g_rs = a->g_rs; fp.g_hs = a->g_hs;
     fp.nqblk = pl.nqblk;
     fp.n_items = (int32_t)pl.n_items;
     fp.n_full = (int32_t)pl.n_full;
@@ -335,6 +343,7 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
             sp.k = (const char *)kptr + 2 * (int64_t)b0 * k_bs;
             sp.v = (const char *)a->v + 2 * (int64_t)b0 * a->v_bs;
             sp.o = (char *)a->out + 2 * (int64_t)b0 * a->o_bs;
+            if (sp.gate) sp.gate = (const char *)a->gate_logits + 2 * (int64_t)b0 * a->g_bs;
             if (sp.q_rstd) sp.q_rstd += (int64_t)b0 * a->Lq;
             if (sp.k_rstd) sp.k_rstd += (int64_t)b0 * a->Lk;
             sp.n_items = sp.n_full = sp.grid = nb * H * pl.nqblk;
@@ -368,6 +377,8 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
         cp.n_full = (int32_t)pl.n_full;
         cp.n_tail = (int32_t)(pl.n_items - pl.n_full);
         cp.num_splits = pl.splits;
+        cp.gate = a->gate_logits;
+        cp.g_bs = a->g_bs; cp.g_rs = a->g_rs; cp.g_hs = a->g_hs;
         if (int e = ltx::launch_combine(cp, D, stream))
             return fail(LTX_ATTN_EHIP, "combine launch: %s", hipGetErrorString((hipError_t)e));
     }

@@ -75,12 +75,15 @@ public:
 
     // norm -> split -> RoPE -> SDPA for one module call. q = to_q(x), k = to_k(context),
     // v = to_v(context) (pre-norm); `rotary` is `pe`, `keyRotary` is `k_pe` (nullptr means
-    // "use pe for both", :310-314). `out` receives [B, Lq, H*D] bf16. Throws Failure.
+    // "use pe for both", :310-314). `out` receives [B, Lq, H*D] bf16. With `gate_logits`
+    // (bf16 [B, Lq, H] contiguous: to_gate_logits(x)) each head's rows are multiplied by
+    // 2*sigmoid(logit), as the module's gate does (:395-399). Throws Failure.
     void operator()(int32_t batch, int32_t inner, const Stream &q, const Stream &k,
                     const Stream &v, void *out, int64_t out_batch_stride,
                     int64_t out_row_stride, Variant variant, const Rotary *rotary,
                     const Rotary *keyRotary, void *workspace, size_t workspace_bytes,
-                    void *stream, const int32_t *k_valid_len = nullptr) const {
+                    void *stream, const int32_t *k_valid_len = nullptr,
+                    const void *gate_logits = nullptr) const {
         if (rotary && !takesRotary(variant))
             throw Failure(LTX_ATTN_EINVAL,
                           std::string(rawValue(variant)) +
@@ -96,6 +99,12 @@ public:
                                rotary, keyRotary, k_valid_len);
         a.workspace = workspace;
         a.workspace_bytes = workspace_bytes;
+        if (gate_logits) {
+            a.gate_logits = gate_logits;
+            a.g_bs = (int64_t)q.tokens * heads;
+            a.g_rs = heads;
+            a.g_hs = 1;
+        }
         check(ltx_attn_fwd(&a, stream));
     }
 

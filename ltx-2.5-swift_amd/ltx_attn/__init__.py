@@ -56,6 +56,8 @@ class Args(ctypes.Structure):
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("kprep", ctypes.c_int32), ("num_splits", ctypes.c_int32),
         ("ev_attn_start", ctypes.c_void_p), ("ev_attn_stop", ctypes.c_void_p),
+        ("gate_logits", ctypes.c_void_p),
+        ("g_bs", ctypes.c_int64), ("g_rs", ctypes.c_int64), ("g_hs", ctypes.c_int64),
     ]
 
 
@@ -209,11 +211,13 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
                   key_rotary: Optional[Rotary] = None,
                   k_valid_len: Optional[Sequence[int]] = None, scale: Optional[float] = None,
                   out=None, kprep: int = KPREP_AUTO, num_splits: int = 0, stream=None,
-                  workspace=None, events=None):
+                  workspace=None, events=None, gate_logits=None):
     """One call of ``ltx_attn_fwd``. Tensors are torch bf16 on the current HIP device.
 
     ``layout="merged"``: q ``[B, Lq, H*D]``, k/v ``[B, Lk, H*D]``, out ``[B, Lq, H*D]``.
     ``layout="split"``:  q ``[B, H, Lq, D]``, k/v ``[B, H, Lk, D]``, out ``[B, H, Lq, D]``.
+    ``gate_logits``: bf16 ``[B, Lq, H]`` (the output of ``to_gate_logits(x)``); each output row
+    of head h is multiplied by ``2*sigmoid(logit)`` (``DiTAttention.swift:395-399``).
     Returns ``out``.
     """
     import torch
@@ -270,6 +274,14 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
     a.num_splits = num_splits
     if events is not None:
         a.ev_attn_start, a.ev_attn_stop = events
+    if gate_logits is not None:
+        if gate_logits.dtype != torch.bfloat16 or not gate_logits.is_cuda:
+            raise Failure(EINVAL, "gate_logits must be a bf16 device tensor")
+        if tuple(gate_logits.shape) != (B, Lq, heads):
+            raise Failure(EINVAL, f"gate_logits shape {tuple(gate_logits.shape)} is not "
+                                  f"{(B, Lq, heads)}")
+        a.gate_logits = _ptr(gate_logits)
+        a.g_bs, a.g_rs, a.g_hs = gate_logits.stride()
     need = lib.ltx_attn_workspace_bytes(ctypes.byref(a))
     st = lib.ltx_attn_validate(ctypes.byref(a))
     if st not in (OK, EWORKSPACE):

@@ -50,7 +50,7 @@ import numpy as np
 
 __all__ = [
     "f32_to_bf16_bits", "bf16_bits_to_f32", "round_bf16", "randn_bf16_bits",
-    "splitmix_bf16_bits", "rms_norm", "split_rope", "sdpa", "attention",
+    "splitmix_bf16_bits", "rms_norm", "split_rope", "sdpa", "head_gate", "attention",
     "frequency_grid", "video_positions", "audio_positions", "rotary_tables",
     "rotaries", "compare",
 ]
@@ -189,6 +189,17 @@ def sdpa(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
     return out
 
 
+def head_gate(logit_bits, mode: str = "exact") -> np.ndarray:
+    """Per-head output gate ``2 * sigmoid(logits)`` (``DiTAttention.swift:395-399``).
+
+    ``logit_bits``: bf16 bits ``[B, L, H]`` (``to_gate_logits(x)``). ``mode="exact"`` returns
+    float64; ``mode="reference"`` rounds to bf16, the dtype of the reference's gate array.
+    """
+    x = bf16_bits_to_f32(logit_bits).astype(np.float64)
+    g = 2.0 / (1.0 + np.exp(-x))
+    return g if mode == "exact" else round_bf16(g)
+
+
 def _split_heads(x_bits: np.ndarray, heads: int) -> np.ndarray:
     """``[B, L, H*D]`` -> ``[B, H, L, D]`` fp32 (``DiTAttention.swift:346-349``)."""
     B, L, inner = x_bits.shape
@@ -198,8 +209,9 @@ def _split_heads(x_bits: np.ndarray, heads: int) -> np.ndarray:
 
 def attention(q_bits, k_bits, v_bits, heads: int, *, q_norm_w=None, k_norm_w=None,
               eps: float = 1e-6, q_cos=None, q_sin=None, k_cos=None, k_sin=None,
-              valid_len=None, scale=None, mode: str = "exact") -> np.ndarray:
-    """The replaced unit ``DiTAttention.swift:358-381`` from the pre-norm projections.
+              valid_len=None, scale=None, mode: str = "exact", gate_bits=None) -> np.ndarray:
+    """The replaced unit ``DiTAttention.swift:358-381`` from the pre-norm projections, and with
+    ``gate_bits`` (bf16 bits ``[B, Lq, H]``) the per-head gate of ``:395-399``.
 
     Inputs are bf16 bit patterns: ``q_bits`` ``[B, Lq, H*D]``, ``k_bits``/``v_bits``
     ``[B, Lk, H*D]``; norm weights ``[H*D]`` bits or None (inputs already normed); RoPE
@@ -231,7 +243,12 @@ def attention(q_bits, k_bits, v_bits, heads: int, *, q_norm_w=None, k_norm_w=Non
         qh = split_rope(qh, qc, qs, mode)
         kh = split_rope(kh, kc, ks, mode)
     o = sdpa(qh, kh, vh, scale, valid_len)
-    return o.transpose(0, 2, 1, 3).reshape(B, Lq, inner)
+    o = o.transpose(0, 2, 1, 3)                       # [B, Lq, H, D]
+    if gate_bits is not None:
+        if mode != "exact":
+            o = round_bf16(o)                         # the attention output is bf16 (:381)
+        o = o * head_gate(gate_bits, mode)[..., None]
+    return o.reshape(B, Lq, inner)
 
 
 # --------------------------------------------------------------------------------------

@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layout_and_version():
     lib = L.load_library()
     assert lib.ltx_attn_args_size() == ctypes.sizeof(L.Args)
-    assert lib.ltx_attn_abi_version() == 1
+    assert lib.ltx_attn_abi_version() == 2
     assert "gfx950" in L.provenance()
     for s in range(5):
         assert lib.ltx_attn_status_string(s)
@@ -112,6 +112,23 @@ def test_invalid_arguments_are_rejected(field, value, status):
     st, msg = _validate(a)
     assert st == status, msg
     assert msg
+
+
+def test_gate_rules():
+    # [B, Lq, H] logits: any 2-byte aligned pointer, non-negative strides
+    a = _args(gate_logits=FAKE + 2, g_bs=3120 * 32, g_rs=32, g_hs=1)
+    st, msg = _validate(a)
+    assert st == L.OK, msg
+    a.gate_logits = FAKE + 1
+    st, msg = _validate(a)
+    assert st == L.EINVAL and "gate_logits" in msg
+    a.gate_logits, a.g_rs = FAKE, -32
+    st, msg = _validate(a)
+    assert st == L.EINVAL and "gate_logits" in msg
+    # the gate costs no workspace
+    lib = L.load_library()
+    assert (lib.ltx_attn_workspace_bytes(ctypes.byref(_args(ws=False, gate_logits=FAKE)))
+            == lib.ltx_attn_workspace_bytes(ctypes.byref(_args(ws=False))))
 
 
 def test_rotary_rules():

@@ -72,6 +72,8 @@ def run(device, q, k, v, heads, **kw):
         extra["rotary"] = L.Rotary(dev(qc, device), dev(qs, device))
     if kc is not None:
         extra["key_rotary"] = L.Rotary(dev(kc, device), dev(ks, device))
+    if isinstance(kw.get("gate_logits"), np.ndarray):
+        extra["gate_logits"] = dev(kw.pop("gate_logits"), device)
     out = L.attention_fwd(tq, tk, tv, heads=heads, **extra, **kw)
     torch.cuda.synchronize()
     return host_f32(out)
@@ -170,6 +172,76 @@ def test_split_kv_ragged_rows_with_empty_splits(device):
     truth = O.attention(q, k, v, H, valid_len=valid, mode="exact")
     got = run(device, q, k, v, H, k_valid_len=valid, num_splits=8)
     check(got, truth, None, "ragged split")
+
+
+def _gate_bits(shape, seed):
+    """Gate logits ~ N(0, 2), with every 7th at +12 and every 11th from the 3rd at -12
+    (saturated gates: x2 and ~x0)."""
+    f = O.bf16_bits_to_f32(O.randn_bf16_bits(shape, seed, std=2.0)).copy()
+    f.ravel()[::7] = 12.0
+    f.ravel()[3::11] = -12.0
+    return O.f32_to_bf16_bits(f)
+
+
+@pytest.mark.parametrize("case", ["dma_whole_and_tail", "register_split", "register_whole",
+                                  "strided_logits"])
+def test_output_gate(device, case):
+    """The per-head gate (DiTAttention.swift:395-399) in every epilogue: the LDS-DMA kernel's
+    whole items and the combine of its split tail items (2 x 16 heads x 9 query blocks = 288
+    items: 256 whole + 32 split in two), the register kernel split and unsplit, and logits
+    given as a strided view."""
+    import torch
+
+    B, H, Lq, Lk, D, kw = {
+        "dma_whole_and_tail": (2, 16, 2100, 128, 128, {}),
+        "register_split": (1, 4, 126, 1500, 64, {"num_splits": 3}),
+        "register_whole": (2, 4, 100, 300, 128, {"num_splits": 1}),
+        "strided_logits": (1, 8, 600, 200, 128, {}),
+    }[case]
+    _say(f"output gate {case}: B={B} H={H} Lq={Lq} Lk={Lk} D={D} {kw}")
+    seed = 0x5EED + 60
+    q = O.randn_bf16_bits((B, Lq, H * D), seed)
+    k = O.randn_bf16_bits((B, Lk, H * D), seed + 1)
+    v = O.randn_bf16_bits((B, Lk, H * D), seed + 2)
+    g = _gate_bits((B, Lq, H), seed + 3)
+    if case == "strided_logits":
+        wide = np.zeros((B, Lq, 2 * H), dtype=np.uint16)
+        wide[:, :, 1::2] = g
+        kw["gate_logits"] = dev(wide, device)[:, :, 1::2]
+        assert kw["gate_logits"].stride() == (Lq * 2 * H, 2 * H, 2)
+    else:
+        kw["gate_logits"] = g
+    truth = O.attention(q, k, v, H, gate_bits=g, mode="exact")
+    got = run(device, q, k, v, H, **kw)
+    check(got, truth, None, f"gate {case}")
+    # The gate itself: the gated output is the ungated output times the bf16 gate, to the
+    # two bf16 roundings in between (2^-8 relative), row by row.
+    kw.pop("gate_logits")
+    plain = run(device, q, k, v, H, **kw).reshape(B, Lq, H, D)
+    want = plain * O.head_gate(g, "reference")[..., None]
+    err = np.abs(got.reshape(B, Lq, H, D) - want)
+    assert np.all(err <= np.abs(want) * 2.0 ** -7 + 1e-6), float(err.max())
+    # rows whose gate saturates at ~0 come out ~0
+    f = O.bf16_bits_to_f32(g)
+    off = got.reshape(B, Lq, H, D)[f < -11.0]
+    assert off.size and np.abs(off).max() < 1e-4
+
+
+@pytest.mark.parametrize("Lq", [40, 300])
+def test_batches_beyond_one_launch(device, Lq):
+    """B = 66 unmasked batch rows run as launches of 64 + 2 rows (the per-row key lengths
+    travel in the kernel arguments); each launch's pointers, statistics and gate start at
+    its first row. Lq = 40: register kernel; Lq = 300: LDS-DMA kernel."""
+    B, H, Lk, D = 66, 2, 50, 64
+    _say(f"batches beyond one launch: B={B} Lq={Lq}")
+    q = O.randn_bf16_bits((B, Lq, H * D), 71)
+    k = O.randn_bf16_bits((B, Lk, H * D), 72)
+    v = O.randn_bf16_bits((B, Lk, H * D), 73)
+    w = O.randn_bf16_bits((H * D,), 74, mean=1.0, std=0.02)
+    g = _gate_bits((B, Lq, H), 75)
+    truth = O.attention(q, k, v, H, q_norm_w=w, k_norm_w=w, gate_bits=g, mode="exact")
+    got = run(device, q, k, v, H, q_norm_w=w, k_norm_w=w, gate_logits=g)
+    check(got, truth, None, f"B={B} Lq={Lq}")
 
 
 def test_rebase_path_large_logits(device):

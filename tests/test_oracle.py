@@ -130,6 +130,48 @@ def test_softmax_shift_invariance():
 
 
 # ---------------------------------------------------------------------------------------
+# Per-head output gate
+# ---------------------------------------------------------------------------------------
+
+def test_head_gate_closed_forms():
+    """2*sigmoid is centred on 1 (DiTAttention.swift:393-394): a zero logit passes through (a
+    plain sigmoid would halve it), large logits saturate at 2 and 0, g(x) + g(-x) = 2, and
+    the gate is increasing."""
+    x = O.f32_to_bf16_bits(np.array([0.0, 30.0, -30.0], dtype=np.float32))
+    g = O.head_gate(x)
+    assert g[0] == 1.0
+    assert abs(g[1] - 2.0) < 1e-12 and abs(g[2]) < 1e-12
+    r = O.randn_bf16_bits((2, 5, 3), 7, std=3.0)
+    neg = O.f32_to_bf16_bits(-O.bf16_bits_to_f32(r))
+    np.testing.assert_allclose(O.head_gate(r) + O.head_gate(neg), 2.0, atol=1e-12)
+    xs = np.sort(O.bf16_bits_to_f32(r).ravel())
+    gs = O.head_gate(O.f32_to_bf16_bits(xs))
+    assert np.all(np.diff(gs) >= 0)
+    # the reference's gate array is bf16: reference mode rounds it
+    assert np.all(O.head_gate(r, "reference") == O.round_bf16(O.head_gate(r)))
+
+
+def test_head_gate_scales_each_heads_rows():
+    """Zero logits leave the attention output unchanged; a logit of -30 on one (token, head)
+    silences exactly that head's row, and doubling comes from +30."""
+    B, L, H, D = 1, 6, 3, 8
+    q = O.randn_bf16_bits((B, L, H * D), 1)
+    k = O.randn_bf16_bits((B, L, H * D), 2)
+    v = O.randn_bf16_bits((B, L, H * D), 3)
+    base = O.attention(q, k, v, H)
+    zero = O.f32_to_bf16_bits(np.zeros((B, L, H), dtype=np.float32))
+    np.testing.assert_array_equal(O.attention(q, k, v, H, gate_bits=zero), base)
+    logits = np.zeros((B, L, H), dtype=np.float32)
+    logits[0, 2, 1] = -30.0
+    logits[0, 4, 2] = 30.0
+    got = O.attention(q, k, v, H, gate_bits=O.f32_to_bf16_bits(logits)).reshape(B, L, H, D)
+    want = base.reshape(B, L, H, D).copy()
+    want[0, 2, 1] *= 0.0
+    want[0, 4, 2] *= 2.0
+    np.testing.assert_allclose(got, want, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------------------
 # RMSNorm over the inner dim
 # ---------------------------------------------------------------------------------------
 
