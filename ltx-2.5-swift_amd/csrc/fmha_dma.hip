@@ -155,13 +155,7 @@ void fmha_dma_kernel(const FmhaParams p) {
     const int q0 = qblk * QT + wave * QW;
     const bool active = q0 < p.Lq;
 
-    bf16x8 qf[2][NC];
-    load_q<D>(p, b, h, q0, active, r, g, qf);
-    // Q is only an MFMA operand: home it in AGPRs, leaving the VGPRs to S and P.
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) asm volatile("" : "+a"(qf[qb][c]));
+    bf16x8 qf[2][NC];                  // loaded after the first copies are on their way
 
     // ---- copies HBM -> LDS -----------------------------------------------------------
     const bf16 *Kb = (const bf16 *)p.k + (int64_t)b * p.k_bs + (int64_t)h * p.k_hs;
@@ -434,6 +428,13 @@ void fmha_dma_kernel(const FmhaParams p) {
         if (t_begin + 1 < t_end) copy_k(t_begin + 1, kbuf(1));
         copy_v(t_begin, vbuf(0));
     }
+    // The Q prologue's loads overlap the first copies (both wait on HBM latency).
+    load_q<D>(p, b, h, q0, active, r, g, qf);
+    // Q is only an MFMA operand: home it in AGPRs, leaving the VGPRs to S and P.
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) asm volatile("" : "+a"(qf[qb][c]));
     // Steps blk_begin-1 .. blk_end (the last one only finishes P.V) in windows of four.
     const int nwin = t_begin < t_end ? (blk_end - blk_begin + 2 + 3) / 4 : 0;
     // Steady-state windows: all four steps complete (not the first block, whose step sets
