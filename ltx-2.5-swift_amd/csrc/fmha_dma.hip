@@ -171,21 +171,30 @@ void fmha_dma_kernel(const FmhaParams p) {
     };
     const u32x4 rkw = rsrc_words(Kb, (int64_t)n_valid * krow_bytes);
     const u32x4 rvw = rsrc_words(Vb, (int64_t)n_valid * vrow_bytes);
-    // Copy j of this wave's share of a K (V) tile: the per-lane offset, and the element offset
-    // of the wave's 64 units in the LDS buffer.
-    auto k_src = [&](int tile, int j, int &voff) __attribute__((always_inline)) {
-        const int blk = wave * T::K_DMA + j;
-        const int q = blk * 64 + lane;
+    // Copy j of this wave's share of a K (V) tile: lane byte offsets within a tile (fixed for
+    // the whole item) plus the tile's offset, a scalar; and the element offset of the wave's
+    // 64 units in the LDS buffer. (The host bounds a head's padded key rows to 2^31 bytes.)
+    const int ktile_bytes = KT * (int)krow_bytes, vtile_bytes = KT * (int)vrow_bytes;
+    int klane[T::K_DMA], vlane[T::V_DMA];
+#pragma unroll
+    for (int j = 0; j < T::K_DMA; ++j) {
+        const int q = (wave * T::K_DMA + j) * 64 + lane;
         const int row = q / KU, u = swz<KU>(row, q % KU);
-        voff = (int)((tile * KT + row) * krow_bytes + 16 * u);
-        return blk * 512;
+        klane[j] = row * (int)krow_bytes + 16 * u;
+    }
+#pragma unroll
+    for (int j = 0; j < T::V_DMA; ++j) {
+        const int q = (wave * T::V_DMA + j) * 64 + lane;
+        const int row = q / KU, u = vswz<KU>(row, q % KU);
+        vlane[j] = row * (int)vrow_bytes + 16 * u;
+    }
+    auto k_src = [&](int tile, int j, int &voff) __attribute__((always_inline)) {
+        voff = tile * ktile_bytes + klane[j];
+        return (wave * T::K_DMA + j) * 512;
     };
     auto v_src = [&](int tile, int j, int &voff) __attribute__((always_inline)) {
-        const int blk = wave * T::V_DMA + j;
-        const int q = blk * 64 + lane;
-        const int row = q / KU, u = vswz<KU>(row, q % KU);
-        voff = (int)((tile * KT + row) * vrow_bytes + 16 * u);
-        return blk * 512;
+        voff = tile * vtile_bytes + vlane[j];
+        return (wave * T::V_DMA + j) * 512;
     };
     auto copy_k = [&](int tile, lds_bf16 *dst) __attribute__((always_inline)) {
 #pragma unroll
@@ -438,11 +447,11 @@ void fmha_dma_kernel(const FmhaParams p) {
     // Steps blk_begin-1 .. blk_end (the last one only finishes P.V) in windows of four.
     const int nwin = t_begin < t_end ? (blk_end - blk_begin + 2 + 3) / 4 : 0;
     // Steady-state windows: all four steps complete (not the first block, whose step sets
-    // the running max, nor the ragged last one) and all four copies in range.
+    // the running max, nor the ragged last one). Their copies of tiles past the range fetch
+    // the range's last tile instead, into a buffer no later step of the range reads.
     const int lim_s = blk_end - blk_begin - 3;          // window w needs 4w < lim_s
-    const int lim_c = t_end - t_begin - 3;              // and 2w < lim_c
     const int wf0 = 1;
-    const int wf1 = min(nwin, min(lim_s > 0 ? (lim_s + 3) / 4 : 0, lim_c > 0 ? (lim_c + 1) / 2 : 0));
+    const int wf1 = min(nwin, lim_s > 0 ? (lim_s + 3) / 4 : 0);
     constexpr int NOPS = NC + 2 * NDB;                  // product pairs per step
     static_assert(NOPS == 2 * (T::K_DMA + T::V_DMA), "one copy per four product pairs");
     // `par` is w & 1: a compile-time constant in the steady state, a value at the edges.
@@ -461,13 +470,13 @@ void fmha_dma_kernel(const FmhaParams p) {
                 u32x4 rs;
                 if (c < 2 * T::K_DMA) {
                     const int tt = c / T::K_DMA;
-                    e = k_src(T0 + 2 + tt, c % T::K_DMA, voff);
+                    e = k_src(min(T0 + 2 + tt, t_end - 1), c % T::K_DMA, voff);
                     dst = kbuf((a + 2 + tt) & 3);
                     rs = rkw;
                 } else {
                     const int c2 = c - 2 * T::K_DMA;
                     const int tt = c2 / T::V_DMA;
-                    e = v_src(T0 + 1 + tt, c2 % T::V_DMA, voff);
+                    e = v_src(min(T0 + 1 + tt, t_end - 1), c2 % T::V_DMA, voff);
                     dst = vbuf((a + 1 + tt) & 3);
                     rs = rvw;
                 }

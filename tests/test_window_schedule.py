@@ -2,7 +2,9 @@
 restated step by step and checked on the CPU over split ranges and ragged key lengths:
 every pipeline step runs exactly once, every operand read finds its tile in the buffer it
 reads, no copy overwrites a buffer its own window reads, and the steady-state windows (no
-edge handling, buffers fixed at compile time) have every part present."""
+edge handling, buffers fixed at compile time) have every step complete. A steady-state
+window's copy of a tile past the range fetches the range's last tile instead (no branch);
+the model tracks what each buffer then holds, so a later read of such a buffer would fail."""
 import pytest
 
 KT = 64
@@ -18,9 +20,9 @@ def schedule(t_begin, t_end, n_valid):
             slots_k[1] = t_begin + 1
         slots_v[0] = t_begin
     nwin = (blk_end - blk_begin + 2 + 3) // 4 if t_begin < t_end else 0
-    lim_s, lim_c = blk_end - blk_begin - 3, t_end - t_begin - 3
+    lim_s = blk_end - blk_begin - 3
     wf0 = 1
-    wf1 = min(nwin, min((lim_s + 3) // 4 if lim_s > 0 else 0, (lim_c + 1) // 2 if lim_c > 0 else 0))
+    wf1 = min(nwin, (lim_s + 3) // 4 if lim_s > 0 else 0)
     order, w = [], 0
     while w < min(wf0, nwin):
         order.append((w, False)); w += 1
@@ -51,8 +53,9 @@ def schedule(t_begin, t_end, n_valid):
                   ("v", T0 + 1, (a + 1) & 3), ("v", T0 + 2, (a + 2) & 3)]
         for kind, tile, slot in copies:
             if tile >= t_end:
-                assert not fast
-                continue
+                if not fast:
+                    continue                      # edge windows skip it
+                tile = ("past the range", min(tile, t_end - 1))
             if kind == "k":
                 assert slot not in reads_k
                 slots_k[slot] = tile
@@ -75,8 +78,8 @@ def test_schedule_invariants(t_begin):
 
 
 def test_benchmark_shapes():
-    # 12480 keys, one whole item: 98 windows, 95 in the steady state
-    assert schedule(0, 195, 12480) == (98, 95)
+    # 12480 keys, one whole item: 98 windows, 96 in the steady state
+    assert schedule(0, 195, 12480) == (98, 96)
     # a tail item's key range of 28 tiles, and the last (ragged-free, shorter) one
-    assert schedule(28, 56, 12480) == (15, 12)
-    assert schedule(168, 195, 12480) == (14, 11)
+    assert schedule(28, 56, 12480) == (15, 13)
+    assert schedule(168, 195, 12480) == (14, 12)
