@@ -455,7 +455,7 @@ void fmha_dma_kernel(const FmhaParams p) {
     constexpr int NOPS = NC + 2 * NDB;                  // product pairs per step
     static_assert(NOPS == 2 * (T::K_DMA + T::V_DMA), "one copy per four product pairs");
     // `par` is w & 1: a compile-time constant in the steady state, a value at the edges.
-    auto window = [&](auto fast, auto par, int w) __attribute__((always_inline)) {
+    auto window = [&](auto fast, auto par, int w, auto first) __attribute__((always_inline)) {
         const int a = 2 * (int)par;                     // slot of K(T0)
         const int T0 = t_begin + 2 * w;
         wait_copies();        // this wave's copies for this window have landed
@@ -501,24 +501,37 @@ void fmha_dma_kernel(const FmhaParams p) {
             __builtin_amdgcn_sched_barrier(0);
             if (active) {
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    edge_step(2 * T0 - 1 + k, kbuf((a + (k >> 1)) & 3), vbuf((a + 3 + (k >> 1)) & 3));
+                for (int k = 0; k < 4; ++k) {
+                    // `first`: the range's first window when its steps 2 and 3 are complete
+                    // (the fill step and the first block's step stay edge steps)
+                    if (decltype(first)::value && k >= 2)
+                        fast_step(2 * T0 - 1 + k, kbuf((a + (k >> 1)) & 3),
+                                  vbuf((a + 3 + (k >> 1)) & 3), [](int) {});
+                    else
+                        edge_step(2 * T0 - 1 + k, kbuf((a + (k >> 1)) & 3),
+                                  vbuf((a + 3 + (k >> 1)) & 3));
+                }
             }
         }
     };
     using even = std::integral_constant<int, 0>;
     using odd = std::integral_constant<int, 1>;
+    using no = std::false_type;
     int w = 0;
-    for (; w < min(wf0, nwin); ++w) window(std::false_type{}, w & 1, w);
-    if (wf0 < wf1) {                                    // here w == wf0
-        if (w & 1) window(std::true_type{}, odd{}, w++);
-        for (; w + 1 < wf1; w += 2) {
-            window(std::true_type{}, even{}, w);
-            window(std::true_type{}, odd{}, w + 1);
-        }
-        if (w < wf1) window(std::true_type{}, even{}, w++);
+    if (nwin > 0) {                                     // window 0 (wf0 == 1)
+        if (lim_s > 0) window(no{}, even{}, 0, std::true_type{});
+        else window(no{}, even{}, 0, no{});
+        w = 1;
     }
-    for (; w < nwin; ++w) window(std::false_type{}, w & 1, w);
+    if (wf0 < wf1) {                                    // here w == wf0
+        if (w & 1) window(std::true_type{}, odd{}, w++, no{});
+        for (; w + 1 < wf1; w += 2) {
+            window(std::true_type{}, even{}, w, no{});
+            window(std::true_type{}, odd{}, w + 1, no{});
+        }
+        if (w < wf1) window(std::true_type{}, even{}, w++, no{});
+    }
+    for (; w < nwin; ++w) window(no{}, w & 1, w, no{});
     wait_copies();
 
     // ---- safe pass: only when some wave's running max was outgrown -------------------

@@ -40,7 +40,7 @@ def schedule(t_begin, t_end, n_valid):
             do_sm = blk_begin <= s < blk_end
             do_s = blk_begin <= s + 1 < blk_end
             do_pv = blk_begin <= s - 1 < blk_end
-            if fast:
+            if fast or (w == 0 and lim_s > 0 and k >= 2):   # steady, or window 0's last two
                 assert do_sm and do_s and do_pv and s not in (blk_begin, blk_end - 1)
             if do_s:
                 assert slots_k.get((a + (k >> 1)) & 3) == (s + 1) // 2
