@@ -17,6 +17,10 @@ register allocator and scheduler put things:
   * no result is still inside its window at a label or a branch (the padding never relies
     on one particular path).
 
+It also rejects any kernel of the file that spills to scratch memory (`.private_seg_size`
+above 0): the kernels are laid out to fit the register file, and a spill would otherwise
+only show as a slowdown.
+
 Wait states: each instruction counts one, `s_nop N` counts N + 1.
 
     python check_mfma_hazards.py <device assembly .s>     (exit status 1 on a violation)
@@ -123,6 +127,9 @@ def main(path):
             count += sum(1 for l in body if re.match(r"\s*;\s*mfma_s\s", l))
             errors += check(body, fn[:60])
             start = None
+    for m in re.finditer(r"\.set (\S+)\.private_seg_size, (\d+)", "\n".join(text)):
+        if int(m.group(2)) > 0:
+            errors.append(f"{m.group(1)[:60]}: {m.group(2)} bytes of scratch (register spills)")
     for e in errors:
         print(e)
     print(f"check_mfma_hazards: {count} S products checked, {len(errors)} violations")

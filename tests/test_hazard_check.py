@@ -78,3 +78,13 @@ def test_built_kernel_passes():
     if not os.path.exists(s):
         pytest.skip("device assembly not built (make -C ltx-2.5-swift_amd/csrc)")
     assert H.main(s) == 0
+
+
+def test_scratch_spill_is_caught(tmp_path):
+    text = ("_Zkernel:\n\ts_endpgm\n"
+            "\t.set _Zkernel.private_seg_size, 316\n")
+    f = tmp_path / "k.s"
+    f.write_text(text)
+    assert H.main(str(f)) == 1
+    f.write_text(text.replace("316", "0"))
+    assert H.main(str(f)) == 0
