@@ -251,6 +251,32 @@ def bench_c5(device, steps, warmup, hip):
             "kernel_ms": per}
 
 
+def bench_rope_tables(device):
+    """The 12480-token video table pair (32 x 12480 x 64 cos + sin, bf16) built on the GPU,
+    against the host builder plus the upload it needs."""
+    import torch
+
+    import ltx_attn as L
+
+    pos = L.rope_video_positions(13, 24, 40)
+    pos_dev = torch.from_numpy(pos).to(device)
+    for _ in range(3):
+        L.rope_tables_device(pos_dev, 4096, [20, 2048, 2048], 32)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 20
+    for _ in range(n):
+        L.rope_tables_device(pos_dev, 4096, [20, 2048, 2048], 32)
+    torch.cuda.synchronize()
+    gpu_ms = (time.perf_counter() - t0) / n * 1e3
+    t0 = time.perf_counter()
+    c, s_ = L.rope_tables(pos, 4096, [20, 2048, 2048], 32)
+    up = [_dev_bits(c, device), _dev_bits(s_, device)]
+    torch.cuda.synchronize()
+    host_ms = (time.perf_counter() - t0) * 1e3
+    return {"device_ms": gpu_ms, "host_build_and_upload_ms": host_ms}
+
+
 def cpu_baseline(x, budget_s):
     """The C restatement of the reference's explicit path (fp32 logits, softmax, P.V, with
     its bf16 rounding points), multithreaded, on a bounded sample of the c4 workload:
@@ -348,6 +374,10 @@ def main():
         c5 = bench_c5(device, 5, 2, hip)
         print(f"# c5: {c5['ms_per_block']:.3f} ms per block attention set", file=sys.stderr,
               flush=True)
+        rope = bench_rope_tables(device)
+        print(f"# rope tables (12480 video tokens): {rope['device_ms']:.3f} ms on the GPU, "
+              f"{rope['host_build_and_upload_ms']:.1f} ms host build + upload", file=sys.stderr,
+              flush=True)
         secondary = {
             "video_self_3120_tflops": round(c1["kernel_tflops"], 2),
             "video_self_3120_pct_peak": round(c1["pct_peak"], 2),
@@ -357,6 +387,8 @@ def main():
             "dit_block_attn_kernel_ms": c5["kernel_ms"],
             "video_self_12480_kernel_ms_min_max": [round(c4["kernel_ms_min"], 4),
                                                    round(c4["kernel_ms_max"], 4)],
+            "rope_tables_12480_device_ms": round(rope["device_ms"], 4),
+            "rope_tables_12480_host_build_upload_ms": round(rope["host_build_and_upload_ms"], 2),
         }
 
     traffic = None

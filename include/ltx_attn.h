@@ -178,6 +178,16 @@ int32_t ltx_rope_tables(const float *positions, int32_t n_pos, int32_t tokens, i
                         const int32_t *max_pos, int32_t heads, double theta, uint16_t *cos_out,
                         uint16_t *sin_out);
 
+/* The same tables built on the GPU, asynchronously on `stream` (a hipStream_t or NULL):
+ * `positions` ([n_pos][tokens][2] float, 4-byte aligned) and `cos_out` / `sin_out` ([heads]
+ * [tokens][inner/2/heads] bf16 bit patterns) are DEVICE pointers; `max_pos` is a host array
+ * of n_pos (<= 8) counts. Same bits as ltx_rope_tables for the same positions. Arguments are
+ * checked before anything is launched (LTX_ATTN_EINVAL); LTX_ATTN_EHIP if the launch fails. */
+ltx_attn_status ltx_rope_tables_device(const float *positions, int32_t n_pos, int32_t tokens,
+                                       int32_t inner, const int32_t *max_pos, int32_t heads,
+                                       double theta, uint16_t *cos_out, uint16_t *sin_out,
+                                       void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,7 +65,7 @@ EXPORTED_SYMBOLS = (
     "ltx_attn_args_init", "ltx_attn_workspace_bytes", "ltx_attn_validate", "ltx_attn_fwd",
     "ltx_attn_status_string", "ltx_attn_last_error", "ltx_attn_provenance",
     "ltx_attn_abi_version", "ltx_attn_args_size", "ltx_rope_frequency_grid", "ltx_rope_video_positions",
-    "ltx_rope_audio_positions", "ltx_rope_tables",
+    "ltx_rope_audio_positions", "ltx_rope_tables", "ltx_rope_tables_device",
 )
 
 _lib = None
@@ -116,6 +116,11 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                     ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
                                     ctypes.c_double, ctypes.c_void_p, ctypes.c_void_p]
     lib.ltx_rope_tables.restype = ctypes.c_int32
+    lib.ltx_rope_tables_device.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                           ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
+                                           ctypes.c_double, ctypes.c_void_p, ctypes.c_void_p,
+                                           ctypes.c_void_p]
+    lib.ltx_rope_tables_device.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -407,6 +412,56 @@ def rope_tables(positions: np.ndarray, inner: int, max_pos, heads: int = 32,
     if rc != 0:
         raise Failure(EINVAL, "bad rotary-table arguments")
     return cos, sin
+
+
+def rope_tables_device(positions, inner: int, max_pos, heads: int = 32,
+                       theta: float = 10000.0, stream=None):
+    """``rope_tables`` built on the GPU: ``positions`` is a float32 ``[n_pos, tokens, 2]``
+    tensor (moved to the current HIP device if it is not there); returns bf16 device tensors
+    ``(cos, sin)``, each ``[heads, tokens, inner/2/heads]``, with the host builder's bits."""
+    import torch
+
+    lib = load_library()
+    if isinstance(positions, np.ndarray):
+        positions = torch.from_numpy(np.ascontiguousarray(positions, dtype=np.float32))
+    if not positions.is_cuda:
+        positions = positions.to("cuda")
+    positions = positions.to(torch.float32).contiguous()
+    n_pos, tokens = positions.shape[0], positions.shape[1]
+    mp = np.ascontiguousarray(max_pos, dtype=np.int32)
+    if mp.size != n_pos:
+        raise Failure(EINVAL, "maxPos length must equal the positional dimension count")
+    per_head = inner // 2 // heads
+    cos = torch.empty((heads, tokens, per_head), dtype=torch.bfloat16, device=positions.device)
+    sin = torch.empty_like(cos)
+    if stream is None:
+        stream = torch.cuda.current_stream(positions.device).cuda_stream
+    _check(lib.ltx_rope_tables_device(ctypes.c_void_p(positions.data_ptr()), n_pos, tokens,
+                                      inner, mp.ctypes.data, heads, theta,
+                                      ctypes.c_void_p(cos.data_ptr()),
+                                      ctypes.c_void_p(sin.data_ptr()), ctypes.c_void_p(stream)))
+    cos._ltx_positions = positions  # noqa: SLF001 -- keep the input alive until the stream ran
+    return cos, sin
+
+
+def rotaries_device(frames: int, height: int, width: int, frame_rate: float = 24.0,
+                    video_width: int = 4096, audio_width: int = 2048, heads: int = 32,
+                    theta: float = 10000.0, audio_tokens: Optional[int] = None):
+    """``rotaries`` with the tables built on the GPU: the positions (a few floats per token)
+    are built on the host and copied; the tables are written in device memory. Returns
+    ``Rotary`` pairs of bf16 device tensors keyed like ``rotaries``."""
+    lf = 1 if frames <= 1 else (frames - 1) // 8 + 1
+    video = rope_video_positions(lf, height // 32, width // 32, 8, 32, frame_rate)
+    if audio_tokens is None:
+        audio_tokens = int(round(frames / frame_rate * 25.0))
+    audio = rope_audio_positions(audio_tokens)
+    out = {
+        "videoSelf": rope_tables_device(video, video_width, [20, 2048, 2048], heads, theta),
+        "audioSelf": rope_tables_device(audio, audio_width, [20], heads, theta),
+        "videoCross": rope_tables_device(video[0:1], audio_width, [20], heads, theta),
+        "audioCross": rope_tables_device(audio, audio_width, [20], heads, theta),
+    }
+    return {k: Rotary(c, s) for k, (c, s) in out.items()}
 
 
 def rotaries(frames: int, height: int, width: int, frame_rate: float = 24.0,

@@ -271,6 +271,32 @@ def test_rope_builders_reject_bad_arguments():
         L.rope_tables(np.zeros((1, 4, 2), np.float32), 2048, [0], 32)   # maxPos 0
 
 
+def test_device_rope_builder_rejects_bad_arguments():
+    """ltx_rope_tables_device checks everything before a launch: these return EINVAL on a
+    host without a GPU (the pointers are never dereferenced)."""
+    lib = L.load_library()
+    mp3 = (ctypes.c_int32 * 3)(20, 2048, 2048)
+    mp0 = (ctypes.c_int32 * 1)(0)
+    good = dict(positions=FAKE, n_pos=3, tokens=240, inner=4096, max_pos=mp3, heads=32,
+                theta=10000.0, cos=FAKE + 256, sin=FAKE + 512)
+
+    def call(**kw):
+        a = dict(good, **kw)
+        return lib.ltx_rope_tables_device(a["positions"], a["n_pos"], a["tokens"], a["inner"],
+                                          ctypes.cast(a["max_pos"], ctypes.c_void_p),
+                                          a["heads"], a["theta"], a["cos"], a["sin"], None)
+
+    assert call(n_pos=0) == L.EINVAL
+    assert call(n_pos=9) == L.EINVAL                 # more positional dims than supported
+    assert call(inner=4096, heads=3) == L.EINVAL     # 2048 columns do not split into 3 heads
+    assert call(n_pos=1, max_pos=mp0) == L.EINVAL    # maxPos 0
+    assert call(positions=FAKE + 2) == L.EINVAL      # float positions misaligned
+    assert call(cos=FAKE + 1) == L.EINVAL            # bf16 output misaligned
+    assert call(sin=None) == L.EINVAL
+    assert call(theta=0.0) == L.EINVAL
+    assert call(inner=6, n_pos=3) == L.EINVAL        # a one-element frequency grid
+
+
 def test_cpp_host_mirror_error_behaviour(tmp_path):
     """The C++ DiTAttention mirror (ltx-2.5-swift_amd/host/dit_attention.hpp) throws the
     reference's structural failures before anything reaches a device."""
