@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define LTX_ATTN_ABI_VERSION 2
+#define LTX_ATTN_ABI_VERSION 3
 
 /* Status codes. The reference throws `DiTAttention.Failure` for structural errors
  * (DiTAttention.swift:107-121); a Swift wrapper maps these onto thrown errors. */
@@ -114,6 +114,12 @@ typedef struct ltx_attn_args {
      * before its bf16 rounding. NULL = no gate (the modules without to_gate_logits). */
     const void *gate_logits;      /* bf16 device pointer, 2-byte aligned                     */
     int64_t g_bs, g_rs, g_hs;     /* non-negative element strides                             */
+
+    /* STG passthrough (DiTAttention.swift:351-356, `allPerturbed`): nonzero = the module is
+     * fully perturbed, so out = V (times the gate, if given) per head, with no attention, no
+     * norm and no RoPE: q, k, their norm weights and tables are ignored and may be NULL, and
+     * no workspace is needed. Self-attention only (Lq == Lk). */
+    int32_t all_perturbed;
 } ltx_attn_args;
 
 /* Fill `a` with defaults: zero sizes and pointers, norm_eps = 1e-6, kprep AUTO, splits auto. */

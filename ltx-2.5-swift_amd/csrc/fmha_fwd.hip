@@ -662,7 +662,45 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineParams p) {
                d) = w;
 }
 
+// ------------------------------------------------------------------------------------------
+// STG passthrough (DiTAttention.swift:351-356): the module's output is V itself, split into
+// heads, times the gate when the module has one. One thread per 16-byte unit of a row.
+// ------------------------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void passthrough_kernel(const PassParams p) {
+    constexpr int U = D / 8;                   // 16-byte units per (token, head) row
+    const int64_t unit = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t rows = (int64_t)p.B * p.L * p.H;
+    if (unit >= rows * U) return;
+    const int64_t row = unit / U;
+    const int u = (int)(unit % U);
+    const int hh = (int)(row % p.H);
+    const int64_t bl = row / p.H;
+    const int l = (int)(bl % p.L), b = (int)(bl / p.L);
+    u32x4 w = ldg16((const bf16 *)p.v + (int64_t)b * p.v_bs + (int64_t)l * p.v_rs +
+                    (int64_t)hh * p.v_hs + 8 * u);
+    if (p.gate) {
+        const float g = gate_factor(p.gate, p.g_bs, p.g_rs, p.g_hs, b, l, hh);
+        float x[8];
+        unpack8(w, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= g;
+        w = pack8(x);
+    }
+    *(u32x4 *)((bf16 *)p.o + (int64_t)b * p.o_bs + (int64_t)l * p.o_rs + (int64_t)hh * p.o_hs +
+               8 * u) = w;
+}
+
 }  // namespace
+
+int launch_passthrough(const PassParams &p, int D, void *stream) {
+    const int64_t units = (int64_t)p.B * p.L * p.H * (D / 8);
+    const dim3 grid((unsigned)((units + 255) / 256)), block(256);
+    hipStream_t st = (hipStream_t)stream;
+    if (D == 128) hipLaunchKernelGGL(passthrough_kernel<128>, grid, block, 0, st, p);
+    else hipLaunchKernelGGL(passthrough_kernel<64>, grid, block, 0, st, p);
+    return (int)hipGetLastError();
+}
 
 int launch_fmha(const FmhaParams &p, int D, int kind, void *stream) {
     if (kind == kDma) return launch_fmha_dma(p, D, stream);

@@ -78,6 +78,17 @@ struct CombineParams {
     int64_t g_bs, g_rs, g_hs;
 };
 
+// STG passthrough: out = V (x 2*sigmoid(gate logit)) per (batch, token, head) row.
+struct PassParams {
+    const void *v;
+    int64_t v_bs, v_rs, v_hs;
+    void *o;
+    int64_t o_bs, o_rs, o_hs;
+    int32_t B, L, H;
+    const void *gate;
+    int64_t g_bs, g_rs, g_hs;
+};
+
 // Launchers (fmha_fwd.hip). Return the hipError_t of the launch as int.
 // Attention kernels:
 //   kRegPlain  K and V staged through registers (V transposed on the way into LDS)
@@ -89,5 +100,6 @@ int launch_fmha(const FmhaParams &p, int D, int kind, void *stream);
 int launch_fmha_dma(const FmhaParams &p, int D, void *stream);   // fmha_dma.hip
 int launch_prep(const PrepParams &p, int D, void *stream);
 int launch_combine(const CombineParams &p, int D, void *stream);
+int launch_passthrough(const PassParams &p, int D, void *stream);
 
 }  // namespace ltx

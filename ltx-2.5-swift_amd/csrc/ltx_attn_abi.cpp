@@ -43,6 +43,7 @@ constexpr double kSplitCharge = 0.02;
 struct Plan {
     bool q_norm = false, k_norm = false;
     bool q_rope = false, k_rope = false;
+    bool passthrough = false;  // STG passthrough: out = V (x gate), no attention
     bool dma = false;          // LDS-DMA kernel (K prologue when K needs work)
     bool k_prologue = false;   // K normalised/rotated by a separate pass into the workspace
     bool k_fused = false;      // K normalised/rotated while staging into LDS
@@ -90,6 +91,21 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
     if ((int64_t)H * D > 16384)
         return fail(LTX_ATTN_EUNSUPPORTED, "inner dim %lld above 16384", (long long)H * D);
     ltx_attn_status s;
+    if (a->all_perturbed) {
+        // STG passthrough: only V, the output and the gate take part.
+        if (a->Lq != a->Lk)
+            return fail(LTX_ATTN_EINVAL, "all_perturbed is self-attention only (Lq %d != Lk %d)",
+                        a->Lq, a->Lk);
+        if ((s = check_tensor("v", a->v, a->v_bs, a->v_rs, a->v_hs, B, a->Lk, H, D))) return s;
+        if ((s = check_tensor("out", a->out, a->o_bs, a->o_rs, a->o_hs, B, a->Lq, H, D)))
+            return s;
+        if (a->gate_logits && (((uintptr_t)a->gate_logits & 1u) || a->g_bs < 0 || a->g_rs < 0 ||
+                               a->g_hs < 0))
+            return fail(LTX_ATTN_EINVAL, "gate_logits misaligned or with a negative stride");
+        pl->passthrough = true;
+        pl->bytes = 0;
+        return LTX_ATTN_OK;
+    }
     if ((s = check_tensor("q", a->q, a->q_bs, a->q_rs, a->q_hs, B, a->Lq, H, D))) return s;
     if ((s = check_tensor("k", a->k, a->k_bs, a->k_rs, a->k_hs, B, a->Lk, H, D))) return s;
     if ((s = check_tensor("v", a->v, a->v_bs, a->v_rs, a->v_hs, B, a->Lk, H, D))) return s;
@@ -267,6 +283,18 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     make_plan(a, &pl);
     char *ws = (char *)a->workspace;
     const int B = a->B, H = a->H, D = a->D;
+
+    if (pl.passthrough) {
+        ltx::PassParams pp{};
+        pp.v = a->v; pp.v_bs = a->v_bs; pp.v_rs = a->v_rs; pp.v_hs = a->v_hs;
+        pp.o = a->out; pp.o_bs = a->o_bs; pp.o_rs = a->o_rs; pp.o_hs = a->o_hs;
+        pp.B = B; pp.L = a->Lq; pp.H = H;
+        pp.gate = a->gate_logits;
+        pp.g_bs = a->g_bs; pp.g_rs = a->g_rs; pp.g_hs = a->g_hs;
+        if (int e = ltx::launch_passthrough(pp, D, stream))
+            return fail(LTX_ATTN_EHIP, "passthrough launch: %s", hipGetErrorString((hipError_t)e));
+        return LTX_ATTN_OK;
+    }
 
     // 1. prologue passes: statistic (and, for the K prologue, the prepared K)
     if (pl.q_norm) {

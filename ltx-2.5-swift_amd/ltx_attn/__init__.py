@@ -58,6 +58,7 @@ class Args(ctypes.Structure):
         ("ev_attn_start", ctypes.c_void_p), ("ev_attn_stop", ctypes.c_void_p),
         ("gate_logits", ctypes.c_void_p),
         ("g_bs", ctypes.c_int64), ("g_rs", ctypes.c_int64), ("g_hs", ctypes.c_int64),
+        ("all_perturbed", ctypes.c_int32),
     ]
 
 
@@ -216,18 +217,23 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
                   key_rotary: Optional[Rotary] = None,
                   k_valid_len: Optional[Sequence[int]] = None, scale: Optional[float] = None,
                   out=None, kprep: int = KPREP_AUTO, num_splits: int = 0, stream=None,
-                  workspace=None, events=None, gate_logits=None):
+                  workspace=None, events=None, gate_logits=None, all_perturbed: bool = False):
     """One call of ``ltx_attn_fwd``. Tensors are torch bf16 on the current HIP device.
 
     ``layout="merged"``: q ``[B, Lq, H*D]``, k/v ``[B, Lk, H*D]``, out ``[B, Lq, H*D]``.
     ``layout="split"``:  q ``[B, H, Lq, D]``, k/v ``[B, H, Lk, D]``, out ``[B, H, Lq, D]``.
     ``gate_logits``: bf16 ``[B, Lq, H]`` (the output of ``to_gate_logits(x)``); each output row
     of head h is multiplied by ``2*sigmoid(logit)`` (``DiTAttention.swift:395-399``).
+    ``all_perturbed``: the STG passthrough (``:351-356``): ``out = v`` per head (times the
+    gate), no attention; ``q`` and ``k`` may then be None.
     Returns ``out``.
     """
     import torch
 
     lib = load_library()
+    if all_perturbed:
+        q = v if q is None else q
+        k = v if k is None else k
     if layout == "merged":
         B, Lq, inner = q.shape
         Lk = k.shape[1]
@@ -279,6 +285,7 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
     a.num_splits = num_splits
     if events is not None:
         a.ev_attn_start, a.ev_attn_stop = events
+    a.all_perturbed = 1 if all_perturbed else 0
     if gate_logits is not None:
         if gate_logits.dtype != torch.bfloat16 or not gate_logits.is_cuda:
             raise Failure(EINVAL, "gate_logits must be a bf16 device tensor")
@@ -351,7 +358,7 @@ class DiTAttentionCore:
             raise RotaryWithoutPosition(variant)
         if key_rotary is not None and rotary is None:
             raise Failure(EINVAL, "keyRotary without rotary")
-        inner = q.shape[-1]
+        inner = (v if q is None else q).shape[-1]
         if inner % self.heads:
             raise Failure(EINVAL, f"inner dim {inner} is not a multiple of {self.heads} heads")
         return attention_fwd(q, k, v, heads=self.heads, q_norm_w=self.q_norm_weight,

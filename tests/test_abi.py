@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layout_and_version():
     lib = L.load_library()
     assert lib.ltx_attn_args_size() == ctypes.sizeof(L.Args)
-    assert lib.ltx_attn_abi_version() == 2
+    assert lib.ltx_attn_abi_version() == 3
     assert "gfx950" in L.provenance()
     for s in range(5):
         assert lib.ltx_attn_status_string(s)
@@ -129,6 +129,22 @@ def test_gate_rules():
     lib = L.load_library()
     assert (lib.ltx_attn_workspace_bytes(ctypes.byref(_args(ws=False, gate_logits=FAKE)))
             == lib.ltx_attn_workspace_bytes(ctypes.byref(_args(ws=False))))
+
+
+def test_passthrough_rules():
+    """STG passthrough (DiTAttention.swift:351-356): q and k are not needed (NULL is fine),
+    nothing is allocated, and it is refused for cross-attention (Lq != Lk)."""
+    lib = L.load_library()
+    a = _args(ws=False, all_perturbed=1, q=0, k=0, q_norm_w=FAKE, q_cos=FAKE)
+    st, msg = _validate(a)
+    assert st == L.OK, msg
+    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == 0
+    st, msg = _validate(_args(ws=False, all_perturbed=1, Lq=3120, Lk=1024))
+    assert st == L.EINVAL and "self-attention" in msg
+    st, msg = _validate(_args(ws=False, all_perturbed=1, v=0))
+    assert st == L.EINVAL
+    st, msg = _validate(_args(ws=False, all_perturbed=1, gate_logits=FAKE + 1))
+    assert st == L.EINVAL and "gate_logits" in msg
 
 
 def test_rotary_rules():

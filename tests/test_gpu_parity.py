@@ -227,6 +227,34 @@ def test_output_gate(device, case):
     assert off.size and np.abs(off).max() < 1e-4
 
 
+@pytest.mark.parametrize("gated", [False, True])
+def test_stg_passthrough(device, gated):
+    """A fully perturbed module (DiTAttention.swift:351-356) returns V split into heads, times
+    the bf16 gate when it has one (:395-399), with no attention: out is V bit for bit, or the
+    one bf16 rounding of V x gate."""
+    import torch
+
+    B, H, L_, D = 2, 32, 300, 128
+    _say(f"STG passthrough gated={gated}")
+    v = O.randn_bf16_bits((B, L_, H * D), 81)
+    tv = dev(v, device)
+    kw = {}
+    g = None
+    if gated:
+        g = _gate_bits((B, L_, H), 82)
+        kw["gate_logits"] = dev(g, device)
+    core = L.DiTAttentionCore(None, None)
+    out = core(None, None, tv, variant=L.Variant.videoSelf, all_perturbed=True, **kw)
+    torch.cuda.synchronize()
+    got = host_bits(out)
+    if not gated:
+        assert np.array_equal(got, v)
+    else:
+        want = O.f32_to_bf16_bits(O.bf16_bits_to_f32(v).reshape(B, L_, H, D) *
+                                  O.head_gate(g, "reference")[..., None]).reshape(v.shape)
+        assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("Lq", [40, 300])
 def test_batches_beyond_one_launch(device, Lq):
     """B = 66 unmasked batch rows run as launches of 64 + 2 rows (the per-row key lengths
