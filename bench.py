@@ -230,10 +230,19 @@ def bench_c5(device, steps, warmup, hip):
         nk = Lk if vl is None else vl[0]
         flops += 4.0 * q.shape[0] * Lq * nk * inner
 
+    # the block driver runs the six calls in block order (the same calls as listed above)
+    norms = {name: (w, w) for name, _, _, w, _, _, _ in calls}
+    names = [c[0] for c in calls]
+    io = {name: (c[1], c[2], c[2], outs[i]) for i, (name, c) in enumerate(zip(names, calls))}
+    tables = {"videoSelf": rot["videoSelf"], "audioSelf": rot["audioSelf"],
+              "videoCross": rot["videoCross"], "audioCross": rot["audioCross"]}
+    block = L.DiTBlockAttention(norms)
+
     def call(ev):
-        for i, (_, q, kv, w, r, kr, vl) in enumerate(calls):
-            L.attention_fwd(q, kv, kv, heads=32, q_norm_w=w, k_norm_w=w, rotary=r,
-                            key_rotary=kr, k_valid_len=vl, out=outs[i], workspace=ws)
+        block.self_attention(io["attn1"], io["audio_attn1"], tables, workspace=ws)
+        block.text_cross(io["attn2"], io["audio_attn2"], valid, workspace=ws)
+        block.cross_modal(io["audio_to_video_attn"], io["video_to_audio_attn"], tables,
+                          workspace=ws)
 
     wall, _ = time_steps(call, steps, warmup, hip, events_per_step=False)
     # per-attention kernel time (one call each, events around the attention kernel)

@@ -77,13 +77,15 @@ public:
     // v = to_v(context) (pre-norm); `rotary` is `pe`, `keyRotary` is `k_pe` (nullptr means
     // "use pe for both", :310-314). `out` receives [B, Lq, H*D] bf16. With `gate_logits`
     // (bf16 [B, Lq, H] contiguous: to_gate_logits(x)) each head's rows are multiplied by
-    // 2*sigmoid(logit), as the module's gate does (:395-399). Throws Failure.
+    // 2*sigmoid(logit), as the module's gate does (:395-399). `allPerturbed` is the STG
+    // passthrough (:351-356): out = V per head (times the gate); q and k are not read (their
+    // `data` may be null, `tokens` still gives Lq). Throws Failure.
     void operator()(int32_t batch, int32_t inner, const Stream &q, const Stream &k,
                     const Stream &v, void *out, int64_t out_batch_stride,
                     int64_t out_row_stride, Variant variant, const Rotary *rotary,
                     const Rotary *keyRotary, void *workspace, size_t workspace_bytes,
                     void *stream, const int32_t *k_valid_len = nullptr,
-                    const void *gate_logits = nullptr) const {
+                    const void *gate_logits = nullptr, bool allPerturbed = false) const {
         if (rotary && !takesRotary(variant))
             throw Failure(LTX_ATTN_EINVAL,
                           std::string(rawValue(variant)) +
@@ -99,6 +101,7 @@ public:
                                rotary, keyRotary, k_valid_len);
         a.workspace = workspace;
         a.workspace_bytes = workspace_bytes;
+        a.all_perturbed = allPerturbed ? 1 : 0;
         if (gate_logits) {
             a.gate_logits = gate_logits;
             a.g_bs = (int64_t)q.tokens * heads;
@@ -111,7 +114,9 @@ public:
     // Workspace the same call needs (0 if none).
     size_t workspaceBytes(int32_t batch, int32_t inner, const Stream &q, const Stream &k,
                           const Stream &v, Variant, const Rotary *rotary,
-                          const Rotary *keyRotary, const int32_t *k_valid_len = nullptr) const {
+                          const Rotary *keyRotary, const int32_t *k_valid_len = nullptr,
+                          bool allPerturbed = false) const {
+        if (allPerturbed) return 0;
         // The output only has to be a valid-looking tensor for sizing; q's geometry is used.
         ltx_attn_args a = args(batch, inner, q, k, v, const_cast<void *>(q.data),
                                q.batch_stride, q.row_stride, rotary, keyRotary, k_valid_len);

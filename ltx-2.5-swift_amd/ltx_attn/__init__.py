@@ -367,6 +367,50 @@ class DiTAttentionCore:
                              **kw)
 
 
+class DiTBlockAttention:
+    """The six attention calls of one DiT block in the reference's order
+    (``Sources/LTXModules/DiTBlock.swift:343-438``), phase by phase, on one stream with one
+    workspace; the Python mirror of ``ltx-2.5-swift_amd/host/dit_block.hpp``.
+
+    ``norms`` maps each variant's raw value (``attn1``, ``audio_attn1``, ``attn2``,
+    ``audio_attn2``, ``audio_to_video_attn``, ``video_to_audio_attn``) to its
+    ``(q_norm.weight, k_norm.weight)``. Each call takes ``(q, k, v, out)`` merged-layout
+    tensors and an optional ``gate`` (``[B, Lq, 32]`` logits). Between phases the caller
+    updates the residual streams and projects the next inputs; phase 3's inputs come from the
+    streams as they stood before audio-to-video (the snapshot, ``:383-387``).
+    """
+
+    def __init__(self, norms):
+        self.m = {v: DiTAttentionCore(*norms[v.value]) for v in Variant}
+
+    def _run(self, variant, io, workspace, **kw):
+        q, k, v, out = io[:4]
+        gate = io[4] if len(io) > 4 else None
+        return self.m[variant](q, k, v, variant=variant, out=out, workspace=workspace,
+                               gate_logits=gate, **kw)
+
+    def self_attention(self, video, audio, rot, video_perturbed=False, audio_perturbed=False,
+                       workspace=None):
+        """attn1 and audio_attn1 (:343-368); a perturbed stream takes the STG passthrough."""
+        self._run(Variant.videoSelf, video, workspace, rotary=rot["videoSelf"],
+                  all_perturbed=video_perturbed)
+        self._run(Variant.audioSelf, audio, workspace, rotary=rot["audioSelf"],
+                  all_perturbed=audio_perturbed)
+
+    def text_cross(self, video, audio, text_valid_len=None, workspace=None):
+        """attn2 and audio_attn2 (:370-381): text K/V, valid tokens per batch row (CFG)."""
+        self._run(Variant.videoCross, video, workspace, k_valid_len=text_valid_len)
+        self._run(Variant.audioCross, audio, workspace, k_valid_len=text_valid_len)
+
+    def cross_modal(self, a2v, v2a, rot, workspace=None):
+        """audio_to_video then video_to_audio (:383-435); pe is the query stream's cross grid,
+        k_pe the other stream's."""
+        self._run(Variant.audioToVideo, a2v, workspace, rotary=rot["videoCross"],
+                  key_rotary=rot["audioCross"])
+        self._run(Variant.videoToAudio, v2a, workspace, rotary=rot["audioCross"],
+                  key_rotary=rot["videoCross"])
+
+
 # --------------------------------------------------------------------------------------
 # RoPE tables (host, through the C ABI)
 # --------------------------------------------------------------------------------------

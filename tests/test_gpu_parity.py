@@ -507,3 +507,60 @@ def test_c5_block_set(device):
         _sample_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, ranges, [5],
                       f"c5 {label}")
         torch.cuda.synchronize()
+
+
+def test_block_driver_matches_single_calls(device):
+    """The block driver (DiTBlock.swift:343-438 order, one workspace) gives each module's
+    output bit for bit as its own call does: CFG rows with different text lengths, a gated
+    audio->video call, and a perturbed (STG passthrough) video self-attention."""
+    import torch
+
+    B, Ta, Tt = 2, 152, 1024
+    rot = L.rotaries_device(25, 320, 480, audio_tokens=Ta)
+    Tv = rot["videoSelf"].cos.shape[1]
+    _say(f"block driver: {Tv} video / {Ta} audio / {Tt} text tokens, B={B}")
+
+    def t(shape, seed, mean=0.0, std=1.0):
+        g = torch.Generator(device=device)
+        g.manual_seed(0x5EED + seed)
+        return (torch.randn(shape, generator=g, device=device) * std + mean).to(torch.bfloat16)
+
+    norms = {v.value: (t((4096 if v in (L.Variant.videoSelf, L.Variant.videoCross) else 2048,),
+                         100 + i, 1.0, 0.02),) * 2 for i, v in enumerate(L.Variant)}
+    v4, a2, t4, t2, v2 = (t((B, Tv, 4096), 1), t((B, Ta, 2048), 2), t((B, Tt, 4096), 3),
+                          t((B, Tt, 2048), 4), t((B, Tv, 2048), 5))
+    gate = t((B, Tv, 32), 6, 0.0, 2.0)
+    valid = [94, 11]
+    io = {
+        "attn1": (v4, v4, v4, torch.empty_like(v4)),
+        "audio_attn1": (a2, a2, a2, torch.empty_like(a2)),
+        "attn2": (v4, t4, t4, torch.empty_like(v4)),
+        "audio_attn2": (a2, t2, t2, torch.empty_like(a2)),
+        "audio_to_video_attn": (v2, a2, a2, torch.empty_like(v2), gate),
+        "video_to_audio_attn": (a2, v2, v2, torch.empty_like(a2)),
+    }
+    ws = torch.empty(256 << 20, dtype=torch.uint8, device=device)
+    blk = L.DiTBlockAttention(norms)
+    blk.self_attention(io["attn1"], io["audio_attn1"], rot, video_perturbed=True, workspace=ws)
+    blk.text_cross(io["attn2"], io["audio_attn2"], valid, workspace=ws)
+    blk.cross_modal(io["audio_to_video_attn"], io["video_to_audio_attn"], rot, workspace=ws)
+    torch.cuda.synchronize()
+
+    def single(name, **kw):
+        q, k, v = io[name][:3]
+        w = norms[name][0]
+        return L.attention_fwd(q, k, v, heads=32, q_norm_w=w, k_norm_w=w, **kw)
+
+    want = {
+        "attn1": v4,                                   # passthrough: V itself
+        "audio_attn1": single("audio_attn1", rotary=rot["audioSelf"]),
+        "attn2": single("attn2", k_valid_len=valid),
+        "audio_attn2": single("audio_attn2", k_valid_len=valid),
+        "audio_to_video_attn": single("audio_to_video_attn", rotary=rot["videoCross"],
+                                      key_rotary=rot["audioCross"], gate_logits=gate),
+        "video_to_audio_attn": single("video_to_audio_attn", rotary=rot["audioCross"],
+                                      key_rotary=rot["videoCross"]),
+    }
+    torch.cuda.synchronize()
+    for name, w in want.items():
+        assert torch.equal(io[name][3], w), name
