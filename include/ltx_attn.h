@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define LTX_ATTN_ABI_VERSION 3
+#define LTX_ATTN_ABI_VERSION 4
 
 /* Status codes. The reference throws `DiTAttention.Failure` for structural errors
  * (DiTAttention.swift:107-121); a Swift wrapper maps these onto thrown errors. */
@@ -120,6 +120,15 @@ typedef struct ltx_attn_args {
      * norm and no RoPE: q, k, their norm weights and tables are ignored and may be NULL, and
      * no workspace is needed. Self-attention only (Lq == Lk). */
     int32_t all_perturbed;
+
+    /* RMS statistic from the projection (ltx_linear's sumsq output): fp32 partial sums of
+     * squares of each token's q (k) values, row b*Lq + l (b*Lk + l) at q_sumsq + row*q_sumsq_rs,
+     * `sumsq_blocks` partials per row whose sum covers all H*D channels. Given with q_norm_w
+     * (k_norm_w), the norm takes its statistic from them instead of a pass over q (k).
+     * NULL = statistic computed here. The partials must describe the q (k) being passed. */
+    const float *q_sumsq, *k_sumsq;
+    int64_t q_sumsq_rs, k_sumsq_rs;   /* >= sumsq_blocks                                  */
+    int32_t sumsq_blocks;             /* >= 1 when either pointer is given                */
 } ltx_attn_args;
 
 /* Fill `a` with defaults: zero sizes and pointers, norm_eps = 1e-6, kprep AUTO, splits auto. */
@@ -153,6 +162,40 @@ int32_t ltx_attn_abi_version(void);
 /* sizeof(ltx_attn_args) as compiled into the library, so an FFI mirror of the struct
  * (Swift, ctypes, ...) can verify its layout at load time. */
 size_t ltx_attn_args_size(void);
+
+/* ----------------------------------------------------------------------------------------
+ * Projection GEMM: `linear` of DiTAttention.swift:178-188, y = x . w^T (+ bias), with the
+ * RMS-norm statistic of y from the epilogue (the q_norm / k_norm that follow, :202-204).
+ * -------------------------------------------------------------------------------------- */
+
+/* Columns of y covered by one partial sum of squares. */
+#define LTX_LINEAR_SUMSQ_COLS 256
+
+typedef struct ltx_linear_args {
+    int32_t M, N, K;              /* y [M, N] = x [M, K] . w [N, K]^T; N % 8 == 0, K % 64 == 0 */
+    const void *x;                /* bf16 device pointer, 16-byte aligned; row stride x_rs
+                                     (x and y may be NULL when M is 0)                        */
+    const void *w;                /* bf16 [N, K], the checkpoint's [out, in] layout; 16-byte   */
+    const void *bias;             /* bf16 [N] (8-byte aligned), or NULL                       */
+    void *y;                      /* bf16, 8-byte aligned, row stride y_rs; must not overlap x/w */
+    int64_t x_rs, w_rs, y_rs;     /* element strides: x_rs, w_rs >= K, multiples of 8;
+                                     y_rs >= N, a multiple of 4                                */
+    /* NULL, or fp32 [M][ltx_linear_sumsq_blocks(N)] at row stride sumsq_rs (4-byte aligned):
+     * partial j of row m = sum of y[m][n]^2 (the bf16 outputs, in fp32) over the columns
+     * n in [256 j, 256 j + 256). Column ranges that start at a multiple of 256 (q, k of a
+     * fused projection) have their own partials. */
+    float *sumsq;
+    int64_t sumsq_rs;
+} ltx_linear_args;
+
+/* ceil(N / LTX_LINEAR_SUMSQ_COLS): partial sums per row of y. */
+int32_t ltx_linear_sumsq_blocks(int32_t N);
+
+/* Run the projection asynchronously on `stream` (a hipStream_t or NULL). The fp32
+ * accumulator is rounded to bf16, then the bias is added in fp32 and rounded again, as the
+ * reference's matmul and add do (:180, :186). M == 0 launches nothing. LoRA deltas (:183-185)
+ * are not applied here. */
+ltx_attn_status ltx_linear(const ltx_linear_args *a, void *stream);
 
 /* ----------------------------------------------------------------------------------------
  * RoPE table construction (host side, no GPU): the reference builds these once per forward

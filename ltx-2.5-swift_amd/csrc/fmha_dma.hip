@@ -24,13 +24,10 @@
 //     compile-time LDS object.
 #include <type_traits>
 
-#include "fmha_device.hpp"
+#include "lds_copy.hpp"
 
 namespace ltx {
 namespace {
-
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) bf16 lds_bf16;
 
 template <int D>
 struct DmaTile {
@@ -108,26 +105,6 @@ __device__ __forceinline__ void s_defined(f32x16 &x, f32x16 &y, const f32x16 &c0
     asm volatile("; s_defined %0 %1" : "+v"(x), "+v"(y) : "v"(c0), "v"(c1));
 }
 
-// s_waitcnt vmcnt(0), expcnt and lgkmcnt left at their maxima: this wave's copies landed.
-__device__ __forceinline__ void wait_copies() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// s_waitcnt vmcnt(n) (n < 64), expcnt and lgkmcnt left at their maxima.
-
-// A copy HBM -> LDS: every lane (all are enabled wherever the kernel copies) moves 16 bytes
-// from the buffer at its offset to M0 + 16*lane. As one assembly statement the compiler sees
-// no memory load, so its waits never account for these; the kernel waits for them itself
-// (vmcnt). The s_nop is the wait state an M0 write needs before the load. The compiler keeps
-// nothing in M0 in these kernels, so the clobber costs nothing.
-__device__ __forceinline__ void copy_all(u32x4 rs, uint32_t lds_byte, int voff) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %1, %2, 0 offen lds"
-        :
-        : "s"(lds_byte), "v"(voff), "s"(rs)
-        : "m0", "memory");
-}
-
 template <int D>
 __global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(1, 1)))
 void fmha_dma_kernel(const FmhaParams p) {
@@ -164,11 +141,6 @@ void fmha_dma_kernel(const FmhaParams p) {
     const int64_t vrow_bytes = p.v_rs * 2;
     // Resources over this (batch, head)'s valid keys: rows past them arrive as zeros; a tile's
     // offset goes into the per-lane offset.
-    auto rsrc_words = [&](const void *base, int64_t bytes) __attribute__((always_inline)) {
-        const uint64_t a = (uint64_t)base;
-        const uint32_t n = bytes <= 0 ? 0u : (bytes >= 0x7fffffff ? 0x7fffffffu : (uint32_t)bytes);
-        return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, n, (uint32_t)kRsrcWord3};
-    };
     const u32x4 rkw = rsrc_words(Kb, (int64_t)n_valid * krow_bytes);
     const u32x4 rvw = rsrc_words(Vb, (int64_t)n_valid * vrow_bytes);
     // Copy j of this wave's share of a K (V) tile: lane byte offsets within a tile (fixed for

@@ -579,7 +579,14 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const PrepParams p) {
         }
     }
     float rstd = 1.0f;
-    if (p.w) {
+    if (p.w && p.sumsq) {
+        // The projection's partial sums, added in order (every thread reads the same row).
+        const float *parts = p.sumsq + (int64_t)rid * p.ss_rs;
+        float tot = 0.f;
+        for (int j = 0; j < p.ss_blocks; ++j) tot += parts[j];
+        rstd = 1.0f / sqrtf(tot / (float)inner + p.eps);
+        if (tid == 0 && p.rstd) p.rstd[rid] = rstd;
+    } else if (p.w) {
         __shared__ float red[4];
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
@@ -622,6 +629,19 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const PrepParams p) {
         *(u32x4 *)(dst + hh * D + 8 * c) = pack8(x1[k]);
         *(u32x4 *)(dst + hh * D + D / 2 + 8 * c) = pack8(x2[k]);
     }
+}
+
+// ------------------------------------------------------------------------------------------
+// RMS statistic from the projection's partial sums of squares: one thread per token row,
+// partials added in order, the same formula as the prologue's.
+// ------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rstd_kernel(const RstdParams p) {
+    const int row = blockIdx.x * 256 + threadIdx.x;
+    if (row >= p.rows) return;
+    const float *parts = p.sumsq + (int64_t)row * p.rs;
+    float tot = 0.f;
+    for (int j = 0; j < p.blocks; ++j) tot += parts[j];
+    p.rstd[row] = 1.0f / sqrtf(tot / (float)p.n + p.eps);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -714,6 +734,12 @@ int launch_fmha(const FmhaParams &p, int D, int kind, void *stream) {
         if (k_fused) hipLaunchKernelGGL((fmha_fwd_kernel<64, true>), grid, block, 0, st, p);
         else hipLaunchKernelGGL((fmha_fwd_kernel<64, false>), grid, block, 0, st, p);
     }
+    return (int)hipGetLastError();
+}
+
+int launch_rstd(const RstdParams &p, void *stream) {
+    const dim3 grid((unsigned)((p.rows + 255) / 256)), block(256);
+    hipLaunchKernelGGL(rstd_kernel, grid, block, 0, (hipStream_t)stream, p);
     return (int)hipGetLastError();
 }
 

@@ -64,6 +64,11 @@ struct PrepParams {
     const void *cos, *sin;           // bf16 [H][L][D/2] or null
     float *rstd;                     // [B][L] or null
     void *out;                       // bf16 [B][L][H*D] contiguous or null
+    // Statistic given as partial sums of squares (row b*L + l at sumsq + row*ss_rs, ss_blocks
+    // partials), or null: computed from x.
+    const float *sumsq;
+    int64_t ss_rs;
+    int32_t ss_blocks;
 };
 
 // Split-KV combine over the tail items' rows.
@@ -89,6 +94,31 @@ struct PassParams {
     int64_t g_bs, g_rs, g_hs;
 };
 
+// Projection GEMM y = x . w^T (+ bias) over 256 x 256 output tiles, with the per-row sum of
+// squares of each tile's bf16 outputs (the RMS-norm statistic of the projection).
+constexpr int kLinearTile = 256;
+struct LinearParams {
+    const void *x;                   // bf16 [M][K], row stride x_rs elements
+    const void *w;                   // bf16 [N][K], row stride w_rs elements
+    const void *bias;                // bf16 [N] or null
+    void *y;                         // bf16 [M][N], row stride y_rs elements
+    int64_t x_rs, w_rs, y_rs;
+    float *sumsq;                    // [M][ceil(N/256)] (row stride ss_rs floats) or null
+    int64_t ss_rs;
+    int32_t M, N, K;
+    int32_t tiles_m, tiles_n;
+};
+
+// RMS statistic from partial sums of squares: rstd[row] = 1/sqrt(sum_j parts[row][j] / n + eps)
+// for rows [0, rows); parts row r at sumsq + r*rs, `blocks` partials.
+struct RstdParams {
+    const float *sumsq;
+    int64_t rs;
+    int32_t rows, blocks, n;
+    float eps;
+    float *rstd;
+};
+
 // Launchers (fmha_fwd.hip). Return the hipError_t of the launch as int.
 // Attention kernels:
 //   kRegPlain  K and V staged through registers (V transposed on the way into LDS)
@@ -101,5 +131,7 @@ int launch_fmha_dma(const FmhaParams &p, int D, void *stream);   // fmha_dma.hip
 int launch_prep(const PrepParams &p, int D, void *stream);
 int launch_combine(const CombineParams &p, int D, void *stream);
 int launch_passthrough(const PassParams &p, int D, void *stream);
+int launch_rstd(const RstdParams &p, void *stream);
+int launch_linear(const LinearParams &p, void *stream);           // linear_gemm.hip
 
 }  // namespace ltx

@@ -1,0 +1,208 @@
+// Projection GEMM of the attention modules, y = x . w^T (+ bias), following
+// Sources/LTXModules/DiTAttention.swift:178-188 (`linear`: matmul in the weight's dtype, then
+// the bias add), with the RMS-norm statistic of the result emitted by the epilogue: for every
+// row of y, the sum of squares of its bf16 values over each 256-column tile, so the q_norm /
+// k_norm that follow (:202-204) need no pass of their own over q and k.
+//
+// Layout: x [M][K] and w [N][K] (the checkpoint's [out, in] layout) are both K-contiguous;
+// y [M][N] row-major. One workgroup of four waves computes a 256 x 256 tile of y; wave (wm, wn)
+// owns rows wm*128.. and columns wn*128.. as 4 x 4 products of v_mfma_f32_32x32x16_bf16 in
+// which w is the A operand and x the B operand, so each lane's accumulators hold one row of y
+// and runs of four consecutive columns (8-byte stores, and the row's sum of squares stays in
+// the lane).
+//
+// Staging: every k step's 256 x BK tiles of x and w are copied HBM -> LDS by the
+// buffer-load-to-LDS path into one of NSTAGE buffers, NSTAGE - 1 steps ahead, rows of BK
+// elements with their 16-byte units XOR-swizzled so the operand reads (32 rows, one unit per
+// half-wave) are free of bank conflicts. The copies are untracked assembly; each step waits for
+// its own copies (vmcnt) and a barrier makes everyone's visible and frees the buffer the step
+// refills. Rows past M (N) read as zeros through the buffer resource's bound.
+//
+// Rounding follows the reference's two operations: the fp32 accumulator is rounded to bf16
+// (the matmul's output), then the bias is added in fp32 and the sum rounded to bf16 again.
+#include "lds_copy.hpp"
+
+namespace ltx {
+namespace {
+
+constexpr int LT = kLinearTile;       // 256 rows and columns of y per workgroup
+
+template <int BK, int NSTAGE>
+struct LinTile {
+    static constexpr int U = BK / 8;              // 16-byte units per LDS row
+    static constexpr int ELEMS = LT * BK;         // one operand's tile of one k step
+    static constexpr int CPT = LT * U / 64 / 4;   // copies per wave per operand tile
+    static constexpr int NCH = BK / 16;           // MFMA reduction chunks per k step
+    static_assert(BK == 64 || BK == 32, "k step");
+    static_assert(NSTAGE >= 2 && 2 * NSTAGE * ELEMS * 2 <= 160 * 1024, "LDS budget");
+    static_assert((NSTAGE - 2) * 2 * CPT < 64, "vmcnt range");
+};
+
+// Unit swizzle: the 16 lanes a 16-byte LDS read serves together read 16 consecutive rows at
+// one logical unit; XOR-ing the unit with bits of the row puts them in 16 distinct 16-byte
+// bank slots of a 256-byte window (rows of 8 units: 2 rows per window; of 4 units: 4).
+template <int U>
+__device__ __forceinline__ int lswz(int row, int u) {
+    return U == 8 ? (u ^ ((row >> 1) & 7)) : (u ^ ((row >> 2) & 3));
+}
+
+template <int BK, int NSTAGE>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void linear_kernel(const LinearParams p) {
+    using T = LinTile<BK, NSTAGE>;
+    constexpr int U = T::U, CPT = T::CPT, NCH = T::NCH, ELEMS = T::ELEMS;
+    __shared__ __attribute__((aligned(16))) bf16 sW[NSTAGE * ELEMS];
+    __shared__ __attribute__((aligned(16))) bf16 sX[NSTAGE * ELEMS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r = lane & 31, g = lane >> 5;
+
+    // Tile of this workgroup. Workgroups go to the 8 XCDs round-robin; each XCD gets a
+    // contiguous range of the tile order, which walks groups of 4 row tiles column tile by
+    // column tile, so the ~32 workgroups an XCD runs at once share 4 row tiles of x and 8
+    // column tiles of w in its L2.
+    const int total = p.tiles_m * p.tiles_n;
+    const int wg = blockIdx.x;
+    const int xcd = wg & 7, slot = wg >> 3;
+    const int q8 = total >> 3, r8 = total & 7;
+    const int t = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + slot;
+    constexpr int GRP = 4;
+    const int group = t / (GRP * p.tiles_n);
+    const int first_m = group * GRP;
+    const int rows_g = min(GRP, p.tiles_m - first_m);
+    const int within = t - group * GRP * p.tiles_n;
+    const int tm = first_m + within % rows_g, tn = within / rows_g;
+    const int m0 = tm * LT, n0 = tn * LT;
+
+    // ---- copies HBM -> LDS ----------------------------------------------------------
+    const int xrow = (int)(p.x_rs * 2), wrow = (int)(p.w_rs * 2);    // row bytes
+    const char *X0 = (const char *)p.x + (int64_t)m0 * xrow;
+    const char *W0 = (const char *)p.w + (int64_t)n0 * wrow;
+    const int64_t xbytes = (int64_t)min(LT, p.M - m0) * xrow;
+    const int64_t wbytes = (int64_t)min(LT, p.N - n0) * wrow;
+    // Copy j of this wave's share of a tile: LDS unit q = (wave*CPT + j)*64 + lane holds row
+    // q / U, logical unit lswz(row, q % U); its source offset is fixed for the whole tile, the
+    // k step moves the resource's base.
+    int xl[CPT], wl[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int q = (wave * CPT + j) * 64 + lane;
+        const int row = q / U, u = lswz<U>(row, q % U);
+        xl[j] = row * xrow + 16 * u;
+        wl[j] = row * wrow + 16 * u;
+    }
+    auto copy_step = [&](int s, int st) __attribute__((always_inline)) {
+        const int kb = s * BK * 2;
+        const u32x4 rx = rsrc_words(X0 + kb, xbytes);
+        const u32x4 rw = rsrc_words(W0 + kb, wbytes);
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            copy_all(rw, (uint32_t)(uintptr_t)((lds_bf16 *)sW + st * ELEMS + (wave * CPT + j) * 512), wl[j]);
+            copy_all(rx, (uint32_t)(uintptr_t)((lds_bf16 *)sX + st * ELEMS + (wave * CPT + j) * 512), xl[j]);
+        }
+    };
+    // Operand of rows row0 + 0..31, reduction chunk c: lane (r, g) reads row row0 + r, unit 2c + g.
+    auto frag = [&](const lds_bf16 *S, int row0, int c) __attribute__((always_inline)) {
+        const int row = row0 + r;
+        return *(const __attribute__((address_space(3))) bf16x8 *)(S + row * BK + 8 * lswz<U>(row, 2 * c + g));
+    };
+
+    f32x16 acc[4][4];              // [n block][m block]
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = splat16(0.f);
+
+    const int nsteps = p.K / BK;
+#pragma unroll
+    for (int s = 0; s < NSTAGE - 1; ++s)
+        if (s < nsteps) copy_step(s, s);
+    for (int s = 0; s < nsteps; ++s) {
+        if (s + NSTAGE - 2 < nsteps) wait_copies_but<(NSTAGE - 2) * 2 * CPT>();
+        else wait_copies();
+        __syncthreads();       // everyone's copies for step s landed; step s-1's reads done
+        const int st = s % NSTAGE;
+        if (s + NSTAGE - 1 < nsteps) copy_step(s + NSTAGE - 1, (s + NSTAGE - 1) % NSTAGE);
+        const lds_bf16 *Ws = (const lds_bf16 *)sW + st * ELEMS;
+        const lds_bf16 *Xs = (const lds_bf16 *)sX + st * ELEMS;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            bf16x8 a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[i] = frag(Ws, wn * 128 + 32 * i, c);
+                b[i] = frag(Xs, wm * 128 + 32 * i, c);
+            }
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = mfma32(a[nb], b[mb], acc[nb][mb]);
+        }
+    }
+
+    // ---- epilogue ---------------------------------------------------------------------
+    // Lane (r, g) of product (nb, mb) holds y[m][n + e] for m = m0 + wm*128 + 32*mb + r,
+    // n = n0 + wn*128 + 32*nb + 8*qd + 4*g (qd = 0..3), e = 0..3 in accumulator 4*qd + e.
+    u32x2 bias[4][4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            const int n = n0 + wn * 128 + 32 * nb + 8 * qd + 4 * g;
+            bias[nb][qd] = (p.bias && n < p.N) ? *(const u32x2 *)((const bf16 *)p.bias + n)
+                                               : u32x2{0u, 0u};
+        }
+    __shared__ float red[2][LT];
+    float ss[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+        const int m = m0 + wm * 128 + 32 * mb + r;
+        bf16 *yrow = (bf16 *)p.y + (int64_t)m * p.y_rs;
+        float sum = 0.f;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const int n = n0 + wn * 128 + 32 * nb + 8 * qd + 4 * g;
+                const f32x16 &c = acc[nb][mb];
+                u32x2 w;
+                w[0] = pack_bf2(c[4 * qd + 0], c[4 * qd + 1]);
+                w[1] = pack_bf2(c[4 * qd + 2], c[4 * qd + 3]);
+                if (p.bias) {
+                    w[0] = pack_bf2(bf_lo(w[0]) + bf_lo(bias[nb][qd][0]),
+                                    bf_hi(w[0]) + bf_hi(bias[nb][qd][0]));
+                    w[1] = pack_bf2(bf_lo(w[1]) + bf_lo(bias[nb][qd][1]),
+                                    bf_hi(w[1]) + bf_hi(bias[nb][qd][1]));
+                }
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const float lo = bf_lo(w[e]), hi = bf_hi(w[e]);
+                    sum += lo * lo;
+                    sum += hi * hi;
+                }
+                if (m < p.M && n < p.N) *(u32x2 *)(yrow + n) = w;
+            }
+        ss[mb] = sum + xlane32(sum);   // the wave's 128 columns (columns past N are zeros)
+    }
+    if (!p.sumsq) return;
+    if (g == 0) {
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) red[wn][wm * 128 + 32 * mb + r] = ss[mb];
+    }
+    __syncthreads();
+    const int m = m0 + tid;
+    if (m < p.M) p.sumsq[(int64_t)m * p.ss_rs + tn] = red[0][tid] + red[1][tid];
+}
+
+}  // namespace
+
+int launch_linear(const LinearParams &p, void *stream) {
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(256);
+    hipLaunchKernelGGL((linear_kernel<64, 2>), grid, block, 0, (hipStream_t)stream, p);
+    return (int)hipGetLastError();
+}
+
+}  // namespace ltx

@@ -13,6 +13,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <utility>
 
 #include "../../include/ltx_attn.h"
 #include "fmha_params.hpp"
@@ -42,6 +43,7 @@ constexpr double kSplitCharge = 0.02;
 // Everything ltx_attn_fwd decides from the arguments alone.
 struct Plan {
     bool q_norm = false, k_norm = false;
+    bool q_stat = false, k_stat = false;   // statistic from the projection's partial sums
     bool q_rope = false, k_rope = false;
     bool passthrough = false;  // STG passthrough: out = V (x gate), no attention
     bool dma = false;          // LDS-DMA kernel (K prologue when K needs work)
@@ -125,6 +127,20 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
         return fail(LTX_ATTN_EINVAL, "norm weights must be 16-byte aligned");
     if ((pl->q_norm || pl->k_norm) && !(a->norm_eps >= 0.f && isfinite(a->norm_eps)))
         return fail(LTX_ATTN_EINVAL, "norm_eps must be finite and >= 0");
+    if (a->q_sumsq || a->k_sumsq) {
+        if ((a->q_sumsq && !pl->q_norm) || (a->k_sumsq && !pl->k_norm))
+            return fail(LTX_ATTN_EINVAL, "a projection statistic without its norm weight");
+        if (a->sumsq_blocks < 1)
+            return fail(LTX_ATTN_EINVAL, "sumsq_blocks must be >= 1 (got %d)", a->sumsq_blocks);
+        if (((uintptr_t)a->q_sumsq & 3u) || ((uintptr_t)a->k_sumsq & 3u))
+            return fail(LTX_ATTN_EINVAL, "statistic partials must be 4-byte aligned");
+        if ((a->q_sumsq && a->q_sumsq_rs < a->sumsq_blocks) ||
+            (a->k_sumsq && a->k_sumsq_rs < a->sumsq_blocks))
+            return fail(LTX_ATTN_EINVAL, "statistic row stride below sumsq_blocks (%d)",
+                        a->sumsq_blocks);
+        pl->q_stat = a->q_sumsq != nullptr;
+        pl->k_stat = a->k_sumsq != nullptr;
+    }
 
     const bool qt = a->q_cos || a->q_sin, kt = a->k_cos || a->k_sin;
     if ((a->q_cos == nullptr) != (a->q_sin == nullptr) ||
@@ -297,7 +313,14 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     }
 
     // 1. prologue passes: statistic (and, for the K prologue, the prepared K)
-    if (pl.q_norm) {
+    if (pl.q_stat) {
+        ltx::RstdParams rp{};
+        rp.sumsq = a->q_sumsq; rp.rs = a->q_sumsq_rs;
+        rp.rows = B * a->Lq; rp.blocks = a->sumsq_blocks; rp.n = H * D; rp.eps = a->norm_eps;
+        rp.rstd = (float *)(ws + pl.off_qrstd);
+        if (int e = ltx::launch_rstd(rp, stream))
+            return fail(LTX_ATTN_EHIP, "q statistic launch: %s", hipGetErrorString((hipError_t)e));
+    } else if (pl.q_norm) {
         ltx::PrepParams pp{};
         pp.x = a->q; pp.bs = a->q_bs; pp.rs = a->q_rs; pp.hs = a->q_hs;
         pp.B = B; pp.L = a->Lq; pp.H = H;
@@ -308,11 +331,21 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     }
     const void *kptr = a->k;
     int64_t k_bs = a->k_bs, k_rs = a->k_rs, k_hs = a->k_hs;
-    if (pl.k_prologue || (pl.k_fused && pl.k_norm)) {
+    if (pl.k_fused && pl.k_stat) {
+        ltx::RstdParams rp{};
+        rp.sumsq = a->k_sumsq; rp.rs = a->k_sumsq_rs;
+        rp.rows = B * a->Lk; rp.blocks = a->sumsq_blocks; rp.n = H * D; rp.eps = a->norm_eps;
+        rp.rstd = (float *)(ws + pl.off_krstd);
+        if (int e = ltx::launch_rstd(rp, stream))
+            return fail(LTX_ATTN_EHIP, "k statistic launch: %s", hipGetErrorString((hipError_t)e));
+    } else if (pl.k_prologue || (pl.k_fused && pl.k_norm)) {
         ltx::PrepParams pp{};
         pp.x = a->k; pp.bs = a->k_bs; pp.rs = a->k_rs; pp.hs = a->k_hs;
         pp.B = B; pp.L = a->Lk; pp.H = H;
         pp.w = a->k_norm_w; pp.eps = a->norm_eps;
+        if (pl.k_stat) {
+            pp.sumsq = a->k_sumsq; pp.ss_rs = a->k_sumsq_rs; pp.ss_blocks = a->sumsq_blocks;
+        }
         if (pl.k_prologue) {
             pp.out = ws + pl.off_kprep;
             pp.cos = a->k_cos ? a->k_cos : a->q_cos;
@@ -434,5 +467,64 @@ const char *ltx_attn_provenance(void) {
 int32_t ltx_attn_abi_version(void) { return LTX_ATTN_ABI_VERSION; }
 
 size_t ltx_attn_args_size(void) { return sizeof(ltx_attn_args); }
+
+int32_t ltx_linear_sumsq_blocks(int32_t N) {
+    return N <= 0 ? 0 : (N + LTX_LINEAR_SUMSQ_COLS - 1) / LTX_LINEAR_SUMSQ_COLS;
+}
+
+ltx_attn_status ltx_linear(const ltx_linear_args *a, void *stream) {
+    g_err[0] = 0;
+    if (!a) return fail(LTX_ATTN_EINVAL, "args is NULL");
+    if (a->M < 0 || a->N < 8 || a->K < 64)
+        return fail(LTX_ATTN_EINVAL, "need M >= 0, N >= 8, K >= 64 (got %d, %d, %d)", a->M,
+                    a->N, a->K);
+    if (a->N % 8) return fail(LTX_ATTN_EINVAL, "N (%d) must be a multiple of 8", a->N);
+    if (a->K % 64) return fail(LTX_ATTN_EUNSUPPORTED, "K (%d) is not a multiple of 64", a->K);
+    if (!a->w || (a->M > 0 && (!a->x || !a->y)))
+        return fail(LTX_ATTN_EINVAL, "w, and x and y unless M is 0, must be given");
+    if (!aligned16(a->x) || !aligned16(a->w))
+        return fail(LTX_ATTN_EINVAL, "x and w must be 16-byte aligned");
+    if (((uintptr_t)a->y & 7u) || ((uintptr_t)a->bias & 7u))
+        return fail(LTX_ATTN_EINVAL, "y and bias must be 8-byte aligned");
+    if (a->x_rs < a->K || a->w_rs < a->K || (a->x_rs % 8) || (a->w_rs % 8))
+        return fail(LTX_ATTN_EINVAL, "x_rs and w_rs must be >= K and multiples of 8");
+    if (a->y_rs < a->N || (a->y_rs % 4))
+        return fail(LTX_ATTN_EINVAL, "y_rs must be >= N and a multiple of 4");
+    // The kernel addresses a 256-row tile of x or w with 32-bit byte offsets.
+    const int64_t max_rs = 0x7fffffff / (2 * (int64_t)ltx::kLinearTile);
+    if (a->x_rs > max_rs || a->w_rs > max_rs)
+        return fail(LTX_ATTN_EUNSUPPORTED, "row strides above %lld elements", (long long)max_rs);
+    const int32_t blocks = ltx_linear_sumsq_blocks(a->N);
+    if (a->sumsq && (((uintptr_t)a->sumsq & 3u) || a->sumsq_rs < blocks))
+        return fail(LTX_ATTN_EINVAL, "sumsq must be 4-byte aligned with a row stride >= %d",
+                    blocks);
+    const int64_t tiles_m = ((int64_t)a->M + ltx::kLinearTile - 1) / ltx::kLinearTile;
+    const int64_t tiles_n = ((int64_t)a->N + ltx::kLinearTile - 1) / ltx::kLinearTile;
+    if (tiles_m * tiles_n > 0x7fffffff) return fail(LTX_ATTN_EUNSUPPORTED, "grid too large");
+    if (a->M == 0) return LTX_ATTN_OK;
+    // y must not overlap its inputs: the tiles read x and w while others write y.
+    auto span = [](const void *p, int64_t rows, int64_t rs, int64_t cols, size_t elem) {
+        const uintptr_t b = (uintptr_t)p;
+        return std::pair<uintptr_t, uintptr_t>(b, b + ((rows - 1) * rs + cols) * elem);
+    };
+    const auto yb = span(a->y, a->M, a->y_rs, a->N, 2);
+    for (const auto &in : {span(a->x, a->M, a->x_rs, a->K, 2), span(a->w, a->N, a->w_rs, a->K, 2)})
+        if (yb.first < in.second && in.first < yb.second)
+            return fail(LTX_ATTN_EINVAL, "y overlaps x or w");
+    if (a->sumsq) {
+        const auto sb = span(a->sumsq, a->M, a->sumsq_rs, blocks, 4);
+        if (sb.first < yb.second && yb.first < sb.second)
+            return fail(LTX_ATTN_EINVAL, "sumsq overlaps y");
+    }
+    ltx::LinearParams p{};
+    p.x = a->x; p.w = a->w; p.bias = a->bias; p.y = a->y;
+    p.x_rs = a->x_rs; p.w_rs = a->w_rs; p.y_rs = a->y_rs;
+    p.sumsq = a->sumsq; p.ss_rs = a->sumsq_rs;
+    p.M = a->M; p.N = a->N; p.K = a->K;
+    p.tiles_m = (int32_t)tiles_m; p.tiles_n = (int32_t)tiles_n;
+    if (int e = ltx::launch_linear(p, stream))
+        return fail(LTX_ATTN_EHIP, "linear launch: %s", hipGetErrorString((hipError_t)e));
+    return LTX_ATTN_OK;
+}
 
 }  // extern "C"

@@ -59,7 +59,25 @@ class Args(ctypes.Structure):
         ("gate_logits", ctypes.c_void_p),
         ("g_bs", ctypes.c_int64), ("g_rs", ctypes.c_int64), ("g_hs", ctypes.c_int64),
         ("all_perturbed", ctypes.c_int32),
+        ("q_sumsq", ctypes.c_void_p), ("k_sumsq", ctypes.c_void_p),
+        ("q_sumsq_rs", ctypes.c_int64), ("k_sumsq_rs", ctypes.c_int64),
+        ("sumsq_blocks", ctypes.c_int32),
     ]
+
+
+class LinearArgs(ctypes.Structure):
+    """``ltx_linear_args`` (field order and types as in include/ltx_attn.h)."""
+
+    _fields_ = [
+        ("M", ctypes.c_int32), ("N", ctypes.c_int32), ("K", ctypes.c_int32),
+        ("x", ctypes.c_void_p), ("w", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("x_rs", ctypes.c_int64), ("w_rs", ctypes.c_int64), ("y_rs", ctypes.c_int64),
+        ("sumsq", ctypes.c_void_p), ("sumsq_rs", ctypes.c_int64),
+    ]
+
+
+SUMSQ_COLS = 256   # LTX_LINEAR_SUMSQ_COLS: columns of y per partial sum of squares
 
 
 EXPORTED_SYMBOLS = (
@@ -67,6 +85,7 @@ EXPORTED_SYMBOLS = (
     "ltx_attn_status_string", "ltx_attn_last_error", "ltx_attn_provenance",
     "ltx_attn_abi_version", "ltx_attn_args_size", "ltx_rope_frequency_grid", "ltx_rope_video_positions",
     "ltx_rope_audio_positions", "ltx_rope_tables", "ltx_rope_tables_device",
+    "ltx_linear", "ltx_linear_sumsq_blocks",
 )
 
 _lib = None
@@ -122,6 +141,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                            ctypes.c_double, ctypes.c_void_p, ctypes.c_void_p,
                                            ctypes.c_void_p]
     lib.ltx_rope_tables_device.restype = ctypes.c_int
+    lib.ltx_linear.argtypes = [ctypes.POINTER(LinearArgs), ctypes.c_void_p]
+    lib.ltx_linear.restype = ctypes.c_int
+    lib.ltx_linear_sumsq_blocks.argtypes = [ctypes.c_int32]
+    lib.ltx_linear_sumsq_blocks.restype = ctypes.c_int32
     _lib = lib
     return lib
 
@@ -217,7 +240,8 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
                   key_rotary: Optional[Rotary] = None,
                   k_valid_len: Optional[Sequence[int]] = None, scale: Optional[float] = None,
                   out=None, kprep: int = KPREP_AUTO, num_splits: int = 0, stream=None,
-                  workspace=None, events=None, gate_logits=None, all_perturbed: bool = False):
+                  workspace=None, events=None, gate_logits=None, all_perturbed: bool = False,
+                  q_sumsq=None, k_sumsq=None):
     """One call of ``ltx_attn_fwd``. Tensors are torch bf16 on the current HIP device.
 
     ``layout="merged"``: q ``[B, Lq, H*D]``, k/v ``[B, Lk, H*D]``, out ``[B, Lq, H*D]``.
@@ -226,6 +250,10 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
     of head h is multiplied by ``2*sigmoid(logit)`` (``DiTAttention.swift:395-399``).
     ``all_perturbed``: the STG passthrough (``:351-356``): ``out = v`` per head (times the
     gate), no attention; ``q`` and ``k`` may then be None.
+    ``q_sumsq`` / ``k_sumsq``: the projection's statistic partials for q / k (fp32
+    ``[B*L, blocks]`` views with a unit column stride, as ``linear(..., sumsq=True)`` returns
+    them, column-sliced to the q / k range of a fused projection); the norm then takes its
+    statistic from them. Both must have the same number of blocks.
     Returns ``out``.
     """
     import torch
@@ -294,6 +322,19 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
                                   f"{(B, Lq, heads)}")
         a.gate_logits = _ptr(gate_logits)
         a.g_bs, a.g_rs, a.g_hs = gate_logits.stride()
+    blocks = None
+    for name, t in (("q_sumsq", q_sumsq), ("k_sumsq", k_sumsq)):
+        if t is None:
+            continue
+        if t.dtype != torch.float32 or not t.is_cuda or t.dim() != 2 or t.stride(1) != 1:
+            raise Failure(EINVAL, f"{name} must be a 2-D fp32 device tensor, unit column stride")
+        if blocks is not None and t.shape[1] != blocks:
+            raise Failure(EINVAL, "q_sumsq and k_sumsq have different block counts")
+        blocks = t.shape[1]
+        setattr(a, name, _ptr(t))
+        setattr(a, name + "_rs", t.stride(0))
+    if blocks is not None:
+        a.sumsq_blocks = blocks
     need = lib.ltx_attn_workspace_bytes(ctypes.byref(a))
     st = lib.ltx_attn_validate(ctypes.byref(a))
     if st not in (OK, EWORKSPACE):
@@ -311,6 +352,61 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
     if need:
         out._ltx_workspace = workspace  # noqa: SLF001 -- lifetime anchor
     return out
+
+
+def linear_sumsq_blocks(n: int) -> int:
+    """Partial sums of squares per row of a projection with ``n`` output columns."""
+    return load_library().ltx_linear_sumsq_blocks(n)
+
+
+def linear(x, weight, bias=None, *, out=None, sumsq=False, stream=None):
+    """``linear(_:_:)`` of ``DiTAttention.swift:178-188`` through ``ltx_linear``:
+    ``y = x . weight^T (+ bias)``, bf16 in and out, fp32 accumulation.
+
+    ``x``: bf16 ``[..., K]`` with a unit last stride (leading axes are flattened to rows, so
+    they must be collapsible); ``weight``: bf16 ``[N, K]`` (the checkpoint's layout);
+    ``bias``: bf16 ``[N]`` or None. ``out``: optional bf16 ``[..., N]`` view to write (unit
+    last stride; e.g. a column slice of a fused buffer). ``sumsq=True`` also returns the
+    statistic partials: fp32 ``[rows, ceil(N/256)]``, partial j of a row being the sum of
+    squares of its bf16 outputs over columns ``[256 j, 256 j + 256)``.
+    Returns ``y`` or ``(y, partials)``.
+    """
+    import torch
+
+    lib = load_library()
+    for name, t in (("x", x), ("weight", weight), ("bias", bias), ("out", out)):
+        if t is not None and (t.dtype != torch.bfloat16 or not t.is_cuda):
+            raise Failure(EINVAL, f"{name} must be a bf16 device tensor")
+    N, K = weight.shape
+    if weight.stride(1) != 1 or x.stride(-1) != 1:
+        raise Failure(EINVAL, "x and weight need a unit last stride")
+    if x.shape[-1] != K:
+        raise Failure(EINVAL, f"x has {x.shape[-1]} columns, weight expects {K}")
+    lead = tuple(x.shape[:-1])
+    x2 = x.reshape(-1, K) if x.dim() != 2 else x
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty(lead + (N,), dtype=torch.bfloat16, device=x.device)
+    if tuple(out.shape) != lead + (N,) or out.stride(-1) != 1:
+        raise Failure(EINVAL, f"out must be {lead + (N,)} with a unit last stride")
+    y2 = out.view(-1, N) if out.dim() != 2 else out
+    if bias is not None and (bias.dim() != 1 or bias.shape[0] != N or not bias.is_contiguous()):
+        raise Failure(EINVAL, f"bias must be a contiguous [{N}] tensor")
+    a = LinearArgs()
+    a.M, a.N, a.K = M, N, K
+    a.x, a.w, a.bias, a.y = _ptr(x2), _ptr(weight), _ptr(bias), _ptr(y2)
+    a.x_rs = x2.stride(0) if M > 1 else K
+    a.w_rs = weight.stride(0) if N > 1 else K
+    a.y_rs = y2.stride(0) if M > 1 else N
+    parts = None
+    if sumsq:
+        nb = lib.ltx_linear_sumsq_blocks(N)
+        parts = torch.empty((M, nb), dtype=torch.float32, device=x.device)
+        a.sumsq, a.sumsq_rs = _ptr(parts), nb
+    if stream is None:
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+    _check(lib.ltx_linear(ctypes.byref(a), ctypes.c_void_p(stream)))
+    return (out, parts) if sumsq else out
 
 
 def workspace_bytes(**kw) -> int:

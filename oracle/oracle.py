@@ -21,6 +21,12 @@ This is a numpy restatement of the reference's arithmetic:
                         equals SDPA restricted to the valid keys, which is what ``sdpa``
                         computes. Zero valid keys is rejected (``TextConditioningLayout.swift:65``
                         throws ``emptyMask``).
+* ``linear``         -- ``DiTAttention.swift:178-188``: ``x . w^T`` in the weight's dtype
+                        (bf16 out of an fp32 accumulation), then ``+ bias`` as a bf16 add.
+* ``sumsq_partials`` -- the RMS statistic of a projection's bf16 output, summed per block of
+                        256 columns (what ``ltx_linear`` emits for ``rms_norm``).
+* ``attention_module`` -- ``DiTAttention.callAsFunction`` (``:315-405``): projections, the
+                        replaced unit, the gate from ``x`` and ``to_out``.
 * RoPE tables        -- ``Sources/LTXModules/DiTForward.swift:455-466`` (``frequencyGrid``),
                         ``:486-520`` (``videoPositions``), ``:606-619`` (``audioPositions``),
                         ``:641-678`` (``rotary``), ``:698-738`` (``rotaries``).
@@ -51,6 +57,7 @@ import numpy as np
 __all__ = [
     "f32_to_bf16_bits", "bf16_bits_to_f32", "round_bf16", "randn_bf16_bits",
     "splitmix_bf16_bits", "rms_norm", "split_rope", "sdpa", "head_gate", "attention",
+    "linear", "sumsq_partials", "attention_module",
     "frequency_grid", "video_positions", "audio_positions", "rotary_tables",
     "rotaries", "compare",
 ]
@@ -249,6 +256,82 @@ def attention(q_bits, k_bits, v_bits, heads: int, *, q_norm_w=None, k_norm_w=Non
             o = round_bf16(o)                         # the attention output is bf16 (:381)
         o = o * head_gate(gate_bits, mode)[..., None]
     return o.reshape(B, Lq, inner)
+
+
+# --------------------------------------------------------------------------------------
+# Projections and the whole module (DiTAttention.swift:178-188, :315-405)
+# --------------------------------------------------------------------------------------
+
+def linear(x_bits, w_bits, bias_bits=None, mode: str = "exact") -> np.ndarray:
+    """``linear(_:_:)`` (``DiTAttention.swift:178-188``): ``y = x . w^T (+ bias)``.
+
+    ``x_bits`` ``[..., K]``, ``w_bits`` ``[N, K]`` (the checkpoint's ``[out, in]``),
+    ``bias_bits`` ``[N]`` or None -- bf16 bit patterns. ``mode="exact"``: float64, nothing
+    rounded. ``mode="reference"``: the matmul's bf16 output (the exact sum rounded to fp32,
+    then to bf16: an fp32 accumulation up to its summation order), then the bias added as
+    two bf16 values in fp32 and rounded to bf16 (``:180``, ``:186``). LoRA deltas
+    (``:183-185``) are not part of this function.
+    """
+    x = bf16_bits_to_f32(x_bits).astype(np.float64)
+    w = bf16_bits_to_f32(w_bits).astype(np.float64)
+    y = x @ w.T
+    b = None if bias_bits is None else bf16_bits_to_f32(bias_bits)
+    if mode == "exact":
+        return y if b is None else y + b
+    y = round_bf16(y.astype(np.float32))
+    if b is not None:
+        y = round_bf16((y + b).astype(np.float32))
+    return y
+
+
+def sumsq_partials(y, cols: int = 256) -> np.ndarray:
+    """Sums of squares of ``y`` ``[..., N]`` over the column blocks ``[cols*j, cols*j + cols)``
+    (float64, ``[..., ceil(N/cols)]``); their row sum is the ``rms_norm`` statistic times N."""
+    y = np.asarray(y, dtype=np.float64)
+    N = y.shape[-1]
+    nb = -(-N // cols)
+    pad = np.zeros(y.shape[:-1] + (nb * cols - N,))
+    yp = np.concatenate([y, pad], axis=-1).reshape(y.shape[:-1] + (nb, cols))
+    return (yp * yp).sum(axis=-1)
+
+
+def attention_module(x_bits, weights: dict, heads: int, *, context_bits=None, q_cos=None,
+                     q_sin=None, k_cos=None, k_sin=None, valid_len=None,
+                     all_perturbed: bool = False, eps: float = 1e-6,
+                     mode: str = "reference") -> np.ndarray:
+    """``DiTAttention.callAsFunction`` (``DiTAttention.swift:315-405``) for one module.
+
+    ``weights`` maps the module's tensor names (``to_q.weight``, ``to_q.bias``, ``to_k.*``,
+    ``to_v.*``, ``q_norm.weight``, ``k_norm.weight``, optional ``to_gate_logits.*``,
+    ``to_out.0.*``; biases optional) to bf16 bit arrays. ``context_bits`` None means
+    self-attention (``:327``). Between operations the data is bf16 as in the reference: each
+    projection output, the attention output (``:381``) and the gated output (``:397-399``) are
+    rounded to bf16; ``mode`` is the arithmetic inside each operation. Returns float64
+    ``[B, Lq, out]`` (before ``to_out``'s final rounding in ``mode="exact"``, rounded in
+    ``"reference"``).
+    """
+    kv_bits = x_bits if context_bits is None else context_bits
+
+    def lin(t_bits, name):
+        return linear(t_bits, weights[name + ".weight"], weights.get(name + ".bias"), mode)
+
+    bits = lambda y: f32_to_bf16_bits(np.asarray(y, dtype=np.float32))   # noqa: E731
+    v = bits(lin(kv_bits, "to_v"))
+    B, Lq = x_bits.shape[0], x_bits.shape[1]
+    inner = v.shape[-1]
+    if all_perturbed:
+        o = bf16_bits_to_f32(v).astype(np.float64)                # :351-356
+    else:
+        q = bits(lin(x_bits, "to_q"))
+        k = bits(lin(kv_bits, "to_k"))
+        o = attention(q, k, v, heads, q_norm_w=weights["q_norm.weight"],
+                      k_norm_w=weights["k_norm.weight"], eps=eps, q_cos=q_cos, q_sin=q_sin,
+                      k_cos=k_cos, k_sin=k_sin, valid_len=valid_len, mode=mode)
+    o = round_bf16(o)                                               # bf16 attention output
+    if "to_gate_logits.weight" in weights:
+        g = head_gate(bits(lin(x_bits, "to_gate_logits")), "reference")
+        o = round_bf16(o.reshape(B, Lq, heads, inner // heads) * g[..., None]).reshape(o.shape)
+    return lin(bits(o), "to_out.0")
 
 
 # --------------------------------------------------------------------------------------

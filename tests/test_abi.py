@@ -22,7 +22,7 @@ GOLDEN = os.path.join(ROOT, "tests", "golden")
 def _declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ltx_(?:attn|rope)_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(ltx_(?:attn_|rope_|linear)\w*)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layout_and_version():
     lib = L.load_library()
     assert lib.ltx_attn_args_size() == ctypes.sizeof(L.Args)
-    assert lib.ltx_attn_abi_version() == 3
+    assert lib.ltx_attn_abi_version() == 4
     assert "gfx950" in L.provenance()
     for s in range(5):
         assert lib.ltx_attn_status_string(s)
@@ -231,6 +231,76 @@ def test_workspace_sizing_and_check():
     need = lib.ltx_attn_workspace_bytes(ctypes.byref(a))
     rows = 7 * 32 * 256
     assert need == (rows * 64 * 4 + 255) // 256 * 256 + (rows * 2 * 4 + 255) // 256 * 256
+
+
+def test_projection_statistic_rules():
+    """q_sumsq / k_sumsq (the projection's partial sums of squares) replace the statistic pass;
+    they need their norm weight, a block count and a row stride that holds the blocks."""
+    w = FAKE + (5 << 32)
+    a = _args(q_norm_w=w, k_norm_w=w, q_sumsq=FAKE + (6 << 32), q_sumsq_rs=16,
+              k_sumsq=FAKE + (7 << 32), k_sumsq_rs=48, sumsq_blocks=16)
+    st, msg = _validate(a)
+    assert st == L.OK, msg
+    for field, value in (("sumsq_blocks", 0), ("q_sumsq_rs", 15), ("k_sumsq", FAKE + 2),
+                         ("q_norm_w", None)):
+        b = _args(q_norm_w=w, k_norm_w=w, q_sumsq=FAKE + (6 << 32), q_sumsq_rs=16,
+                  k_sumsq=FAKE + (7 << 32), k_sumsq_rs=48, sumsq_blocks=16)
+        setattr(b, field, value)
+        st, msg = _validate(b)
+        assert st == L.EINVAL and msg, (field, msg)
+    # the statistic still lands in the workspace, so the workspace is unchanged
+    lib = L.load_library()
+    plain = _args(ws=False, q_norm_w=w, k_norm_w=w)
+    given = _args(ws=False, q_norm_w=w, k_norm_w=w, q_sumsq=FAKE, q_sumsq_rs=16,
+                  k_sumsq=FAKE, k_sumsq_rs=16, sumsq_blocks=16)
+    assert (lib.ltx_attn_workspace_bytes(ctypes.byref(given))
+            == lib.ltx_attn_workspace_bytes(ctypes.byref(plain)) > 0)
+
+
+def _linear_args(M=12480, N=4096, K=4096, **kw):
+    a = L.LinearArgs()
+    a.M, a.N, a.K = M, N, K
+    a.x, a.w, a.y = FAKE, FAKE + (1 << 32), FAKE + (2 << 32)
+    a.x_rs, a.w_rs, a.y_rs = K, K, N
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("field,value,status", [
+    ("N", 12, L.EINVAL),                # not a multiple of 8
+    ("N", 0, L.EINVAL),
+    ("K", 96, L.EUNSUPPORTED),          # not a multiple of 64
+    ("K", 32, L.EINVAL),
+    ("M", -1, L.EINVAL),
+    ("x", FAKE + 8, L.EINVAL),          # misaligned
+    ("w", None, L.EINVAL),
+    ("y", FAKE + (2 << 32) + 4, L.EINVAL),
+    ("bias", FAKE + 2, L.EINVAL),
+    ("x_rs", 4100, L.EINVAL),           # not a multiple of 8
+    ("w_rs", 2048, L.EINVAL),           # below K
+    ("y_rs", 4098, L.EINVAL),           # not a multiple of 4
+    ("x_rs", 1 << 23, L.EUNSUPPORTED),  # a 256-row tile past 32-bit offsets
+    ("sumsq", FAKE + (3 << 32) + 2, L.EINVAL),
+    ("y", FAKE + 1024, L.EINVAL),       # y overlaps x
+])
+def test_linear_rejects_bad_arguments(field, value, status):
+    """Every rejection happens on the host before a launch (this host has no GPU)."""
+    lib = L.load_library()
+    a = _linear_args(sumsq=FAKE + (3 << 32), sumsq_rs=16)
+    setattr(a, field, value)
+    assert lib.ltx_linear(ctypes.byref(a), None) == status
+    assert lib.ltx_attn_last_error().decode()
+
+
+def test_linear_statistic_layout():
+    lib = L.load_library()
+    assert [lib.ltx_linear_sumsq_blocks(n) for n in (8, 256, 264, 2048, 4096, 12288 + 32)] == \
+        [1, 1, 2, 8, 16, 49]
+    # a row stride below the block count is rejected; M = 0 launches nothing
+    a = _linear_args(sumsq=FAKE + (3 << 32), sumsq_rs=15)
+    assert lib.ltx_linear(ctypes.byref(a), None) == L.EINVAL
+    assert lib.ltx_linear(ctypes.byref(_linear_args(M=0)), None) == L.OK
 
 
 def test_zero_work_needs_no_gpu():

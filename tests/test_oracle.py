@@ -172,6 +172,121 @@ def test_head_gate_scales_each_heads_rows():
 
 
 # ---------------------------------------------------------------------------------------
+# Projections (linear) and the whole module
+# ---------------------------------------------------------------------------------------
+
+def test_linear_matches_python_brute_force():
+    """y[m][n] = sum_k x[m][k] w[n][k] + b[n]: w is [out, in] (a transposed operand or a
+    dropped bias fails this), summed exactly here with math.fsum."""
+    M, N, K = 3, 5, 7
+    x = O.randn_bf16_bits((M, K), 11)
+    w = O.randn_bf16_bits((N, K), 12)
+    b = O.randn_bf16_bits((N,), 13)
+    xf, wf, bf = (O.bf16_bits_to_f32(t).astype(float) for t in (x, w, b))
+    want = np.array([[math.fsum([xf[m, k] * wf[n, k] for k in range(K)] + [bf[n]])
+                      for n in range(N)] for m in range(M)])
+    np.testing.assert_allclose(O.linear(x, w, b), want, rtol=1e-13, atol=1e-13)
+    # leading axes are rows
+    np.testing.assert_allclose(O.linear(x.reshape(1, M, K), w, b)[0], want, rtol=1e-13,
+                               atol=1e-13)
+
+
+def test_linear_reference_mode_rounds_matmul_then_bias():
+    """The matmul's output is bf16 before the bias is added (DiTAttention.swift:180, :186):
+    1 + 2^-9 rounds to 1, and 1 + 2^-8 is a tie that rounds to even (1), whereas one rounding
+    of 1 + 2^-9 + 2^-8 gives 1 + 2^-7. An identity weight passes x through unchanged."""
+    x = _bits([[1.0, 2.0 ** -9]])
+    w = _bits([[1.0, 1.0]])
+    b = _bits([2.0 ** -8])
+    assert O.linear(x, w, b, "reference")[0, 0] == 1.0
+    assert O.round_bf16(np.float32(1.0 + 2.0 ** -9 + 2.0 ** -8)) == 1.0 + 2.0 ** -7
+    assert O.linear(x, w, b, "exact")[0, 0] == 1.0 + 2.0 ** -9 + 2.0 ** -8
+    xi = O.randn_bf16_bits((4, 64), 3)
+    eye = _bits(np.eye(64))
+    np.testing.assert_array_equal(O.linear(xi, eye, None, "reference"), O.bf16_bits_to_f32(xi))
+
+
+def test_sumsq_partials_blocks():
+    """Partials cover [256 j, 256 j + 256); the last block is ragged, and the partials add up
+    to the row's sum of squares (the rms_norm statistic times N)."""
+    y = np.ones((2, 600))
+    np.testing.assert_array_equal(O.sumsq_partials(y), [[256, 256, 88]] * 2)
+    r = np.random.default_rng(5).standard_normal((3, 4096))
+    p = O.sumsq_partials(r)
+    assert p.shape == (3, 16)
+    np.testing.assert_allclose(p.sum(-1), (r * r).sum(-1), rtol=1e-12)
+    np.testing.assert_allclose(p[:, 3], (r[:, 768:1024] ** 2).sum(-1), rtol=1e-12)
+    # the statistic the norm derives from them
+    np.testing.assert_allclose(O.rms_norm(r, np.ones(4096), 0.0, "exact"),
+                               r / np.sqrt(p.sum(-1, keepdims=True) / 4096), rtol=1e-12)
+
+
+def _module_weights(inner, K, heads, seed, gate=True, identity=False):
+    rng = np.random.default_rng(seed)
+    def w(n, k, scale):
+        return O.f32_to_bf16_bits((rng.standard_normal((n, k)) * scale).astype(np.float32))
+    ws = {}
+    for name in ("to_q", "to_k", "to_v"):
+        ws[name + ".weight"] = _bits(np.eye(inner, K)) if identity else w(inner, K, K ** -0.5)
+        if not identity:
+            ws[name + ".bias"] = w(1, inner, 0.1)[0]
+    ws["q_norm.weight"] = w(1, inner, 0.2)[0] + 0 if not identity else _bits(np.ones(inner))
+    ws["k_norm.weight"] = w(1, inner, 0.2)[0] if not identity else _bits(np.ones(inner))
+    ws["to_out.0.weight"] = _bits(np.eye(K, inner)) if identity else w(K, inner, inner ** -0.5)
+    if gate:
+        ws["to_gate_logits.weight"] = w(heads, K, K ** -0.5)
+        ws["to_gate_logits.bias"] = w(1, heads, 0.5)[0]
+    return ws
+
+
+def test_attention_module_reduces_to_the_core():
+    """With identity projections and unit norm weights the module is the replaced unit on x
+    itself; fully perturbed it returns v = x (DiTAttention.swift:351-356); a gate whose
+    logits are 0 passes through and one of -30 silences its head (the logits are read off x,
+    :387-391: they change with x, not with the attention output)."""
+    B, L, H, D = 1, 5, 2, 8
+    inner = H * D
+    x = O.randn_bf16_bits((B, L, inner), 21)
+    ws = _module_weights(inner, inner, H, 1, gate=False, identity=True)
+    core = O.round_bf16(O.attention(x, x, x, H, q_norm_w=ws["q_norm.weight"],
+                                    k_norm_w=ws["k_norm.weight"], mode="reference"))
+    np.testing.assert_array_equal(O.attention_module(x, ws, H), core)
+    np.testing.assert_array_equal(O.attention_module(x, ws, H, all_perturbed=True),
+                                  O.bf16_bits_to_f32(x))
+    gw = dict(ws)
+    gw["to_gate_logits.weight"] = _bits(np.zeros((H, inner)))
+    np.testing.assert_array_equal(O.attention_module(x, gw, H), core)
+    gw["to_gate_logits.bias"] = _bits([-30.0, 0.0])
+    got = O.attention_module(x, gw, H).reshape(B, L, H, D)
+    assert np.all(np.abs(got[..., 0, :]) < 1e-11)          # 2*sigmoid(-30) ~ 1.9e-13
+    np.testing.assert_array_equal(got[..., 1, :], core.reshape(B, L, H, D)[..., 1, :])
+
+
+def test_attention_module_context_feeds_k_and_v_only():
+    """Cross-attention: q from x, k and v from the context (:327, :341, :358-359). Swapping
+    which stream feeds q changes the result; the output width is to_out's."""
+    B, Lq, Lk, H, D, K = 1, 4, 6, 2, 8, 32
+    inner = H * D
+    x = O.randn_bf16_bits((B, Lq, K), 31)
+    c = O.randn_bf16_bits((B, Lk, K), 32)
+    ws = _module_weights(inner, K, H, 2)
+    out = O.attention_module(x, ws, H, context_bits=c)
+    assert out.shape == (B, Lq, K)
+    q = O.f32_to_bf16_bits(O.linear(x, ws["to_q.weight"], ws["to_q.bias"], "reference"))
+    k = O.f32_to_bf16_bits(O.linear(c, ws["to_k.weight"], ws["to_k.bias"], "reference"))
+    v = O.f32_to_bf16_bits(O.linear(c, ws["to_v.weight"], ws["to_v.bias"], "reference"))
+    o = O.round_bf16(O.attention(q, k, v, H, q_norm_w=ws["q_norm.weight"],
+                                 k_norm_w=ws["k_norm.weight"], mode="reference"))
+    g = O.head_gate(O.f32_to_bf16_bits(O.linear(x, ws["to_gate_logits.weight"],
+                                                ws["to_gate_logits.bias"], "reference")),
+                    "reference")
+    o = O.round_bf16(o.reshape(B, Lq, H, D) * g[..., None]).reshape(B, Lq, inner)
+    want = O.linear(O.f32_to_bf16_bits(o), ws["to_out.0.weight"], ws["to_out.0.bias"]
+                    if "to_out.0.bias" in ws else None, "reference")
+    np.testing.assert_array_equal(out, want)
+
+
+# ---------------------------------------------------------------------------------------
 # RMSNorm over the inner dim
 # ---------------------------------------------------------------------------------------
 
