@@ -12,14 +12,24 @@
 // the lane).
 //
 // Staging: every k step's 256 x BK tiles of x and w are copied HBM -> LDS by the
-// buffer-load-to-LDS path into one of NSTAGE buffers, NSTAGE - 1 steps ahead, rows of BK
-// elements with their 16-byte units XOR-swizzled so the operand reads (32 rows, one unit per
-// half-wave) are free of bank conflicts. The copies are untracked assembly; each step waits for
-// its own copies (vmcnt) and a barrier makes everyone's visible and frees the buffer the step
-// refills. Rows past M (N) read as zeros through the buffer resource's bound.
+// buffer-load-to-LDS path into one of two buffers, rows of BK elements with their 16-byte units
+// XOR-swizzled so the operand reads (32 rows, one unit per half-wave) are free of bank
+// conflicts. Rows past M (N) read as zeros through the buffer resource's bound. The step loop is
+// arranged around its one barrier, which sits in the last reduction chunk of each step, after
+// that chunk's operands have been read into registers and before its products:
+//   * the barrier certifies that every wave's copies for the next step have landed (each wave
+//     waits for its own first: the copies are untracked assembly, counted by vmcnt) and that
+//     every wave has finished reading the current step's buffer;
+//   * right after it, the wave reads the next step's first operands and issues the copies for
+//     the step after next into the buffer just freed, one after each of the chunk's products,
+//     so the matrix cores have the chunk's products to run while the reads return, and the
+//     copies have a whole step to land.
+// Within a step, the operands of chunk c + 1 are read while the products of chunk c run.
 //
 // Rounding follows the reference's two operations: the fp32 accumulator is rounded to bf16
 // (the matmul's output), then the bias is added in fp32 and the sum rounded to bf16 again.
+#include <type_traits>
+
 #include "lds_copy.hpp"
 
 namespace ltx {
@@ -27,15 +37,14 @@ namespace {
 
 constexpr int LT = kLinearTile;       // 256 rows and columns of y per workgroup
 
-template <int BK, int NSTAGE>
+template <int BK>
 struct LinTile {
     static constexpr int U = BK / 8;              // 16-byte units per LDS row
     static constexpr int ELEMS = LT * BK;         // one operand's tile of one k step
     static constexpr int CPT = LT * U / 64 / 4;   // copies per wave per operand tile
     static constexpr int NCH = BK / 16;           // MFMA reduction chunks per k step
-    static_assert(BK == 64 || BK == 32, "k step");
-    static_assert(NSTAGE >= 2 && 2 * NSTAGE * ELEMS * 2 <= 160 * 1024, "LDS budget");
-    static_assert((NSTAGE - 2) * 2 * CPT < 64, "vmcnt range");
+    static_assert(BK == 64, "k step: the copy schedule places 2*CPT = 16 copies in 16 products");
+    static_assert(2 * 2 * ELEMS * 2 <= 160 * 1024, "LDS budget");
 };
 
 // Unit swizzle: the 16 lanes a 16-byte LDS read serves together read 16 consecutive rows at
@@ -46,13 +55,13 @@ __device__ __forceinline__ int lswz(int row, int u) {
     return U == 8 ? (u ^ ((row >> 1) & 7)) : (u ^ ((row >> 2) & 3));
 }
 
-template <int BK, int NSTAGE>
+template <int BK>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void linear_kernel(const LinearParams p) {
-    using T = LinTile<BK, NSTAGE>;
+    using T = LinTile<BK>;
     constexpr int U = T::U, CPT = T::CPT, NCH = T::NCH, ELEMS = T::ELEMS;
-    __shared__ __attribute__((aligned(16))) bf16 sW[NSTAGE * ELEMS];
-    __shared__ __attribute__((aligned(16))) bf16 sX[NSTAGE * ELEMS];
+    __shared__ __attribute__((aligned(16))) bf16 sW[2 * ELEMS];
+    __shared__ __attribute__((aligned(16))) bf16 sX[2 * ELEMS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -61,15 +70,15 @@ void linear_kernel(const LinearParams p) {
     const int r = lane & 31, g = lane >> 5;
 
     // Tile of this workgroup. Workgroups go to the 8 XCDs round-robin; each XCD gets a
-    // contiguous range of the tile order, which walks groups of 4 row tiles column tile by
-    // column tile, so the ~32 workgroups an XCD runs at once share 4 row tiles of x and 8
+    // contiguous range of the tile order, which walks groups of 8 row tiles column tile by
+    // column tile, so the ~32 workgroups an XCD runs at once share 8 row tiles of x and 4
     // column tiles of w in its L2.
     const int total = p.tiles_m * p.tiles_n;
     const int wg = blockIdx.x;
     const int xcd = wg & 7, slot = wg >> 3;
     const int q8 = total >> 3, r8 = total & 7;
     const int t = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + slot;
-    constexpr int GRP = 4;
+    constexpr int GRP = 8;
     const int group = t / (GRP * p.tiles_n);
     const int first_m = group * GRP;
     const int rows_g = min(GRP, p.tiles_m - first_m);
@@ -94,14 +103,18 @@ void linear_kernel(const LinearParams p) {
         xl[j] = row * xrow + 16 * u;
         wl[j] = row * wrow + 16 * u;
     }
-    auto copy_step = [&](int s, int st) __attribute__((always_inline)) {
+    // Copy j (0 .. 2*CPT-1) of this wave's share of k step s into buffer st: even j of w, odd
+    // of x.
+    auto copy_one = [&](int s, int st, int j) __attribute__((always_inline)) {
         const int kb = s * BK * 2;
-        const u32x4 rx = rsrc_words(X0 + kb, xbytes);
-        const u32x4 rw = rsrc_words(W0 + kb, wbytes);
-#pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            copy_all(rw, (uint32_t)(uintptr_t)((lds_bf16 *)sW + st * ELEMS + (wave * CPT + j) * 512), wl[j]);
-            copy_all(rx, (uint32_t)(uintptr_t)((lds_bf16 *)sX + st * ELEMS + (wave * CPT + j) * 512), xl[j]);
+        if ((j & 1) == 0) {
+            copy_all(rsrc_words(W0 + kb, wbytes),
+                     (uint32_t)(uintptr_t)((lds_bf16 *)sW + st * ELEMS + (wave * CPT + j / 2) * 512),
+                     wl[j / 2]);
+        } else {
+            copy_all(rsrc_words(X0 + kb, xbytes),
+                     (uint32_t)(uintptr_t)((lds_bf16 *)sX + st * ELEMS + (wave * CPT + j / 2) * 512),
+                     xl[j / 2]);
         }
     };
     // Operand of rows row0 + 0..31, reduction chunk c: lane (r, g) reads row row0 + r, unit 2c + g.
@@ -117,31 +130,65 @@ void linear_kernel(const LinearParams p) {
         for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = splat16(0.f);
 
     const int nsteps = p.K / BK;
-#pragma unroll
-    for (int s = 0; s < NSTAGE - 1; ++s)
-        if (s < nsteps) copy_step(s, s);
-    for (int s = 0; s < nsteps; ++s) {
-        if (s + NSTAGE - 2 < nsteps) wait_copies_but<(NSTAGE - 2) * 2 * CPT>();
-        else wait_copies();
-        __syncthreads();       // everyone's copies for step s landed; step s-1's reads done
-        const int st = s % NSTAGE;
-        if (s + NSTAGE - 1 < nsteps) copy_step(s + NSTAGE - 1, (s + NSTAGE - 1) % NSTAGE);
+    bf16x8 a[2][4], b[2][4];       // operands of the current and the next chunk
+    auto read_chunk = [&](int st, int c, int buf) __attribute__((always_inline)) {
         const lds_bf16 *Ws = (const lds_bf16 *)sW + st * ELEMS;
         const lds_bf16 *Xs = (const lds_bf16 *)sX + st * ELEMS;
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            bf16x8 a[4], b[4];
+        for (int i = 0; i < 4; ++i) {
+            a[buf][i] = frag(Ws, wn * 128 + 32 * i, c);
+            b[buf][i] = frag(Xs, wm * 128 + 32 * i, c);
+        }
+    };
+    // Prologue: steps 0 and 1 into both buffers, then step 0's first operands.
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                a[i] = frag(Ws, wn * 128 + 32 * i, c);
-                b[i] = frag(Xs, wm * 128 + 32 * i, c);
+    for (int j = 0; j < 2 * CPT; ++j) copy_one(0, 0, j);
+    if (nsteps > 1) {
+#pragma unroll
+        for (int j = 0; j < 2 * CPT; ++j) copy_one(1, 1, j);
+        wait_copies_but<2 * CPT>();
+    } else {
+        wait_copies();
+    }
+    __syncthreads();
+    read_chunk(0, 0, 0);
+
+    // One k step; COPY: issue the copies of step s + 2, NEXT: read step s + 1's first operands.
+    auto step = [&](int s, auto copy, auto next) __attribute__((always_inline)) {
+        const int st = s & 1;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int cb = c & 1;          // NCH is even: chunk 0 of every step is in buffer 0
+            if (c < NCH - 1) {
+                read_chunk(st, c + 1, cb ^ 1);
+            } else {
+                // Step s+1's copies (issued one step ago) have landed for this wave; after the
+                // barrier they have for every wave, and every wave's reads of buffer st are done.
+                // The scheduling fences keep the earlier chunks' products ahead of the wait.
+                __builtin_amdgcn_sched_barrier(0);
+                wait_copies();
+                __syncthreads();
+                __builtin_amdgcn_sched_barrier(0);
+                if (decltype(next)::value) read_chunk(st ^ 1, 0, 0);
             }
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-                for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = mfma32(a[nb], b[mb], acc[nb][mb]);
+                for (int mb = 0; mb < 4; ++mb) {
+                    acc[nb][mb] = mfma32(a[cb][nb], b[cb][mb], acc[nb][mb]);
+                    if (decltype(copy)::value && c == NCH - 1) {
+                        copy_one(s + 2, st, 4 * nb + mb);      // one copy per product
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
         }
-    }
+    };
+    using yes = std::true_type;
+    using no = std::false_type;
+    int s = 0;
+    for (; s + 2 < nsteps; ++s) step(s, yes{}, yes{});
+    if (s + 1 < nsteps) step(s++, no{}, yes{});
+    step(s, no{}, no{});
 
     // ---- epilogue ---------------------------------------------------------------------
     // Lane (r, g) of product (nb, mb) holds y[m][n + e] for m = m0 + wm*128 + 32*mb + r,
@@ -201,7 +248,7 @@ void linear_kernel(const LinearParams p) {
 
 int launch_linear(const LinearParams &p, void *stream) {
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(256);
-    hipLaunchKernelGGL((linear_kernel<64, 2>), grid, block, 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL((linear_kernel<64>), grid, block, 0, (hipStream_t)stream, p);
     return (int)hipGetLastError();
 }
 
