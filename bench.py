@@ -13,7 +13,8 @@ Prints ONE JSON line. ``roofline`` is for the dominant kernel (the attention ker
 timed with HIP events recorded by the library around that kernel on the call's stream.
 ``cpu_baseline`` times the C restatement of the reference's explicit fp32 path on a bounded
 sample of the same workload, on this host's cores. ``secondary`` holds the other two figures
-the metric names: 3120-token self-attention TFLOP/s and ms per DiT-block attention set.
+the metric names (3120-token self-attention TFLOP/s and ms per DiT-block attention set) and
+the projection GEMM / whole-module figures at the 12480-token shapes.
 """
 
 import argparse
@@ -286,6 +287,84 @@ def bench_rope_tables(device):
     return {"device_ms": gpu_ms, "host_build_and_upload_ms": host_ms}
 
 
+def _time_ms(fn, n, warm):
+    import torch
+
+    for _ in range(warm):
+        fn()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(n):
+        fn()
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) / n
+
+
+def bench_projection(device, x):
+    """The projection GEMM with the RMS statistic from its epilogue (``ltx_linear``) at the
+    12480-token video self-attention's shapes: to_q (12480 x 4096 x 4096) and to_q/to_k/to_v
+    fused into one N = 12288 projection, with hipBLASLt (torch's linear, no statistic) timed
+    beside it on the same shapes as a point of comparison; the attention call taking its
+    statistic from the partials instead of its own pass over q; and the whole module
+    (DiTAttention.callAsFunction: projections, attention with the gate, to_out) through
+    ``DiTAttentionModule``."""
+    import torch
+    import torch.nn.functional as F
+
+    import ltx_attn as L
+
+    T, C = 12480, 4096
+    xin = _randn((1, T, C), 0x5EED + 40, device)
+    w = {n: _randn((C, C), 0x5EED + 41 + i, device, 0.0, C ** -0.5)
+         for i, n in enumerate(("to_q", "to_k", "to_v", "to_out.0"))}
+    wf = torch.cat([w["to_q"], w["to_k"], w["to_v"]], 0).contiguous()
+    y1 = torch.empty((1, T, C), dtype=torch.bfloat16, device=device)
+    y3 = torch.empty((1, T, 3 * C), dtype=torch.bfloat16, device=device)
+    ms_q = _time_ms(lambda: L.linear(xin, w["to_q"], out=y1, sumsq=True), 20, 5)
+    ms_qkv = _time_ms(lambda: L.linear(xin, wf, out=y3, sumsq=True), 10, 3)
+    ms_q_blas = _time_ms(lambda: F.linear(xin, w["to_q"]), 20, 5)
+    ms_qkv_blas = _time_ms(lambda: F.linear(xin, wf), 10, 3)
+    fl_q, fl_qkv = 2.0 * T * C * C, 2.0 * T * 3 * C * C
+
+    # attention with the projection's statistic vs its own statistic pass
+    out = torch.empty_like(x["q"])
+    ws = torch.empty(512 << 20, dtype=torch.uint8, device=device)
+    _, qs = L.linear(xin, w["to_q"], sumsq=True)
+    _, ks = L.linear(xin, w["to_k"], sumsq=True)
+    kw = dict(heads=x["H"], q_norm_w=x["wq"], k_norm_w=x["wk"], rotary=x["rot"], out=out,
+              workspace=ws)
+    ms_attn_own = _time_ms(lambda: L.attention_fwd(x["q"], x["k"], x["v"], **kw), 10, 3)
+    ms_attn_given = _time_ms(lambda: L.attention_fwd(x["q"], x["k"], x["v"], q_sumsq=qs,
+                                                     k_sumsq=ks, **kw), 10, 3)
+
+    # the whole module
+    weights = {n + ".weight": t for n, t in w.items()}
+    for i, n in enumerate(("to_q", "to_k", "to_v", "to_out.0")):
+        weights[n + ".bias"] = _randn((C,), 0x5EED + 50 + i, device, 0.0, 0.1)
+    weights["to_gate_logits.weight"] = _randn((32, C), 0x5EED + 55, device, 0.0, C ** -0.5)
+    weights["q_norm.weight"], weights["k_norm.weight"] = x["wq"], x["wk"]
+    mod = L.DiTAttentionModule(weights)
+    ms_mod = _time_ms(lambda: mod(xin, variant=L.Variant.videoSelf, rotary=x["rot"],
+                                  workspace=ws), 5, 2)
+    fl_mod = 5 * fl_q + 2.0 * T * C * 32 + 4.0 * T * T * C
+    return {
+        "linear_12480x4096x4096_ms": round(ms_q, 4),
+        "linear_12480x4096x4096_tflops": round(fl_q / ms_q / 1e9, 1),
+        "linear_12480x4096x4096_pct_peak": round(100 * fl_q / ms_q / 1e9 / PEAK_BF16_TFLOPS, 2),
+        "linear_fused_qkv_12480x12288x4096_ms": round(ms_qkv, 4),
+        "linear_fused_qkv_tflops": round(fl_qkv / ms_qkv / 1e9, 1),
+        "linear_fused_qkv_pct_peak": round(100 * fl_qkv / ms_qkv / 1e9 / PEAK_BF16_TFLOPS, 2),
+        "hipblaslt_12480x4096x4096_ms": round(ms_q_blas, 4),
+        "hipblaslt_fused_qkv_ms": round(ms_qkv_blas, 4),
+        "attn_12480_own_statistic_ms": round(ms_attn_own, 4),
+        "attn_12480_projection_statistic_ms": round(ms_attn_given, 4),
+        "video_self_module_12480_ms": round(ms_mod, 4),
+        "video_self_module_12480_tflops": round(fl_mod / ms_mod / 1e9, 1),
+    }
+
+
 def cpu_baseline(x, budget_s):
     """The C restatement of the reference's explicit path (fp32 logits, softmax, P.V, with
     its bf16 rounding points), multithreaded, on a bounded sample of the c4 workload:
@@ -387,6 +466,11 @@ def main():
         print(f"# rope tables (12480 video tokens): {rope['device_ms']:.3f} ms on the GPU, "
               f"{rope['host_build_and_upload_ms']:.1f} ms host build + upload", file=sys.stderr,
               flush=True)
+        proj = bench_projection(device, x)
+        print(f"# projection 12480x4096x4096: {proj['linear_12480x4096x4096_ms']:.3f} ms "
+              f"({proj['linear_12480x4096x4096_tflops']} TFLOP/s; hipBLASLt "
+              f"{proj['hipblaslt_12480x4096x4096_ms']:.3f} ms); video self-attention module "
+              f"{proj['video_self_module_12480_ms']:.3f} ms", file=sys.stderr, flush=True)
         secondary = {
             "video_self_3120_tflops": round(c1["kernel_tflops"], 2),
             "video_self_3120_pct_peak": round(c1["pct_peak"], 2),
@@ -398,6 +482,7 @@ def main():
                                                    round(c4["kernel_ms_max"], 4)],
             "rope_tables_12480_device_ms": round(rope["device_ms"], 4),
             "rope_tables_12480_host_build_upload_ms": round(rope["host_build_and_upload_ms"], 2),
+            "projection": proj,
         }
 
     traffic = None

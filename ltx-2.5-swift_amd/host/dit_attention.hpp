@@ -79,13 +79,17 @@ public:
     // (bf16 [B, Lq, H] contiguous: to_gate_logits(x)) each head's rows are multiplied by
     // 2*sigmoid(logit), as the module's gate does (:395-399). `allPerturbed` is the STG
     // passthrough (:351-356): out = V per head (times the gate); q and k are not read (their
-    // `data` may be null, `tokens` still gives Lq). Throws Failure.
+    // `data` may be null, `tokens` still gives Lq). `q_sumsq` / `k_sumsq`: the statistic
+    // partials ltx_linear wrote for q / k ([B*L][sumsq_blocks]), which replace the norm's own
+    // statistic pass. Throws Failure.
     void operator()(int32_t batch, int32_t inner, const Stream &q, const Stream &k,
                     const Stream &v, void *out, int64_t out_batch_stride,
                     int64_t out_row_stride, Variant variant, const Rotary *rotary,
                     const Rotary *keyRotary, void *workspace, size_t workspace_bytes,
                     void *stream, const int32_t *k_valid_len = nullptr,
-                    const void *gate_logits = nullptr, bool allPerturbed = false) const {
+                    const void *gate_logits = nullptr, bool allPerturbed = false,
+                    const float *q_sumsq = nullptr, const float *k_sumsq = nullptr,
+                    int32_t sumsq_blocks = 0) const {
         if (rotary && !takesRotary(variant))
             throw Failure(LTX_ATTN_EINVAL,
                           std::string(rawValue(variant)) +
@@ -107,6 +111,12 @@ public:
             a.g_bs = (int64_t)q.tokens * heads;
             a.g_rs = heads;
             a.g_hs = 1;
+        }
+        if (q_sumsq || k_sumsq) {
+            // the projections' statistic partials (ltx_linear), [B*L][sumsq_blocks] each
+            a.q_sumsq = q_sumsq;
+            a.k_sumsq = k_sumsq;
+            a.q_sumsq_rs = a.k_sumsq_rs = a.sumsq_blocks = sumsq_blocks;
         }
         check(ltx_attn_fwd(&a, stream));
     }

@@ -3,6 +3,9 @@
 A thin ctypes layer over the C ABI in ``include/ltx_attn.h``. It mirrors the reference's call
 surface for the replaced unit:
 
+* ``DiTAttentionModule`` -- the whole ``DiTAttention.callAsFunction`` (``:315-405``):
+  projections (``linear``, with the RMS statistic from the q / k projections), the replaced
+  unit, the gate and ``to_out``.
 * ``DiTAttentionCore``  -- the norm -> split -> RoPE -> SDPA part of
   ``DiTAttention.callAsFunction`` (``Sources/LTXModules/DiTAttention.swift:315-381``), with the
   reference's ``Variant`` / ``Rotary`` / ``Failure`` vocabulary (``:69-122``).
@@ -461,6 +464,53 @@ class DiTAttentionCore:
                              k_norm_w=self.k_norm_weight, eps=self.norm_epsilon,
                              rotary=rotary, key_rotary=key_rotary, k_valid_len=k_valid_len,
                              **kw)
+
+
+class DiTAttentionModule:
+    """The whole attention module, ``DiTAttention.callAsFunction``
+    (``Sources/LTXModules/DiTAttention.swift:315-405``): ``to_v`` / ``to_q`` / ``to_k`` through
+    ``linear`` (q and k emitting the RMS statistic partials), the replaced unit taking its
+    statistic from them, the gate from ``to_gate_logits(x)`` and ``to_out.0``. The Python
+    mirror of ``ltx-2.5-swift_amd/host/dit_module.hpp``.
+
+    ``weights`` maps the module's tensor names (``to_q.weight``, ``to_q.bias``, ``to_k.*``,
+    ``to_v.*``, ``q_norm.weight``, ``k_norm.weight``, ``to_out.0.*``, optional
+    ``to_gate_logits.*``; biases optional) to bf16 device tensors.
+    """
+
+    heads = 32
+    norm_epsilon = 1e-6
+
+    def __init__(self, weights, heads: int = 32):
+        self.w = weights
+        self.heads = heads
+        q = weights["to_q.weight"]
+        if q.shape[0] % heads:
+            raise Failure(EINVAL, f"to_q.weight {tuple(q.shape)} is not [k * {heads}, queryDim]")
+        self.core = DiTAttentionCore(weights["q_norm.weight"], weights["k_norm.weight"], heads)
+
+    def _lin(self, t, name, sumsq=False):
+        return linear(t, self.w[name + ".weight"], self.w.get(name + ".bias"), sumsq=sumsq)
+
+    def __call__(self, x, context=None, *, variant: Variant, rotary: Optional[Rotary] = None,
+                 key_rotary: Optional[Rotary] = None, k_valid_len=None,
+                 all_perturbed: bool = False, workspace=None):
+        kv = x if context is None else context                       # :327
+        B, Lq, Lk = x.shape[0], x.shape[1], kv.shape[1]
+        v = self._lin(kv, "to_v")                                     # :341
+        gate = None
+        if "to_gate_logits.weight" in self.w:                          # :387-391
+            gate = self._lin(x, "to_gate_logits")
+        if all_perturbed:                                              # :351-356
+            o = self.core(None, None, v, variant=variant, gate_logits=gate, all_perturbed=True,
+                          workspace=workspace)
+        else:
+            q, qs = self._lin(x, "to_q", sumsq=True)                   # :358-359
+            k, ks = self._lin(kv, "to_k", sumsq=True)
+            o = self.core(q, k, v, variant=variant, rotary=rotary, key_rotary=key_rotary,
+                          k_valid_len=k_valid_len, gate_logits=gate, workspace=workspace,
+                          q_sumsq=qs.view(B * Lq, -1), k_sumsq=ks.view(B * Lk, -1))
+        return self._lin(o, "to_out.0")                               # :402-404
 
 
 class DiTBlockAttention:

@@ -397,6 +397,20 @@ def test_cpp_block_driver_host_behaviour(tmp_path):
     assert "0 failure(s)" in run.stdout
 
 
+def test_cpp_module_driver_host_behaviour(tmp_path):
+    """The C++ module driver (ltx-2.5-swift_amd/host/dit_module.hpp): weight shapes checked at
+    construction, the workspace layout, and failures thrown before any launch."""
+    src = os.path.join(ROOT, "tests", "cpp", "test_dit_module.cpp")
+    exe = str(tmp_path / "test_dit_module")
+    libdir = os.path.dirname(L.LIB_PATH)
+    subprocess.run(["g++", "-std=c++17", "-O1", src, "-o", exe, f"-L{libdir}", "-lltx_attn",
+                    f"-Wl,-rpath,{libdir}", "-L/opt/rocm/lib", "-Wl,-rpath-link,/opt/rocm/lib"],
+                   check=True, capture_output=True)
+    run = subprocess.run([exe], capture_output=True, text=True)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert "0 failure(s)" in run.stdout
+
+
 def test_cpp_host_mirror_error_behaviour(tmp_path):
     """The C++ DiTAttention mirror (ltx-2.5-swift_amd/host/dit_attention.hpp) throws the
     reference's structural failures before anything reaches a device."""
