@@ -419,6 +419,9 @@ def main():
                     help="seconds of CPU work for the cpu_baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--projection-only", action="store_true",
+                    help="only run the 12480 x 4096 x 4096 projection (ltx_linear with its "
+                         "statistic), --steps times (for counter passes)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB, --steps times "
                          "(the known-size kernel that scales FETCH_SIZE / WRITE_SIZE counters)")
@@ -449,6 +452,16 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": n, "launches": args.steps}), flush=True)
+        return
+
+    if args.projection_only:
+        xin = _randn((12480, 4096), 0x5EED + 40, device)
+        w = _randn((4096, 4096), 0x5EED + 41, device, 0.0, 4096 ** -0.5)
+        y = torch.empty((12480, 4096), dtype=torch.bfloat16, device=device)
+        for _ in range(args.steps):
+            L.linear(xin, w, out=y, sumsq=True)
+        torch.cuda.synchronize()
+        print(json.dumps({"projection": [12480, 4096, 4096], "launches": args.steps}), flush=True)
         return
 
     x, c4 = bench_c4(device, args.steps, args.warmup, hip, args.settle_ms / 1e3)
