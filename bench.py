@@ -194,6 +194,73 @@ def bench_c1(device, steps, warmup, hip):
             "pct_peak": 100.0 * flops / (km * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
 
 
+def bench_short_keys(device, steps, warmup, hip):
+    """The HBM-bound calls at 640x384x97: text cross-attention (3120 video queries over 1024
+    text keys, 94 valid; and the CFG pair at B=2 with 94 and 1 valid), and the cross-modal
+    pair of a 4 s clip at D=64 with 1-D temporal RoPE (frame index 0..12 for the 3120 video
+    tokens, 0..125 for the 126 audio tokens): video queries over audio K/V and audio queries
+    over video K/V. Per call: the attention kernel's time (events the library records around
+    it), the whole call's, the algorithmic bytes (Q, valid K and V, tables, O, once each) and
+    the kernel's GB/s."""
+    import numpy as np
+    import torch
+
+    import ltx_attn as L
+
+    H = 32
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=device)
+    res = {}
+
+    def measure(name, q, k, v, bytes_, flops, **kw):
+        out = torch.empty_like(q)
+
+        def call(ev):
+            L.attention_fwd(q, k, v, heads=H, out=out, workspace=ws,
+                            events=None if ev is None else (ev[0], ev[1]), **kw)
+
+        wall, _ = time_steps(call, steps, warmup, hip, events_per_step=False)
+        _, kms = time_steps(call, steps, 0, hip)
+        km = sum(kms) / len(kms)
+        res[name] = {"kernel_ms": round(km, 4), "call_ms": round(wall / steps * 1e3, 4),
+                     "bytes": int(bytes_), "kernel_gbs": round(bytes_ / (km * 1e-3) / 1e9, 1),
+                     "pct_hbm_peak": round(100 * bytes_ / (km * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+                     "gflop": round(flops / 1e9, 3)}
+
+    Tv, Tt = 3120, 1024
+    for B, valid in ((1, [94]), (2, [94, 1])):
+        q = _randn((B, Tv, H * 128), 0x5EED + 20, device)
+        k = _randn((B, Tt, H * 128), 0x5EED + 21, device)
+        v = _randn((B, Tt, H * 128), 0x5EED + 22, device)
+        nk = sum(valid)
+        measure(f"text_cross_3120_B{B}", q, k, v, 2 * (2 * B * Tv + 2 * nk) * H * 128,
+                4.0 * Tv * nk * H * 128, k_valid_len=valid)
+
+    Ta, D = 126, 64
+    inner = H * D
+
+    def index_tables(idx):
+        pos = np.zeros((1, len(idx), 2), dtype=np.float32)     # [n_pos, tokens, (start, end)]
+        pos[0, :, 0] = idx
+        pos[0, :, 1] = idx
+        c, s_ = L.rope_tables(pos, inner, [20], H)
+        return L.Rotary(_dev_bits(c, device), _dev_bits(s_, device))
+
+    rv = index_tables(np.arange(Tv) // (20 * 12))
+    ra = index_tables(np.arange(Ta))
+    xv = _randn((1, Tv, inner), 0x5EED + 23, device)
+    xa = _randn((1, Ta, inner), 0x5EED + 24, device)
+    ya = _randn((1, Ta, inner), 0x5EED + 25, device)
+    yv = _randn((1, Tv, inner), 0x5EED + 26, device)
+    per_tok = 2 * inner          # one bf16 row of a stream, or its cos + sin table rows
+    measure("cross_modal_video_q_3120x126", xv, xa, ya,
+            (2 * Tv + 2 * Ta) * per_tok + (Tv + Ta) * per_tok, 4.0 * Tv * Ta * inner,
+            rotary=rv, key_rotary=ra)
+    measure("cross_modal_audio_q_126x3120", xa, xv, yv,
+            (2 * Ta + 2 * Tv) * per_tok + (Tv + Ta) * per_tok, 4.0 * Tv * Ta * inner,
+            rotary=ra, key_rotary=rv)
+    return res
+
+
 def bench_c5(device, steps, warmup, hip):
     """The six attentions of one DiT block at 1280x768x121, B=2 (CFG), in block order
     (Sources/LTXModules/DiTBlock.swift:343-438): attn1, audio_attn1, attn2, audio_attn2,
@@ -472,6 +539,11 @@ def main():
         c1 = bench_c1(device, 10, 3, hip)
         print(f"# c1: {c1['kernel_ms']:.3f} ms kernel, {c1['kernel_tflops']:.1f} TFLOP/s",
               file=sys.stderr, flush=True)
+        short = bench_short_keys(device, 10, 3, hip)
+        print("# short-key calls: " + ", ".join(f"{k} {v['kernel_ms']:.4f} ms "
+                                                 f"({v['kernel_gbs']:.0f} GB/s)"
+                                                 for k, v in short.items()),
+              file=sys.stderr, flush=True)
         c5 = bench_c5(device, 5, 2, hip)
         print(f"# c5: {c5['ms_per_block']:.3f} ms per block attention set", file=sys.stderr,
               flush=True)
@@ -488,6 +560,9 @@ def main():
             "video_self_3120_tflops": round(c1["kernel_tflops"], 2),
             "video_self_3120_pct_peak": round(c1["pct_peak"], 2),
             "video_self_3120_ms": round(c1["kernel_ms"], 4),
+            "video_self_3120_call_ms": round(c1["ms_per_call"], 4),
+            "video_self_3120_call_tflops": round(c1["tflops"], 2),
+            "short_key_calls": short,
             "dit_block_attn_ms": round(c5["ms_per_block"], 4),
             "dit_block_attn_tflops": round(c5["tflops"], 2),
             "dit_block_attn_kernel_ms": c5["kernel_ms"],

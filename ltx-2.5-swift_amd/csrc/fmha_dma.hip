@@ -40,32 +40,6 @@ struct DmaTile {
     static_assert(K_DMA >= 1 && V_DMA >= 1 && QW * D == ELEMS, "tile geometry");
 };
 
-// Unit swizzle for gfx950's LDS (64 four-byte banks; a 16-byte access is serviced 16 lanes
-// at a time): 16 consecutive rows reading the same logical unit hit 16 distinct bank groups.
-// Rows of 16 units span all banks (XOR with row & 15); rows of 8 units pair up per bank
-// window (XOR with (row >> 1) & 7). XOR makes the map its own inverse.
-template <int UNITS>
-__device__ __forceinline__ int swz(int row, int u) {
-    static_assert(UNITS == 16 || UNITS == 8, "row width");
-    return UNITS == 16 ? (u ^ (row & 15)) : (u ^ ((row >> 1) & 7));
-}
-
-// V tiles stay row-major (key rows of D channels) and are read through the transposing LDS
-// read: 32 lanes of a ds_read_b64_tr_b16 read 4 consecutive rows x 64 bytes, so the units of
-// rows r and r+1..r+3 must fall in distinct bank windows (XOR the unit with row & 3 scaled to
-// a quarter row; rows of 64 channels pair up, so rows r and r+2 differ instead).
-template <int UNITS>
-__device__ __forceinline__ int vswz(int row, int u) {
-    static_assert(UNITS == 16 || UNITS == 8, "row width");
-    return UNITS == 16 ? (u ^ ((row & 3) << 2)) : (u ^ (((row >> 1) & 1) << 2));
-}
-
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x2 ds_read_tr(const __attribute__((address_space(3))) bf16 *p) {
-    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4 *)p);
-    return __builtin_bit_cast(u32x2, v);
-}
-
 // S products with VGPR results. The builtin MFMA puts every result of this kernel in AGPRs
 // (the O accumulators need them), so S would reach the softmax through one v_accvgpr_read
 // per element; these are written as inline assembly instead:

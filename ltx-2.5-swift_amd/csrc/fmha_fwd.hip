@@ -557,9 +557,11 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const PrepParams p) {
     constexpr int PPH = D / 16;               // pair units per head
     constexpr int MAXU = 4;                   // pair units per thread (inner <= 16384)
     const int tid = threadIdx.x;
-    const int rid = blockIdx.x;
+    const int rid = blockIdx.x;                // output row b*L + lrow
     const int b = rid / p.L;
     const int lrow = rid % p.L;
+    const int Lf = p.L_full > 0 ? p.L_full : p.L;
+    const int64_t frow = (int64_t)b * Lf + lrow;  // row of the statistic and partials
     const int inner = p.H * D;
     const int units = p.H * PPH;
     const bf16 *row = (const bf16 *)p.x + (int64_t)b * p.bs + (int64_t)lrow * p.rs;
@@ -581,11 +583,11 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const PrepParams p) {
     float rstd = 1.0f;
     if (p.w && p.sumsq) {
         // The projection's partial sums, added in order (every thread reads the same row).
-        const float *parts = p.sumsq + (int64_t)rid * p.ss_rs;
+        const float *parts = p.sumsq + frow * p.ss_rs;
         float tot = 0.f;
         for (int j = 0; j < p.ss_blocks; ++j) tot += parts[j];
         rstd = 1.0f / sqrtf(tot / (float)inner + p.eps);
-        if (tid == 0 && p.rstd) p.rstd[rid] = rstd;
+        if (tid == 0 && p.rstd) p.rstd[frow] = rstd;
     } else if (p.w) {
         __shared__ float red[4];
 #pragma unroll
@@ -594,7 +596,7 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const PrepParams p) {
         __syncthreads();
         const float tot = red[0] + red[1] + red[2] + red[3];
         rstd = 1.0f / sqrtf(tot / (float)inner + p.eps);
-        if (tid == 0 && p.rstd) p.rstd[rid] = rstd;
+        if (tid == 0 && p.rstd) p.rstd[frow] = rstd;
     }
     if (!p.out) return;
     bf16 *dst = (bf16 *)p.out + (int64_t)rid * inner;
@@ -615,7 +617,7 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const PrepParams p) {
             }
         }
         if (p.cos) {
-            const int64_t toff = ((int64_t)hh * p.L + lrow) * (D / 2) + 8 * c;
+            const int64_t toff = ((int64_t)hh * Lf + lrow) * (D / 2) + 8 * c;
             float fc[8], fs[8];
             unpack8(ldg16((const bf16 *)p.cos + toff), fc);
             unpack8(ldg16((const bf16 *)p.sin + toff), fs);

@@ -13,6 +13,8 @@ constexpr int kQueriesPerWave = 64;
 constexpr int kWavesPerGroup = 4;
 constexpr int kQueriesPerGroup = kQueriesPerWave * kWavesPerGroup;  // 256
 constexpr int kMaxSplits = 16;
+// Keys of one (batch, head) the short-key kernel keeps resident in LDS.
+constexpr int short_max_keys(int D) { return D == 128 ? 128 : 256; }
 
 // Main attention kernel.
 struct FmhaParams {
@@ -48,6 +50,8 @@ struct FmhaParams {
     float *part_o;                   // tail partials [S][n_tail][256][D] fp32
     float *part_ml;                  // [S][n_tail][256][2]: running max (log2 units), row sum
     int32_t valid[kMaxBatch];        // keys valid per batch row (Lk when unmasked)
+    // Short-key kernel: workgroups per (batch, head); the grid is B * H * short_groups.
+    int32_t short_groups;
     // Output gate: bf16 logits, element strides; output rows times 2*sigmoid(logit), or null.
     const void *gate;
     int64_t g_bs, g_rs, g_hs;
@@ -58,14 +62,15 @@ struct FmhaParams {
 struct PrepParams {
     const void *x;                   // bf16
     int64_t bs, rs, hs;
-    int32_t B, L, H;
+    int32_t B, L, H;                 // rows 0 .. L-1 of each batch row are processed
+    int32_t L_full;                  // rows per batch of the tables, rstd and partials (0: L)
     const void *w;                   // bf16 [H*D] or null (no norm)
     float eps;
-    const void *cos, *sin;           // bf16 [H][L][D/2] or null
-    float *rstd;                     // [B][L] or null
+    const void *cos, *sin;           // bf16 [H][L_full][D/2] or null
+    float *rstd;                     // [B][L_full] or null
     void *out;                       // bf16 [B][L][H*D] contiguous or null
-    // Statistic given as partial sums of squares (row b*L + l at sumsq + row*ss_rs, ss_blocks
-    // partials), or null: computed from x.
+    // Statistic given as partial sums of squares (row b*L_full + l at sumsq + row*ss_rs,
+    // ss_blocks partials), or null: computed from x.
     const float *sumsq;
     int64_t ss_rs;
     int32_t ss_blocks;
@@ -128,6 +133,7 @@ struct RstdParams {
 enum KernelKind { kRegPlain = 0, kRegFused = 1, kDma = 2 };
 int launch_fmha(const FmhaParams &p, int D, int kind, void *stream);
 int launch_fmha_dma(const FmhaParams &p, int D, void *stream);   // fmha_dma.hip
+int launch_fmha_short(const FmhaParams &p, int D, void *stream); // fmha_short.hip
 int launch_prep(const PrepParams &p, int D, void *stream);
 int launch_combine(const CombineParams &p, int D, void *stream);
 int launch_passthrough(const PassParams &p, int D, void *stream);

@@ -47,10 +47,14 @@ struct Plan {
     bool q_rope = false, k_rope = false;
     bool passthrough = false;  // STG passthrough: out = V (x gate), no attention
     bool dma = false;          // LDS-DMA kernel (K prologue when K needs work)
+    bool shortk = false;       // short-key kernel: the head's keys resident in LDS
     bool k_prologue = false;   // K normalised/rotated by a separate pass into the workspace
     bool k_fused = false;      // K normalised/rotated while staging into LDS
     int nqblk = 0;
     int ntiles_max = 0;
+    int kmax = 0;              // largest valid key count over the batch
+    int kprep_rows = 0;        // rows per batch the K prologue prepares
+    int short_groups = 0;
     int64_t n_items = 0;       // (batch, head, query block) work items
     int64_t n_full = 0;        // items run whole; the rest are split into key ranges
     int splits = 1;
@@ -176,12 +180,13 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
                     ltx::kMaxSplits);
 
     pl->nqblk = (a->Lq + ltx::kQueriesPerGroup - 1) / ltx::kQueriesPerGroup;
-    pl->ntiles_max = (a->Lk + ltx::kKeyTile - 1) / ltx::kKeyTile;
+    pl->kmax = a->Lk;
     if (a->k_valid_len) {
-        int nmax = 1;
-        for (int b = 0; b < B; ++b) nmax = std::max(nmax, (int)a->k_valid_len[b]);
-        pl->ntiles_max = (nmax + ltx::kKeyTile - 1) / ltx::kKeyTile;
+        pl->kmax = 1;
+        for (int b = 0; b < B; ++b) pl->kmax = std::max(pl->kmax, (int)a->k_valid_len[b]);
     }
+    pl->ntiles_max = (pl->kmax + ltx::kKeyTile - 1) / ltx::kKeyTile;
+    pl->kprep_rows = a->Lk;
 
     // Kernel: with two or more query blocks per (batch, head) the LDS-DMA kernel reads K
     // (prepared by the K prologue when it needs norm/RoPE, one extra read+write of K) and V
@@ -190,6 +195,42 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
     // 32-bit byte offsets up to the key length padded to whole tiles; calls past that take
     // the register-staged kernel.
     const bool k_work = pl->k_norm || pl->k_rope;
+    // Short key ranges (text cross-attention over its valid keys, video queries over the
+    // audio keys) take the short-key kernel: the head's K (prepared by the prologue, only
+    // its valid rows, when it needs norm/RoPE) and V stay in LDS while the queries stream
+    // past. It addresses a head's Q rows with 32-bit byte offsets, and has no D = 128
+    // variant with RoPE (no such call in the model: text cross-attention takes no RoPE).
+    const int64_t lq_pad = ((int64_t)a->Lq + ltx::kQueriesPerWave - 1) / ltx::kQueriesPerWave *
+                           ltx::kQueriesPerWave;
+    if (a->kprep == LTX_ATTN_KPREP_AUTO && a->num_splits == 0 && B <= ltx::kMaxBatch &&
+        pl->kmax <= ltx::short_max_keys(D) && !(D == 128 && pl->q_rope) &&
+        lq_pad * a->q_rs * 2 < 0x7fffffff) {
+        pl->shortk = true;
+        pl->k_prologue = k_work;
+        pl->kprep_rows = pl->kmax;
+        // about four waves' worth of query blocks per SIMD at once: B*H*G workgroups of four
+        // waves over 256 CUs, no more groups than a head's query blocks fill
+        const int64_t heads = (int64_t)B * H;
+        const int64_t qb64 = (a->Lq + ltx::kQueriesPerWave - 1) / ltx::kQueriesPerWave;
+        int64_t G = (kConcurrentGroups * ltx::kWavesPerGroup + heads * ltx::kWavesPerGroup - 1) /
+                    (heads * ltx::kWavesPerGroup);
+        G = std::max<int64_t>(1, std::min(G, (qb64 + ltx::kWavesPerGroup - 1) / ltx::kWavesPerGroup));
+        pl->short_groups = (int)G;
+        pl->n_items = pl->n_full = heads * G;
+        pl->grid = heads * G;
+        if (pl->grid > 0x7fffffff) return fail(LTX_ATTN_EUNSUPPORTED, "grid too large");
+        size_t off = 0;
+        if (pl->q_norm) {
+            pl->off_qrstd = off;
+            off = align_up(off + sizeof(float) * (size_t)B * a->Lq, 256);
+        }
+        if (pl->k_prologue) {
+            pl->off_kprep = off;
+            off = align_up(off + 2 * (size_t)B * pl->kprep_rows * H * D, 256);
+        }
+        pl->bytes = off;
+        return LTX_ATTN_OK;
+    }
     const int64_t lk_pad = ((int64_t)a->Lk + ltx::kKeyTile - 1) / ltx::kKeyTile * ltx::kKeyTile;
     const int64_t k_rs_eff = k_work ? (int64_t)H * D : a->k_rs;
     const bool dma_fits = lk_pad * k_rs_eff * 2 < 0x7fffffff && lk_pad * a->v_rs * 2 < 0x7fffffff;
@@ -341,7 +382,7 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     } else if (pl.k_prologue || (pl.k_fused && pl.k_norm)) {
         ltx::PrepParams pp{};
         pp.x = a->k; pp.bs = a->k_bs; pp.rs = a->k_rs; pp.hs = a->k_hs;
-        pp.B = B; pp.L = a->Lk; pp.H = H;
+        pp.B = B; pp.L = pl.k_prologue ? pl.kprep_rows : a->Lk; pp.L_full = a->Lk; pp.H = H;
         pp.w = a->k_norm_w; pp.eps = a->norm_eps;
         if (pl.k_stat) {
             pp.sumsq = a->k_sumsq; pp.ss_rs = a->k_sumsq_rs; pp.ss_blocks = a->sumsq_blocks;
@@ -357,7 +398,7 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
             return fail(LTX_ATTN_EHIP, "k prologue launch: %s", hipGetErrorString((hipError_t)e));
         if (pl.k_prologue) {
             kptr = ws + pl.off_kprep;
-            k_bs = (int64_t)a->Lk * H * D; k_rs = (int64_t)H * D; k_hs = D;
+            k_bs = (int64_t)pl.kprep_rows * H * D; k_rs = (int64_t)H * D; k_hs = D;
         }
     }
 
@@ -388,6 +429,7 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     fp.num_splits = pl.splits;
     fp.tiles_per_split = pl.tiles_per_split;
     fp.grid = (int32_t)pl.grid;
+    fp.short_groups = pl.short_groups;
     if (pl.n_full < pl.n_items) {
         fp.part_o = (float *)(ws + pl.off_part_o);
         fp.part_ml = (float *)(ws + pl.off_part_ml);
@@ -423,7 +465,8 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     if (a->ev_attn_start)
         if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_start, (hipStream_t)stream))
             return fail(LTX_ATTN_EHIP, "event record: %s", hipGetErrorString(e));
-    if (int e = ltx::launch_fmha(fp, D, kind, stream))
+    if (int e = pl.shortk ? ltx::launch_fmha_short(fp, D, stream)
+                          : ltx::launch_fmha(fp, D, kind, stream))
         return fail(LTX_ATTN_EHIP, "attention launch: %s", hipGetErrorString((hipError_t)e));
     if (a->ev_attn_stop)
         if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_stop, (hipStream_t)stream))

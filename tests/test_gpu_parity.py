@@ -118,7 +118,8 @@ def test_golden_fixture(device, name):
           if key in g}
     if "valid_len" in g:
         kw["k_valid_len"] = list(g["valid_len"])
-    for kprep in (L.KPREP_FUSED, L.KPREP_PROLOGUE):
+    # AUTO picks the short-key kernel where the keys fit in LDS, else the LDS-DMA kernel
+    for kprep in (L.KPREP_AUTO, L.KPREP_FUSED, L.KPREP_PROLOGUE):
         got = run(device, g["q"], g["k"], g["v"], meta["heads"], kprep=kprep, **dict(kw))
         check(got, g["out_exact"], O.bf16_bits_to_f32(g["out_ref_bf16"]),
               f"{name} kprep={kprep}")
@@ -184,16 +185,17 @@ def _gate_bits(shape, seed):
 
 
 @pytest.mark.parametrize("case", ["dma_whole_and_tail", "register_split", "register_whole",
-                                  "strided_logits"])
+                                  "short_keys", "strided_logits"])
 def test_output_gate(device, case):
     """The per-head gate (DiTAttention.swift:395-399) in every epilogue: the LDS-DMA kernel's
     whole items and the combine of its split tail items (2 x 16 heads x 9 query blocks = 288
-    items: 256 whole + 32 split in two), the register kernel split and unsplit, and logits
-    given as a strided view."""
+    items: 256 whole + 32 split in two), the register kernel split and unsplit, the short-key
+    kernel, and logits given as a strided view."""
     import torch
 
     B, H, Lq, Lk, D, kw = {
-        "dma_whole_and_tail": (2, 16, 2100, 128, 128, {}),
+        "dma_whole_and_tail": (2, 16, 2100, 128, 128, {"kprep": L.KPREP_PROLOGUE}),
+        "short_keys": (2, 8, 1500, 100, 128, {}),
         "register_split": (1, 4, 126, 1500, 64, {"num_splits": 3}),
         "register_whole": (2, 4, 100, 300, 128, {"num_splits": 1}),
         "strided_logits": (1, 8, 600, 200, 128, {}),
@@ -291,6 +293,52 @@ def test_rebase_path_large_logits(device):
     # the same through split-KV (rebases inside each split, then the combine)
     got = run(device, q, k, v, H, scale=scale, num_splits=4)
     check(got, truth, None, "rebase split")
+
+
+@pytest.mark.parametrize("B,H,Lq,Lk,D,valid,rope", [
+    (2, 4, 1000, 1024, 128, [128, 1], False),   # most keys kept at D=128; a single key
+    (2, 4, 1000, 300, 64, [256, 129], True),    # most keys kept at D=64, norm + RoPE
+    (2, 32, 4100, 77, 64, None, True),          # 65 query blocks per head: 4-5 per wave
+    (1, 2, 1, 3, 128, None, False),             # one query
+])
+def test_short_key_kernel(device, B, H, Lq, Lk, D, valid, rope):
+    """The short-key kernel (the head's keys resident in LDS, queries streamed by blocks of
+    64 with the next block's Q in flight) against the oracle, and the LDS-DMA kernel on the
+    same call, with norm on both sides (its gated epilogue: test_output_gate)."""
+    _say(f"short keys B={B} H={H} Lq={Lq} Lk={Lk} D={D} valid={valid} rope={rope}")
+    seed = 0x5EED + 90 + Lq
+    q = O.randn_bf16_bits((B, Lq, H * D), seed)
+    k = O.randn_bf16_bits((B, Lk, H * D), seed + 1)
+    v = O.randn_bf16_bits((B, Lk, H * D), seed + 2)
+    wq = O.randn_bf16_bits((H * D,), seed + 3, mean=1.0, std=0.02)
+    wk = O.randn_bf16_bits((H * D,), seed + 4, mean=1.0, std=0.02)
+    kw = dict(q_norm_w=wq, k_norm_w=wk)
+    if rope:
+        qc, qs = _index_rotary(np.arange(Lq) // 7, H * D, H)
+        kc, ks = _index_rotary(np.arange(Lk) // 3, H * D, H)
+        kw.update(q_cos=qc, q_sin=qs, k_cos=kc, k_sin=ks)
+    truth = O.attention(q, k, v, H, valid_len=valid, mode="exact", **kw)
+    ref = O.attention(q, k, v, H, valid_len=valid, mode="reference", **kw)
+    for kprep in (L.KPREP_AUTO, L.KPREP_PROLOGUE):
+        got = run(device, q, k, v, H, k_valid_len=valid, kprep=kprep, **dict(kw))
+        check(got, truth, O.round_bf16(ref), f"short keys kprep={kprep}")
+
+
+def test_short_key_kernel_large_logits(device):
+    """Logits growing along the keys (up to ~100 log2 units above the first 32-key block's
+    max) make the short-key kernel redo its blocks from the true row max. scale = ln 2 folds
+    to exactly 1, so the logits are exact and the check is on the softmax arithmetic."""
+    B, H, Lq, Lk, D = 1, 2, 200, 250, 64
+    rng = np.random.default_rng(7)
+    qf = rng.standard_normal((B, Lq, H * D)).astype(np.float32) * 2.0
+    kf = rng.standard_normal((B, Lk, H * D)).astype(np.float32)
+    kf *= (1.0 + np.arange(Lk, dtype=np.float32) / 40.0)[None, :, None]
+    q, k = O.f32_to_bf16_bits(qf), O.f32_to_bf16_bits(kf)
+    v = O.randn_bf16_bits((B, Lk, H * D), 8)
+    scale = float(np.float32(math.log(2.0)))
+    truth = O.attention(q, k, v, H, scale=scale, mode="exact")
+    got = run(device, q, k, v, H, scale=scale)
+    check(got, truth, None, "short keys, large logits")
 
 
 def test_split_layout_and_strided_output(device):
