@@ -194,7 +194,7 @@ def bench_c1(device, steps, warmup, hip):
             "pct_peak": 100.0 * flops / (km * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
 
 
-def bench_short_keys(device, steps, warmup, hip):
+def bench_short_keys(device, steps, warmup, hip, block=True):
     """The HBM-bound calls at 640x384x97: text cross-attention (3120 video queries over 1024
     text keys, 94 valid; and the CFG pair at B=2 with 94 and 1 valid), and the cross-modal
     pair of a 4 s clip at D=64 with 1-D temporal RoPE (frame index 0..12 for the 3120 video
@@ -258,6 +258,29 @@ def bench_short_keys(device, steps, warmup, hip):
     measure("cross_modal_audio_q_126x3120", xa, xv, yv,
             (2 * Ta + 2 * Tv) * per_tok + (Tv + Ta) * per_tok, 4.0 * Tv * Ta * inner,
             rotary=ra, key_rotary=rv)
+    if not block:
+        return res
+
+    # The block set's two large short-key calls at 1280x768x121, B=2: video->text over 94 of
+    # 1024 text keys (norm on both sides) and video queries over the 152 audio keys (norm +
+    # temporal RoPE); bytes are the attention kernel's own (the statistic and K passes are
+    # separate launches).
+    B, Tv, Ta = 2, 15360, 152
+    tabs = L.rotaries(121, 768, 1280, audio_tokens=Ta)
+    rvc = L.Rotary(*(_dev_bits(t, device) for t in tabs["videoCross"]))
+    rac = L.Rotary(*(_dev_bits(t, device) for t in tabs["audioCross"]))
+    w4 = _randn((4096,), 0x5EED + 100, device, 1.0, 0.02)
+    w2 = _randn((2048,), 0x5EED + 101, device, 1.0, 0.02)
+    qv = _randn((B, Tv, 4096), 0x5EED + 50, device)
+    kt = _randn((B, 1024, 4096), 0x5EED + 70, device)
+    measure("block_text_cross_15360_B2", qv, kt, kt, 2 * (2 * B * Tv + 2 * 188) * 4096,
+            4.0 * B * Tv * 94 * 4096, q_norm_w=w4, k_norm_w=w4, k_valid_len=[94, 94])
+    del qv, kt
+    qv2 = _randn((B, Tv, 2048), 0x5EED + 90, device)
+    ka = _randn((B, Ta, 2048), 0x5EED + 60, device)
+    measure("block_video_q_15360x152_B2", qv2, ka, ka,
+            2 * (2 * B * Tv + 2 * B * Ta) * 2048 + 2 * (Tv + Ta) * 2048,
+            4.0 * B * Tv * Ta * 2048, q_norm_w=w2, k_norm_w=w2, rotary=rvc, key_rotary=rac)
     return res
 
 
@@ -489,6 +512,10 @@ def main():
     ap.add_argument("--projection-only", action="store_true",
                     help="only run the 12480 x 4096 x 4096 projection (ltx_linear with its "
                          "statistic), --steps times (for counter passes)")
+    ap.add_argument("--short-keys-only", action="store_true",
+                    help="only run the short-key calls (text cross-attention, the cross-modal "
+                         "pair, the block set's video->text and video->audio-keys calls), "
+                         "--steps times each (for counter passes)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB, --steps times "
                          "(the known-size kernel that scales FETCH_SIZE / WRITE_SIZE counters)")
@@ -529,6 +556,11 @@ def main():
             L.linear(xin, w, out=y, sumsq=True)
         torch.cuda.synchronize()
         print(json.dumps({"projection": [12480, 4096, 4096], "launches": args.steps}), flush=True)
+        return
+
+    if args.short_keys_only:
+        res = bench_short_keys(device, args.steps, args.warmup, hip)
+        print(json.dumps({"short_key_calls": res}), flush=True)
         return
 
     x, c4 = bench_c4(device, args.steps, args.warmup, hip, args.settle_ms / 1e3)

@@ -550,14 +550,20 @@ void fmha_fwd_kernel(const FmhaParams p) {
 // ------------------------------------------------------------------------------------------
 // Prologue: per-token RMS statistic over the inner dim (DiTAttention.swift:202-204), and for
 // the K-prologue strategy the normalised + rotated tensor in the merged layout.
-// One workgroup per token row.
+// One wave per token row, four rows per workgroup. A lane holds UPL pair units of its row
+// (channels 8c .. +7 and D/2 + 8c .. +7 of a head, the two halves the rotation mixes) and
+// issues all of their loads, and those of its RoPE table rows, before any arithmetic, so
+// each lane has its whole share of the row in flight; the sum of squares is reduced within
+// the wave.
 // ------------------------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(256) void qk_prep_kernel(const PrepParams p) {
+constexpr int kPrepRows = NT / 64;             // token rows per workgroup
+
+template <int D, int UPL>
+__global__ __launch_bounds__(NT) void qk_prep_kernel(const PrepParams p) {
     constexpr int PPH = D / 16;               // pair units per head
-    constexpr int MAXU = 4;                   // pair units per thread (inner <= 16384)
-    const int tid = threadIdx.x;
-    const int rid = blockIdx.x;                // output row b*L + lrow
+    const int lane = threadIdx.x & 63;
+    const int rid = blockIdx.x * kPrepRows + (threadIdx.x >> 6);   // output row b*L + lrow
+    if (rid >= p.B * p.L) return;
     const int b = rid / p.L;
     const int lrow = rid % p.L;
     const int Lf = p.L_full > 0 ? p.L_full : p.L;
@@ -566,45 +572,57 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const PrepParams p) {
     const int units = p.H * PPH;
     const bf16 *row = (const bf16 *)p.x + (int64_t)b * p.bs + (int64_t)lrow * p.rs;
 
-    float x1[MAXU][8], x2[MAXU][8];
-    float ss = 0.f;
+    u32x4 x1[UPL], x2[UPL], tc[UPL], ts[UPL];
 #pragma unroll
-    for (int k = 0; k < MAXU; ++k) {
-        const int u = tid + 256 * k;
+    for (int k = 0; k < UPL; ++k) {
+        const int u = lane + 64 * k;
         if (u < units) {
             const int hh = u / PPH, c = u % PPH;
             const bf16 *src = row + (int64_t)hh * p.hs;
-            unpack8(ldg16(src + 8 * c), x1[k]);
-            unpack8(ldg16(src + D / 2 + 8 * c), x2[k]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ss += x1[k][e] * x1[k][e] + x2[k][e] * x2[k][e];
+            x1[k] = ldg16(src + 8 * c);
+            x2[k] = ldg16(src + D / 2 + 8 * c);
+            if (p.out && p.cos) {
+                const int64_t toff = ((int64_t)hh * Lf + lrow) * (D / 2) + 8 * c;
+                tc[k] = ldg16((const bf16 *)p.cos + toff);
+                ts[k] = ldg16((const bf16 *)p.sin + toff);
+            }
         }
     }
     float rstd = 1.0f;
     if (p.w && p.sumsq) {
-        // The projection's partial sums, added in order (every thread reads the same row).
+        // The projection's partial sums, added in order (every lane reads the same row).
         const float *parts = p.sumsq + frow * p.ss_rs;
         float tot = 0.f;
         for (int j = 0; j < p.ss_blocks; ++j) tot += parts[j];
         rstd = 1.0f / sqrtf(tot / (float)inner + p.eps);
-        if (tid == 0 && p.rstd) p.rstd[frow] = rstd;
+        if (lane == 0 && p.rstd) p.rstd[frow] = rstd;
     } else if (p.w) {
-        __shared__ float red[4];
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < UPL; ++k) {
+            if (lane + 64 * k < units) {
+                float a[8], c2[8];
+                unpack8(x1[k], a);
+                unpack8(x2[k], c2);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss += a[e] * a[e] + c2[e] * c2[e];
+            }
+        }
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
-        __syncthreads();
-        const float tot = red[0] + red[1] + red[2] + red[3];
-        rstd = 1.0f / sqrtf(tot / (float)inner + p.eps);
-        if (tid == 0 && p.rstd) p.rstd[frow] = rstd;
+        rstd = 1.0f / sqrtf(ss / (float)inner + p.eps);
+        if (lane == 0 && p.rstd) p.rstd[frow] = rstd;
     }
     if (!p.out) return;
     bf16 *dst = (bf16 *)p.out + (int64_t)rid * inner;
 #pragma unroll
-    for (int k = 0; k < MAXU; ++k) {
-        const int u = tid + 256 * k;
+    for (int k = 0; k < UPL; ++k) {
+        const int u = lane + 64 * k;
         if (u >= units) continue;
         const int hh = u / PPH, c = u % PPH;
+        float a[8], c2[8];
+        unpack8(x1[k], a);
+        unpack8(x2[k], c2);
         if (p.w) {
             float w1[8], w2[8];
             const bf16 *w = (const bf16 *)p.w + hh * D;
@@ -612,24 +630,23 @@ __global__ __launch_bounds__(256) void qk_prep_kernel(const PrepParams p) {
             unpack8(ldg16(w + D / 2 + 8 * c), w2);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                x1[k][e] = (x1[k][e] * rstd) * w1[e];
-                x2[k][e] = (x2[k][e] * rstd) * w2[e];
+                a[e] = (a[e] * rstd) * w1[e];
+                c2[e] = (c2[e] * rstd) * w2[e];
             }
         }
         if (p.cos) {
-            const int64_t toff = ((int64_t)hh * Lf + lrow) * (D / 2) + 8 * c;
             float fc[8], fs[8];
-            unpack8(ldg16((const bf16 *)p.cos + toff), fc);
-            unpack8(ldg16((const bf16 *)p.sin + toff), fs);
+            unpack8(tc[k], fc);
+            unpack8(ts[k], fs);
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float a = x1[k][e], bb = x2[k][e];
-                x1[k][e] = a * fc[e] - bb * fs[e];
-                x2[k][e] = bb * fc[e] + a * fs[e];
+                const float x = a[e], y = c2[e];
+                a[e] = x * fc[e] - y * fs[e];
+                c2[e] = y * fc[e] + x * fs[e];
             }
         }
-        *(u32x4 *)(dst + hh * D + 8 * c) = pack8(x1[k]);
-        *(u32x4 *)(dst + hh * D + D / 2 + 8 * c) = pack8(x2[k]);
+        *(u32x4 *)(dst + hh * D + 8 * c) = pack8(a);
+        *(u32x4 *)(dst + hh * D + D / 2 + 8 * c) = pack8(c2);
     }
 }
 
@@ -745,11 +762,22 @@ int launch_rstd(const RstdParams &p, void *stream) {
     return (int)hipGetLastError();
 }
 
+template <int D>
+static void launch_prep_d(const PrepParams &p, dim3 grid, hipStream_t st) {
+    const int upl = (p.H * (D / 16) + 63) / 64;   // pair units per lane (inner <= 16384)
+    if (upl <= 1) hipLaunchKernelGGL((qk_prep_kernel<D, 1>), grid, dim3(NT), 0, st, p);
+    else if (upl <= 2) hipLaunchKernelGGL((qk_prep_kernel<D, 2>), grid, dim3(NT), 0, st, p);
+    else if (upl <= 4) hipLaunchKernelGGL((qk_prep_kernel<D, 4>), grid, dim3(NT), 0, st, p);
+    else if (upl <= 8) hipLaunchKernelGGL((qk_prep_kernel<D, 8>), grid, dim3(NT), 0, st, p);
+    else hipLaunchKernelGGL((qk_prep_kernel<D, 16>), grid, dim3(NT), 0, st, p);
+}
+
 int launch_prep(const PrepParams &p, int D, void *stream) {
-    const dim3 grid(p.B * p.L), block(256);
+    const int64_t rows = (int64_t)p.B * p.L;
+    const dim3 grid((unsigned)((rows + kPrepRows - 1) / kPrepRows));
     hipStream_t st = (hipStream_t)stream;
-    if (D == 128) hipLaunchKernelGGL(qk_prep_kernel<128>, grid, block, 0, st, p);
-    else hipLaunchKernelGGL(qk_prep_kernel<64>, grid, block, 0, st, p);
+    if (D == 128) launch_prep_d<128>(p, grid, st);
+    else launch_prep_d<64>(p, grid, st);
     return (int)hipGetLastError();
 }
 
