@@ -47,9 +47,14 @@ typedef enum {
     LTX_ATTN_EWORKSPACE = 4    /* workspace missing or smaller than ltx_attn_workspace_bytes */
 } ltx_attn_status;
 
-/* How K gets its norm + RoPE (only matters when a K norm weight or K tables are given). */
+/* How K gets its norm + RoPE (when a K norm weight or K tables are given), and with it the
+ * attention kernel. AUTO: calls whose valid keys fit in LDS (<= 128 at D=128 without RoPE,
+ * <= 256 at D=64) take the short-key kernel (the prologue prepares only the valid K rows);
+ * other calls the prologue when K is re-read by >= 2 query blocks, else the fused staging.
+ * FUSED and PROLOGUE force the register-staged and the LDS-DMA kernel. Results agree within
+ * the stated tolerance, not bit for bit, across kernels. */
 typedef enum {
-    LTX_ATTN_KPREP_AUTO = 0,     /* pick by cost: prologue when K is re-read by >= 2 query blocks */
+    LTX_ATTN_KPREP_AUTO = 0,     /* pick by cost (above)                                          */
     LTX_ATTN_KPREP_FUSED = 1,    /* normalise + rotate K inside the attention kernel's LDS staging */
     LTX_ATTN_KPREP_PROLOGUE = 2  /* one pass writes normed+rotated K (bf16) into the workspace     */
 } ltx_attn_kprep;
