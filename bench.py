@@ -284,6 +284,40 @@ def bench_short_keys(device, steps, warmup, hip, block=True):
     return res
 
 
+def bench_connector(device, steps, warmup, hip):
+    """The embeddings connector's attention at 1024 tokens (EmbeddingsConnector.swift:
+    288-331), video width 4096 (32 x 128) and audio width 2048 (32 x 64): q/k norm over the
+    width, the connector's 1-D RoPE, the per-head gate, no mask. ms per call (events around
+    the attention kernel, and the whole call)."""
+    import torch
+
+    import ltx_attn as L
+
+    H, T = 32, 1024
+    res = {}
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=device)
+    for width, seed in ((4096, 300), (2048, 310)):
+        q, k, v = (_randn((1, T, width), 0x5EED + seed + i, device) for i in range(3))
+        w = _randn((width,), 0x5EED + seed + 3, device, 1.0, 0.02)
+        gate = _randn((1, T, H), 0x5EED + seed + 4, device, 0.0, 2.0)
+        rot = L.connector_rotary(T, width, H, device)
+        out = torch.empty_like(q)
+
+        def call(ev):
+            L.attention_fwd(q, k, v, heads=H, q_norm_w=w, k_norm_w=w, rotary=rot,
+                            gate_logits=gate, out=out, workspace=ws,
+                            events=None if ev is None else (ev[0], ev[1]))
+
+        wall, _ = time_steps(call, steps, warmup, hip, events_per_step=False)
+        _, kms = time_steps(call, steps, 0, hip)
+        km = sum(kms) / len(kms)
+        fl = 4.0 * T * T * width
+        res[f"connector_{width}"] = {"kernel_ms": round(km, 4),
+                                     "call_ms": round(wall / steps * 1e3, 4),
+                                     "kernel_tflops": round(fl / (km * 1e-3) / 1e12, 1)}
+    return res
+
+
 def bench_c5(device, steps, warmup, hip):
     """The six attentions of one DiT block at 1280x768x121, B=2 (CFG), in block order
     (Sources/LTXModules/DiTBlock.swift:343-438): attn1, audio_attn1, attn2, audio_attn2,
@@ -576,6 +610,7 @@ def main():
                                                  f"({v['kernel_gbs']:.0f} GB/s)"
                                                  for k, v in short.items()),
               file=sys.stderr, flush=True)
+        conn = bench_connector(device, 10, 3, hip)
         c5 = bench_c5(device, 5, 2, hip)
         print(f"# c5: {c5['ms_per_block']:.3f} ms per block attention set", file=sys.stderr,
               flush=True)
@@ -595,6 +630,7 @@ def main():
             "video_self_3120_call_ms": round(c1["ms_per_call"], 4),
             "video_self_3120_call_tflops": round(c1["tflops"], 2),
             "short_key_calls": short,
+            "connector_attn_1024": conn,
             "dit_block_attn_ms": round(c5["ms_per_block"], 4),
             "dit_block_attn_tflops": round(c5["tflops"], 2),
             "dit_block_attn_kernel_ms": c5["kernel_ms"],

@@ -594,6 +594,29 @@ def rope_audio_positions(tokens, hop_length=160, sample_rate=16000, downsample=4
     return out
 
 
+def rope_connector_positions(sequence: int) -> np.ndarray:
+    """The embeddings connector's 1-D index grid (EmbeddingsConnector.swift:239-248):
+    positions ``0 .. sequence-1`` as ``[1, sequence, 2]`` bounds whose centre is the index,
+    for ``rope_tables(..., max_pos=[CONNECTOR_MAX_POS])``."""
+    idx = np.arange(sequence, dtype=np.float32)
+    return np.stack([idx, idx], axis=-1)[None]
+
+
+CONNECTOR_MAX_POS = 4096   # EmbeddingsConnector.positionalMaxPosition (:84)
+
+
+def connector_rotary(sequence: int, width: int, heads: int = 32, device=None):
+    """The connector's split-RoPE tables for ``sequence`` tokens of a ``width``-wide stream
+    (4096 video, 2048 audio; theta 1e4, maxPos 4096, one positional dimension, no identity
+    padding) as a ``Rotary`` of bf16 device tensors."""
+    import torch
+
+    cos, sin = rope_tables(rope_connector_positions(sequence), width, [CONNECTOR_MAX_POS], heads)
+    dev = device or "cuda"
+    to = lambda b: torch.from_numpy(b.view(np.int16)).to(dev).view(torch.bfloat16)  # noqa: E731
+    return Rotary(to(cos), to(sin))
+
+
 def rope_tables(positions: np.ndarray, inner: int, max_pos, heads: int = 32,
                 theta: float = 10000.0):
     """bf16 bit patterns ``(cos, sin)``, each ``[heads, tokens, inner/2/heads]`` uint16."""

@@ -4,6 +4,7 @@ without a GPU), sizes its workspace, and builds the RoPE tables like the referen
 
 import ctypes
 import json
+import math
 import os
 import re
 import subprocess
@@ -423,3 +424,38 @@ def test_cpp_host_mirror_error_behaviour(tmp_path):
     run = subprocess.run([exe], capture_output=True, text=True)
     assert run.returncode == 0, run.stdout + run.stderr
     assert "0 failure(s)" in run.stdout
+
+
+def test_connector_rope_tables():
+    """The embeddings connector's tables (EmbeddingsConnector.swift:218-248): positions
+    arange(seq) over maxPos 4096, one positional dimension filling width/2 frequencies (no
+    identity padding), per-head reshape. Checked against the oracle's table recipe (the two
+    evaluate cos/sin of the same float32 angle with different float32 libraries, which may
+    land on either side of a bf16 rounding boundary: at most one step, in at most 1e-5 of the
+    entries), and against the closed form angle_i = f_i * (2p/4096 - 1),
+    f_i = 1e4^(i/(n-1)) * pi/2, with cos/sin of the float32 angle in float64 (within one bf16
+    step, plus the float32 evaluation's absolute error)."""
+    import oracle as O
+
+    seq, heads = 1024, 32
+    for width in (4096, 2048):
+        cos, sin = L.rope_tables(L.rope_connector_positions(seq), width, [L.CONNECTOR_MAX_POS],
+                                 heads)
+        pos = np.zeros((1, 1, seq, 2), dtype=np.float32)
+        pos[0, 0, :, 0] = pos[0, 0, :, 1] = np.arange(seq)
+        oc, os_ = O.rotary_tables(pos, width, [L.CONNECTOR_MAX_POS], heads)
+        for got, ref in ((cos, oc), (sin, os_)):
+            diff = got != ref
+            assert diff.mean() <= 1e-5
+            step = np.abs(got.astype(np.int32) - ref.astype(np.int32))
+            assert step.max() <= 1
+        n = width // 2
+        t = np.array([1.0 if i == n - 1 else i * (1.0 / (n - 1)) for i in range(n)])
+        f = (10000.0 ** t * math.pi / 2).astype(np.float32)
+        frac = (np.arange(seq, dtype=np.float32) / np.float32(4096.0)).astype(np.float32)
+        ang = (f[None, :] * (frac * np.float32(2.0) - np.float32(1.0))[:, None]).astype(np.float32)
+        want_c = np.cos(ang.astype(np.float64)).reshape(seq, heads, n // heads).transpose(1, 0, 2)
+        want_s = np.sin(ang.astype(np.float64)).reshape(seq, heads, n // heads).transpose(1, 0, 2)
+        for got, want in ((cos, want_c), (sin, want_s)):
+            g = O.bf16_bits_to_f32(got).astype(np.float64)
+            assert np.all(np.abs(g - want) <= 2.0 ** -7 * np.abs(want) + 1e-7)

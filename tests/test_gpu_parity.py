@@ -341,6 +341,33 @@ def test_short_key_kernel_large_logits(device):
     check(got, truth, None, "short keys, large logits")
 
 
+@pytest.mark.parametrize("width,head_dim", [(4096, 128), (2048, 64)])
+def test_connector_attention(device, width, head_dim):
+    """The embeddings connector's attention (EmbeddingsConnector.swift:288-331): q/k
+    RMS-normed over the full width, the connector's 1-D split RoPE (arange(1024) over
+    maxPos 4096), no mask, scale 1/sqrt(head_dim), and the per-head 2*sigmoid gate from
+    to_gate_logits, over 1024 tokens and 32 heads, against the oracle (whose arithmetic is the
+    connector's explicit fp32 softmax). The attention is compared ungated to the stated
+    tolerance and the gate as the gated output against the ungated one times the bf16 gate."""
+    H, T = 32, 1024
+    _say(f"connector attention width={width} head_dim={head_dim}")
+    seed = 0x5EED + 200 + head_dim
+    x = [O.randn_bf16_bits((1, T, width), seed + i) for i in range(3)]
+    wq = O.randn_bf16_bits((width,), seed + 3, mean=1.0, std=0.02)
+    wk = O.randn_bf16_bits((width,), seed + 4, mean=1.0, std=0.02)
+    cos, sin = L.rope_tables(L.rope_connector_positions(T), width, [L.CONNECTOR_MAX_POS], H)
+    g = _gate_bits((1, T, H), seed + 5)
+    kw = dict(q_norm_w=wq, k_norm_w=wk, q_cos=cos, q_sin=sin)
+    truth = O.attention(*x, H, mode="exact", **kw)
+    ref = O.attention(*x, H, mode="reference", **kw)
+    plain = run(device, *x, H, **dict(kw))
+    check(plain, truth, O.round_bf16(ref), f"connector {width}")
+    gated = run(device, *x, H, gate_logits=g, **dict(kw))
+    want = plain.reshape(1, T, H, head_dim) * O.head_gate(g, "reference")[..., None]
+    err = np.abs(gated.reshape(1, T, H, head_dim) - want)
+    assert np.all(err <= np.abs(want) * 2.0 ** -7 + 1e-6), float(err.max())
+
+
 def test_split_layout_and_strided_output(device):
     import torch
 
