@@ -1,34 +1,41 @@
 // Attention kernel for short key ranges: text cross-attention over its valid keys, and the
 // cross-modal call of the video queries over the audio keys (Sources/LTXModules/
 // DiTBlock.swift:390-415, :470-508). The whole K and V of a (batch, head) stay resident in
-// LDS and every wave streams blocks of 64 queries past them.
+// LDS and every wave streams blocks of 32 queries past them.
 //
 // These calls move far more bytes than they compute (Q in and O out per query, a few KB of
 // K/V per head): HBM bounds them, and what matters is keeping loads in flight. A workgroup of
-// four waves owns one (batch, head) and 1/G of its query blocks. It copies the head's K and V
+// eight waves owns one (batch, head) and 1/G of its query blocks. It copies the head's K and V
 // into LDS once (LDS DMA, the tile layout of fmha_dma.hip: K rows swizzled for 16-byte
 // operand reads, V rows for transposing reads), then each wave walks its own query blocks
 // with no further barrier, loading the next block's Q, statistic and RoPE table rows into
-// registers while it computes the current one. Per block: S^T = K.Q'^T on the matrix cores
-// (Q' normalised, rotated and scaled by scale*log2(e) in fp32, rounded once), the first
-// 32-key block sets the row max, p = exp2(s - m) rounded to bf16 with row sums of those
-// bf16 weights, O^T += V^T.P^T, then O * gate / l is staged in the wave's LDS area and
-// stored as whole 16-byte units of the output rows.
+// registers while it computes the current one, two waves per SIMD. Per block: S^T = K.Q'^T
+// on the matrix cores (Q' normalised, rotated and scaled by scale*log2(e) in fp32, rounded
+// once), the first 32-key block sets the row max, p = exp2(s - m) rounded to bf16 with row
+// sums of those bf16 weights, O^T += V^T.P^T, then O * gate / l is staged in the wave's LDS
+// area and stored as whole 16-byte units of the output rows.
 #include "lds_copy.hpp"
 
 namespace ltx {
 namespace {
 
+// Eight waves of 32-query blocks per workgroup, two waves per SIMD, so that one wave's
+// arithmetic overlaps the other's loads (four waves of 64-query blocks, one per SIMD, reached
+// 2.9-3.6 TB/s on the block set's calls against 3.8-5.0 TB/s with this shape). The per-group
+// arrays below are indexed by the 32-query group of the wave block (QB of them).
 template <int D, bool ROPE>
-__global__ __attribute__((amdgpu_flat_work_group_size(NT, NT), amdgpu_waves_per_eu(1, 1)))
+__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
 void fmha_short_kernel(const FmhaParams p) {
     constexpr int NC = D / 16, NDB = D / 32, KU = D / 8;
+    constexpr int QB = 1;                             // 32-query groups per wave block
+    constexpr int SQW = 32 * QB;                      // queries per wave block
+    constexpr int SNW = 8;                            // waves per workgroup
     constexpr int TE = KT * D;                        // elements of a 64-key tile
     constexpr int TILES = short_max_keys(D) / KT;     // resident tiles
     constexpr int CPT = TE / 512;                     // 1 KB copies per tile
     __shared__ __attribute__((aligned(16))) bf16 sK[TILES * TE];
     __shared__ __attribute__((aligned(16))) bf16 sV[TILES * TE];
-    __shared__ __attribute__((aligned(16))) bf16 sO[NW * QW * D];
+    __shared__ __attribute__((aligned(16))) bf16 sO[SNW * SQW * D];
     __shared__ __attribute__((aligned(16))) bf16 sW[D];   // q_norm.weight of the head
 
     const int tid = threadIdx.x;
@@ -53,7 +60,7 @@ void fmha_short_kernel(const FmhaParams p) {
         const u32x4 rk = rsrc_words(Kb, (int64_t)n_valid * krow);
         const u32x4 rv = rsrc_words(Vb, (int64_t)n_valid * vrow);
         for (int t = 0; t < ntiles; ++t)
-            for (int c = wave; c < CPT; c += NW) {
+            for (int c = wave; c < CPT; c += SNW) {
                 const int q = c * 64 + lane;          // 16-byte unit of the tile
                 const int row = q / KU, slot = q % KU;
                 const int key = t * KT + row;
@@ -88,21 +95,21 @@ void fmha_short_kernel(const FmhaParams p) {
     };
 
     // ---- Q blocks of this wave -------------------------------------------------------
-    const int nqb = (p.Lq + QW - 1) / QW;
-    const int stride = G * NW;
+    const int nqb = (p.Lq + SQW - 1) / SQW;
+    const int stride = G * SNW;
     const bf16 *Qb = (const bf16 *)p.q + (int64_t)b * p.q_bs + (int64_t)h * p.q_hs;
     const rsrc_t rq = make_rsrc(Qb, (int64_t)p.Lq * p.q_rs * 2);   // rows past Lq read zero
     const int qrow = (int)(p.q_rs * 2);
     const bool norm = p.q_rstd != nullptr;
     struct Raw {
-        u32x4 x[2][NC];
-        u32x4 cs[2][ROPE ? NC / 2 : 1], sn[2][ROPE ? NC / 2 : 1];
-        float rs[2];
+        u32x4 x[QB][NC];
+        u32x4 cs[QB][ROPE ? NC / 2 : 1], sn[QB][ROPE ? NC / 2 : 1];
+        float rs[QB];
     };
     auto fetch = [&](int j, Raw &f) __attribute__((always_inline)) {
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-            const int qi = j * QW + 32 * qb + r;
+        for (int qb = 0; qb < QB; ++qb) {
+            const int qi = j * SQW + 32 * qb + r;
             const int qc = min(qi, p.Lq - 1);
 #pragma unroll
             for (int c = 0; c < NC; ++c)
@@ -120,9 +127,9 @@ void fmha_short_kernel(const FmhaParams p) {
     };
     // The Q prologue of load_q (fmha_device.hpp): norm with the statistic and the weight,
     // split-half rotation, scale*log2(e), one bf16 rounding.
-    auto convert = [&](const Raw &f, bf16x8 (&qf)[2][NC]) __attribute__((always_inline)) {
+    auto convert = [&](const Raw &f, bf16x8 (&qf)[QB][NC]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
+        for (int qb = 0; qb < QB; ++qb) {
             float x[NC][8];
 #pragma unroll
             for (int c = 0; c < NC; ++c) unpack8(f.x[qb][c], x[c]);
@@ -158,44 +165,54 @@ void fmha_short_kernel(const FmhaParams p) {
         }
     };
 
-    bf16 *Os = sO + wave * QW * D;                    // this wave's staging area
+    bf16 *Os = sO + wave * SQW * D;                   // this wave's staging area
     bf16 *Ob = (bf16 *)p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs;
-    int j = gi * NW + wave;
+    int j = gi * SNW + wave;
     Raw cur;
     if (j < nqb) fetch(j, cur);
     for (; j < nqb; j += stride) {
-        bf16x8 qf[2][NC];
+        bf16x8 qf[QB][NC];
         convert(cur, qf);
         if (j + stride < nqb) fetch(j + stride, cur);  // in flight while this block computes
 
-        f32x16 o[NDB][2];
+        f32x16 o[NDB][QB];
+        float l[QB];
+        f32x16 negm[QB];
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) o[db][0] = o[db][1] = splat16(0.f);
-        float l[2] = {0.f, 0.f};
-        f32x16 negm[2] = {splat16(0.f), splat16(0.f)};
+        for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) o[db][qb] = splat16(0.f);
+            l[qb] = 0.f;
+            negm[qb] = splat16(0.f);
+        }
         bool over = false;
         // S of key block kb, accumulated from C = init; keys past the valid ones -> -inf.
-        auto s_block = [&](int kb, f32x16 (&s)[2]) __attribute__((always_inline)) {
+        auto s_block = [&](int kb, f32x16 (&s)[QB]) __attribute__((always_inline)) {
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 const bf16x8 a = k_opnd(kb, c);
-                s[0] = mfma32(a, qf[0][c], c == 0 ? negm[0] : s[0]);
-                s[1] = mfma32(a, qf[1][c], c == 0 ? negm[1] : s[1]);
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb)
+                    s[qb] = mfma32(a, qf[qb][c], c == 0 ? negm[qb] : s[qb]);
             }
             if (ragged && kb == nkb - 1) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int key = 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
-                    if (key >= n_valid) s[0][i] = s[1][i] = -INFINITY;
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb)
+                        if (key >= n_valid) s[qb][i] = -INFINITY;
                 }
             }
         };
         // P = exp2(S) in bf16, the row sums of those weights, O^T += V^T.P^T.
-        auto p_block = [&](const f32x16 (&s)[2], int kb) __attribute__((always_inline)) {
-            bf16x8 pn[2][2];
-            float ts[2] = {0.f, 0.f};
+        auto p_block = [&](const f32x16 (&s)[QB], int kb) __attribute__((always_inline)) {
+            bf16x8 pn[QB][2];
+            float ts[QB];
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb)
+            for (int qb = 0; qb < QB; ++qb) ts[qb] = 0.f;
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
                 for (int hf = 0; hf < 2; ++hf) {
                     u32x4 w;
@@ -207,16 +224,18 @@ void fmha_short_kernel(const FmhaParams p) {
                     }
                     pn[qb][hf] = __builtin_bit_cast(bf16x8, w);
                 }
-            over |= !(ts[0] <= kRebaseBound) || !(ts[1] <= kRebaseBound);
-            l[0] += ts[0];
-            l[1] += ts[1];
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                over |= !(ts[qb] <= kRebaseBound);
+                l[qb] += ts[qb];
+            }
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
                 for (int db = 0; db < NDB; ++db) {
                     const bf16x8 a = v_opnd(2 * kb + hf, db);
-                    o[db][0] = mfma32(a, pn[0][hf], o[db][0]);
-                    o[db][1] = mfma32(a, pn[1][hf], o[db][1]);
+#pragma unroll
+                    for (int qb = 0; qb < QB; ++qb) o[db][qb] = mfma32(a, pn[qb][hf], o[db][qb]);
                 }
         };
         // Pass 0: the first block's row max is the reference for all blocks (softmax is
@@ -224,18 +243,22 @@ void fmha_short_kernel(const FmhaParams p) {
         // row outgrew it (pathological inputs): the true row max first, every weight <= 1.
         for (int pass = 0; pass < 2; ++pass) {
             if (pass == 1) {
-                float mt[2] = {-INFINITY, -INFINITY};
-                negm[0] = negm[1] = splat16(0.f);
+                float mt[QB];
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    mt[qb] = -INFINITY;
+                    negm[qb] = splat16(0.f);
+                }
                 for (int kb = 0; kb < nkb; ++kb) {
-                    f32x16 s[2];
+                    f32x16 s[QB];
                     s_block(kb, s);
 #pragma unroll
-                    for (int qb = 0; qb < 2; ++qb)
+                    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
                         for (int i = 0; i < 16; ++i) mt[qb] = fmaxf(mt[qb], s[qb][i]);
                 }
 #pragma unroll
-                for (int qb = 0; qb < 2; ++qb) {
+                for (int qb = 0; qb < QB; ++qb) {
                     negm[qb] = splat16(-fmaxf(mt[qb], xlane32(mt[qb])));
 #pragma unroll
                     for (int db = 0; db < NDB; ++db) o[db][qb] = splat16(0.f);
@@ -244,11 +267,11 @@ void fmha_short_kernel(const FmhaParams p) {
                 over = false;
             }
             for (int kb = 0; kb < nkb; ++kb) {
-                f32x16 s[2];
+                f32x16 s[QB];
                 s_block(kb, s);
                 if (pass == 0 && kb == 0) {
 #pragma unroll
-                    for (int qb = 0; qb < 2; ++qb) {
+                    for (int qb = 0; qb < QB; ++qb) {
                         float mx = s[qb][0];
 #pragma unroll
                         for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[qb][i]);
@@ -263,27 +286,28 @@ void fmha_short_kernel(const FmhaParams p) {
         }
 
         // ---- epilogue: O * gate / l, staged in LDS, whole 16-byte units stored ---------
-        const int q0 = j * QW;
-        const float lt0 = l[0] + xlane32(l[0]), lt1 = l[1] + xlane32(l[1]);
-        const float inv0 = gate_factor(p.gate, p.g_bs, p.g_rs, p.g_hs, b, min(q0 + r, p.Lq - 1), h) / lt0;
-        const float inv1 = gate_factor(p.gate, p.g_bs, p.g_rs, p.g_hs, b, min(q0 + 32 + r, p.Lq - 1), h) / lt1;
+        const int q0 = j * SQW;
+        float inv[QB];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+        for (int qb = 0; qb < QB; ++qb)
+            inv[qb] = gate_factor(p.gate, p.g_bs, p.g_rs, p.g_hs, b, min(q0 + 32 * qb + r, p.Lq - 1), h) /
+                      (l[qb] + xlane32(l[qb]));
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
 #pragma unroll
                 for (int i4 = 0; i4 < 4; ++i4) {
-                    const float inv = qb ? inv1 : inv0;
                     const int row = 32 * qb + r;
                     u32x2 w;
-                    w[0] = pack_bf2(o[db][qb][4 * i4 + 0] * inv, o[db][qb][4 * i4 + 1] * inv);
-                    w[1] = pack_bf2(o[db][qb][4 * i4 + 2] * inv, o[db][qb][4 * i4 + 3] * inv);
+                    w[0] = pack_bf2(o[db][qb][4 * i4 + 0] * inv[qb], o[db][qb][4 * i4 + 1] * inv[qb]);
+                    w[1] = pack_bf2(o[db][qb][4 * i4 + 2] * inv[qb], o[db][qb][4 * i4 + 3] * inv[qb]);
                     *(u32x2 *)(Os + row * D + 8 * swz<KU>(row, 4 * db + i4) + 4 * g) = w;
                 }
         // The wave's LDS operations complete in order: the reads below see the writes above,
         // and the next block's writes come after these reads.
 #pragma unroll
-        for (int it = 0; it < QW * KU / 64; ++it) {
+        for (int it = 0; it < SQW * KU / 64; ++it) {
             const int u = lane + 64 * it;
             const int row = u / KU, c = u % KU;
             const int q = q0 + row;
@@ -297,18 +321,15 @@ void fmha_short_kernel(const FmhaParams p) {
 }  // namespace
 
 int launch_fmha_short(const FmhaParams &p, int D, void *stream) {
-    const dim3 grid(p.grid), block(NT);
+    const dim3 grid(p.grid), block(512);
     hipStream_t st = (hipStream_t)stream;
     const bool rope = p.q_cos != nullptr;
-    if (D == 128) {
-        // D = 128 with RoPE does not fit the register file with the next block in flight; the
-        // host plan sends such calls to the other kernels.
-        if (rope) return (int)hipErrorInvalidValue;
-        hipLaunchKernelGGL((fmha_short_kernel<128, false>), grid, block, 0, st, p);
-    } else {
-        if (rope) hipLaunchKernelGGL((fmha_short_kernel<64, true>), grid, block, 0, st, p);
-        else hipLaunchKernelGGL((fmha_short_kernel<64, false>), grid, block, 0, st, p);
-    }
+    // D = 128 with RoPE does not fit the register file with a block in flight; the host plan
+    // sends such calls to the other kernels.
+    if (D == 128 && rope) return (int)hipErrorInvalidValue;
+    if (D == 128) hipLaunchKernelGGL((fmha_short_kernel<128, false>), grid, block, 0, st, p);
+    else if (rope) hipLaunchKernelGGL((fmha_short_kernel<64, true>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((fmha_short_kernel<64, false>), grid, block, 0, st, p);
     return (int)hipGetLastError();
 }
 

@@ -208,13 +208,13 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
         pl->shortk = true;
         pl->k_prologue = k_work;
         pl->kprep_rows = pl->kmax;
-        // about four waves' worth of query blocks per SIMD at once: B*H*G workgroups of four
-        // waves over 256 CUs, no more groups than a head's query blocks fill
+        // Eight waves of 32-query blocks per workgroup (two per SIMD); one workgroup per CU:
+        // B*H*G workgroups over 256 CUs, no more groups than a head's query blocks fill.
+        const int waves = 8, qw = 32;
         const int64_t heads = (int64_t)B * H;
-        const int64_t qb64 = (a->Lq + ltx::kQueriesPerWave - 1) / ltx::kQueriesPerWave;
-        int64_t G = (kConcurrentGroups * ltx::kWavesPerGroup + heads * ltx::kWavesPerGroup - 1) /
-                    (heads * ltx::kWavesPerGroup);
-        G = std::max<int64_t>(1, std::min(G, (qb64 + ltx::kWavesPerGroup - 1) / ltx::kWavesPerGroup));
+        const int64_t nqb = (a->Lq + qw - 1) / qw;
+        int64_t G = (kConcurrentGroups + heads - 1) / heads;
+        G = std::max<int64_t>(1, std::min(G, (nqb + waves - 1) / waves));
         pl->short_groups = (int)G;
         pl->n_items = pl->n_full = heads * G;
         pl->grid = heads * G;
