@@ -318,6 +318,37 @@ def bench_connector(device, steps, warmup, hip):
     return res
 
 
+def bench_gemma(device, steps, warmup):
+    """The Gemma-4 text encoder's attention at its 1024 tokens (GemmaTextEncoder.swift:158-239):
+    a sliding layer (D 256, 16 query heads over 8 KV heads, window 1024) and a full layer
+    (D 512, one KV head shared as V, partial RoPE), one prompt, no padding. ms per call (the
+    per-head prologue and the attention), and TFLOP/s over the causal pairs (4 * pairs * D *
+    Hq)."""
+    import torch
+
+    import ltx_attn as L
+
+    T, res = 1024, {}
+    for name, spec, seed in (("sliding", L.GEMMA_SLIDING, 500), ("full", L.GEMMA_FULL, 510)):
+        D, Hq, Hkv = spec["head_dim"], spec["q_heads"], spec["kv_heads"]
+        q = _randn((1, T, Hq * D), 0x5EED + seed, device)
+        k = _randn((1, T, Hkv * D), 0x5EED + seed + 1, device)
+        v = k if spec["shares_kv"] else _randn((1, T, Hkv * D), 0x5EED + seed + 2, device)
+        wq = _randn((D,), 0x5EED + seed + 3, device, 1.03, 0.02)
+        wk = _randn((D,), 0x5EED + seed + 4, device, 0.12 if D == 256 else 0.06, 0.01)
+        cos, sin = (torch.from_numpy(t).to(device) for t in
+                    L.gemma_rope_tables(T, D, spec["theta"], spec["partial"], spec["proportional"]))
+        out = torch.empty((1, T, Hq * D), dtype=torch.float32, device=device)
+        ws = torch.empty(64 << 20, dtype=torch.uint8, device=device)
+        ms = _time_ms(lambda: L.gemma_attention_fwd(
+            q, k, v, q_heads=Hq, kv_heads=Hkv, q_norm_w=wq, k_norm_w=wk, cos=cos, sin=sin,
+            window=spec["window"], out=out, workspace=ws), steps, warmup)
+        pairs = T * (T + 1) / 2
+        res[f"gemma_{name}_1024_ms"] = round(ms, 4)
+        res[f"gemma_{name}_1024_tflops"] = round(4.0 * pairs * D * Hq / (ms * 1e-3) / 1e12, 1)
+    return res
+
+
 def bench_c5(device, steps, warmup, hip):
     """The six attentions of one DiT block at 1280x768x121, B=2 (CFG), in block order
     (Sources/LTXModules/DiTBlock.swift:343-438): attn1, audio_attn1, attn2, audio_attn2,
@@ -611,6 +642,7 @@ def main():
                                                  for k, v in short.items()),
               file=sys.stderr, flush=True)
         conn = bench_connector(device, 10, 3, hip)
+        gemma = bench_gemma(device, 10, 3)
         c5 = bench_c5(device, 5, 2, hip)
         print(f"# c5: {c5['ms_per_block']:.3f} ms per block attention set", file=sys.stderr,
               flush=True)
@@ -631,6 +663,7 @@ def main():
             "video_self_3120_call_tflops": round(c1["tflops"], 2),
             "short_key_calls": short,
             "connector_attn_1024": conn,
+            "gemma_text_encoder_attn": gemma,
             "dit_block_attn_ms": round(c5["ms_per_block"], 4),
             "dit_block_attn_tflops": round(c5["tflops"], 2),
             "dit_block_attn_kernel_ms": c5["kernel_ms"],

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define LTX_ATTN_ABI_VERSION 4
+#define LTX_ATTN_ABI_VERSION 5
 
 /* Status codes. The reference throws `DiTAttention.Failure` for structural errors
  * (DiTAttention.swift:107-121); a Swift wrapper maps these onto thrown errors. */
@@ -241,6 +241,54 @@ ltx_attn_status ltx_rope_tables_device(const float *positions, int32_t n_pos, in
                                        int32_t inner, const int32_t *max_pos, int32_t heads,
                                        double theta, uint16_t *cos_out, uint16_t *sin_out,
                                        void *stream);
+
+/* ----------------------------------------------------------------------------------------
+ * Gemma-4 text-encoder attention (Sources/LTXModules/GemmaTextEncoder.swift:158-239 with the
+ * mask of :288-321), from the q/k/v projections to the merged output before o_proj.
+ * Replaces, per layer: q = rope(q_norm(q_proj)), k = rope(k_norm(k_proj)), v = v_norm(v_proj
+ * or the PRE-norm k_proj on the K-shares-V layers), the KV-head repeat (GQA), and the SDPA
+ * with scale 1.0 under the causal / sliding-window / padding mask (rows with no allowed key
+ * attend to every key, :306-319). Norms per head over D: x * pow(mean(x^2) + eps, -0.5) *
+ * weight (no 1 + weight), fp32; v's norm has no weight. The sliding layers are D = 256,
+ * 16 query heads over 8 KV heads, window 1024, theta 1e4; the full layers D = 512, 16 query
+ * heads over 1 KV head with V from K, partial ("proportional") rotation, theta 1e6.
+ * -------------------------------------------------------------------------------------- */
+typedef struct ltx_gemma_attn_args {
+    int32_t B, T;                 /* batch rows (prompts), tokens (queries = keys)             */
+    int32_t Hq, Hkv, D;           /* D in {256, 512}; Hq a multiple of Hkv                     */
+    const void *q;                /* bf16 [B, T, Hq*D] (q_proj output), element strides below  */
+    const void *k;                /* bf16 [B, T, Hkv*D] (k_proj output)                        */
+    const void *v;                /* bf16 [B, T, Hkv*D] (v_proj output), or == k: V = v_norm of */
+                                  /* the pre-norm K projection (the K-shares-V layers)          */
+    int64_t q_bs, q_rs, k_bs, k_rs, v_bs, v_rs;
+    const void *q_norm_w, *k_norm_w;  /* bf16 [D]                                              */
+    float eps;                    /* rms_norm_eps (1e-6)                                       */
+    const float *cos, *sin;       /* fp32 [T, D/2], positions 0..T-1 (ltx_gemma_rope_tables)   */
+    int32_t window;               /* sliding window (keys q - window < k <= q), 0 = causal only */
+    const int32_t *first_valid;   /* HOST [B]: keys < first_valid[b] are left padding, or NULL */
+    float scale;                  /* logit scale: GemmaAttentionSpec.attentionScaling = 1.0     */
+    float *out;                   /* fp32 [B, T, Hq*D] (the reference's explicit path returns   */
+                                  /* fp32: its q is promoted by the fp32 RoPE tables, :224-239) */
+    int64_t o_bs, o_rs;           /* element strides                                           */
+    void *workspace;              /* device, 256-byte aligned, >= ltx_gemma_attn_workspace_bytes */
+    size_t workspace_bytes;
+} ltx_gemma_attn_args;
+
+/* Workspace for the prepared q (two bf16 parts), k (normed, rotated) and v^T; 0 on bad args. */
+size_t ltx_gemma_attn_workspace_bytes(const ltx_gemma_attn_args *a);
+
+/* Validate, then run asynchronously on `stream`: the per-head prologue, then the attention.
+ * Same status convention as ltx_attn_fwd; nothing is launched on an error. */
+ltx_attn_status ltx_gemma_attn_fwd(const ltx_gemma_attn_args *a, void *stream);
+
+/* GemmaAttentionSpec.inverseFrequencies (GemmaAttentionSpec.swift:88-121) in double, then the
+ * tables of GemmaTextEncoder.positionEmbeddings (:135-145): fp32 angle = position * float(inv),
+ * fp32 cos/sin, [tokens][head_dim/2]. `proportional` != 0: the denominator is the full head dim
+ * and only partial_factor*head_dim/2 frequencies are non-zero; else the denominator is the
+ * rotated width head_dim*partial_factor. Returns 0 or -1 on bad arguments. */
+int32_t ltx_gemma_rope_tables(int32_t tokens, int32_t head_dim, double theta,
+                              double partial_factor, int32_t proportional, float *cos_out,
+                              float *sin_out);
 
 #ifdef __cplusplus
 }

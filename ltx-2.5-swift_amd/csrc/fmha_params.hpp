@@ -124,6 +124,28 @@ struct RstdParams {
     float *rstd;
 };
 
+// Gemma-4 text-encoder attention (gemma_attn.hip). The prologue normalises (per head over D),
+// rotates and scales q and k into q' [B][Hq][T][D], k' [B][Hkv][T][D], and normalises v into
+// v' stored transposed, [B][Hkv][D][T].
+struct GemmaPrepParams {
+    const void *q, *k, *v;           // bf16 projections, element strides below
+    int64_t q_bs, q_rs, k_bs, k_rs, v_bs, v_rs;
+    int32_t B, T, Hq, Hkv;
+    const void *q_w, *k_w;           // bf16 [D]
+    float eps;
+    float q_factor;                  // scale * log2(e), folded into q'
+    const float *cos, *sin;          // fp32 [T][D/2]
+    void *qp, *qp_lo, *kp, *vt;      // bf16 outputs (workspace); q' as hi + lo parts
+};
+struct GemmaAttnParams {
+    const void *qp, *qp_lo, *kp, *vt;
+    float *out;                      // fp32 [B][T][Hq*D], element strides below
+    int64_t o_bs, o_rs;
+    int32_t B, T, Hq, Hkv;
+    int32_t window;                  // 0: causal only
+    int32_t first_valid[kMaxBatch];  // keys below are left padding
+};
+
 // Launchers (fmha_fwd.hip). Return the hipError_t of the launch as int.
 // Attention kernels:
 //   kRegPlain  K and V staged through registers (V transposed on the way into LDS)
@@ -139,5 +161,7 @@ int launch_combine(const CombineParams &p, int D, void *stream);
 int launch_passthrough(const PassParams &p, int D, void *stream);
 int launch_rstd(const RstdParams &p, void *stream);
 int launch_linear(const LinearParams &p, void *stream);           // linear_gemm.hip
+int launch_gemma_prep(const GemmaPrepParams &p, int D, void *stream);   // gemma_attn.hip
+int launch_gemma_attn(const GemmaAttnParams &p, int D, void *stream);
 
 }  // namespace ltx

@@ -301,6 +301,63 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
     return LTX_ATTN_OK;
 }
 
+// Gemma-4 text-encoder attention: validation and workspace layout.
+
+struct GemmaPlan {
+    size_t off_q = 0, off_qlo = 0, off_k = 0, off_v = 0, bytes = 0;
+};
+
+ltx_attn_status gemma_plan(const ltx_gemma_attn_args *a, GemmaPlan *pl) {
+    g_err[0] = 0;
+    if (!a) return fail(LTX_ATTN_EINVAL, "args is NULL");
+    if (a->B < 1 || a->T < 4 || a->Hq < 1 || a->Hkv < 1)
+        return fail(LTX_ATTN_EINVAL, "B, Hq, Hkv must be >= 1 and T >= 4 (got %d, %d, %d, %d)",
+                    a->B, a->Hq, a->Hkv, a->T);
+    if (a->D != 256 && a->D != 512)
+        return fail(LTX_ATTN_EUNSUPPORTED, "head dim %d is not 256 or 512", a->D);
+    if (a->T % 4)
+        return fail(LTX_ATTN_EUNSUPPORTED, "T (%d) must be a multiple of 4", a->T);
+    if (a->Hq % a->Hkv)
+        return fail(LTX_ATTN_EINVAL, "Hq (%d) is not a multiple of Hkv (%d)", a->Hq, a->Hkv);
+    if (a->B > ltx::kMaxBatch)
+        return fail(LTX_ATTN_EUNSUPPORTED, "batch %d above %d", a->B, ltx::kMaxBatch);
+    const int64_t D = a->D;
+    struct T3 { const char *n; const void *p; int64_t bs, rs; int64_t H; };
+    for (const T3 &t : {T3{"q", a->q, a->q_bs, a->q_rs, a->Hq}, T3{"k", a->k, a->k_bs, a->k_rs, a->Hkv},
+                        T3{"v", a->v, a->v_bs, a->v_rs, a->Hkv}}) {
+        if (!t.p) return fail(LTX_ATTN_EINVAL, "%s is NULL", t.n);
+        if (!aligned16(t.p)) return fail(LTX_ATTN_EINVAL, "%s is not 16-byte aligned", t.n);
+        if (t.bs < 0 || t.rs < t.H * D || (t.bs % 8) || (t.rs % 8) || (a->B > 1 && t.bs == 0))
+            return fail(LTX_ATTN_EINVAL, "%s strides (%lld, %lld) must be multiples of 8 with a "
+                        "row of at least %lld elements", t.n, (long long)t.bs, (long long)t.rs,
+                        (long long)(t.H * D));
+    }
+    if (!a->q_norm_w || !a->k_norm_w || !aligned16(a->q_norm_w) || !aligned16(a->k_norm_w))
+        return fail(LTX_ATTN_EINVAL, "q_norm_w and k_norm_w must be given, 16-byte aligned");
+    if (!a->cos || !a->sin || ((uintptr_t)a->cos & 3u) || ((uintptr_t)a->sin & 3u))
+        return fail(LTX_ATTN_EINVAL, "cos and sin tables must be given, 4-byte aligned");
+    if (!(a->eps >= 0.f) || !isfinite(a->eps) || !(a->scale > 0.f) || !isfinite(a->scale))
+        return fail(LTX_ATTN_EINVAL, "eps must be finite and >= 0, scale positive and finite");
+    if (a->window < 0) return fail(LTX_ATTN_EINVAL, "window %d is negative", a->window);
+    if (a->first_valid)
+        for (int b = 0; b < a->B; ++b)
+            if (a->first_valid[b] < 0 || a->first_valid[b] > a->T)
+                return fail(LTX_ATTN_EINVAL, "first_valid[%d] = %d outside [0, %d]", b,
+                            a->first_valid[b], a->T);
+    if (!a->out || !aligned16(a->out) || a->o_rs < a->Hq * D || (a->o_rs % 4) ||
+        a->o_bs < 0 || (a->o_bs % 4) || (a->B > 1 && a->o_bs == 0))
+        return fail(LTX_ATTN_EINVAL, "out must be 16-byte aligned with strides that are "
+                    "multiples of 4 and a row of at least Hq*D");
+    const size_t qn = 2 * (size_t)a->B * a->Hq * a->T * D;
+    const size_t kn = 2 * (size_t)a->B * a->Hkv * a->T * D;
+    pl->off_q = 0;
+    pl->off_qlo = align_up(qn, 256);
+    pl->off_k = pl->off_qlo + align_up(qn, 256);
+    pl->off_v = pl->off_k + align_up(kn, 256);
+    pl->bytes = pl->off_v + align_up(kn, 256);
+    return LTX_ATTN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -486,6 +543,43 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
         if (int e = ltx::launch_combine(cp, D, stream))
             return fail(LTX_ATTN_EHIP, "combine launch: %s", hipGetErrorString((hipError_t)e));
     }
+    return LTX_ATTN_OK;
+}
+
+size_t ltx_gemma_attn_workspace_bytes(const ltx_gemma_attn_args *a) {
+    GemmaPlan pl;
+    return gemma_plan(a, &pl) == LTX_ATTN_OK ? pl.bytes : 0;
+}
+
+ltx_attn_status ltx_gemma_attn_fwd(const ltx_gemma_attn_args *a, void *stream) {
+    GemmaPlan pl;
+    if (ltx_attn_status s = gemma_plan(a, &pl)) return s;
+    if (!a->workspace || a->workspace_bytes < pl.bytes)
+        return fail(LTX_ATTN_EWORKSPACE, "workspace of %zu bytes needed (got %zu at %p)",
+                    pl.bytes, a->workspace_bytes, a->workspace);
+    if ((uintptr_t)a->workspace & 255u)
+        return fail(LTX_ATTN_EINVAL, "workspace must be 256-byte aligned");
+    char *ws = (char *)a->workspace;
+    ltx::GemmaPrepParams pp{};
+    pp.q = a->q; pp.k = a->k; pp.v = a->v;
+    pp.q_bs = a->q_bs; pp.q_rs = a->q_rs; pp.k_bs = a->k_bs; pp.k_rs = a->k_rs;
+    pp.v_bs = a->v_bs; pp.v_rs = a->v_rs;
+    pp.B = a->B; pp.T = a->T; pp.Hq = a->Hq; pp.Hkv = a->Hkv;
+    pp.q_w = a->q_norm_w; pp.k_w = a->k_norm_w;
+    pp.eps = a->eps;
+    pp.q_factor = (float)((double)a->scale * 1.4426950408889634);
+    pp.cos = a->cos; pp.sin = a->sin;
+    pp.qp = ws + pl.off_q; pp.qp_lo = ws + pl.off_qlo; pp.kp = ws + pl.off_k;
+    pp.vt = ws + pl.off_v;
+    if (int e = ltx::launch_gemma_prep(pp, a->D, stream))
+        return fail(LTX_ATTN_EHIP, "gemma prologue launch: %s", hipGetErrorString((hipError_t)e));
+    ltx::GemmaAttnParams ap{};
+    ap.qp = pp.qp; ap.qp_lo = pp.qp_lo; ap.kp = pp.kp; ap.vt = pp.vt;
+    ap.out = a->out; ap.o_bs = a->o_bs; ap.o_rs = a->o_rs;
+    ap.B = a->B; ap.T = a->T; ap.Hq = a->Hq; ap.Hkv = a->Hkv; ap.window = a->window;
+    for (int b = 0; b < a->B; ++b) ap.first_valid[b] = a->first_valid ? a->first_valid[b] : 0;
+    if (int e = ltx::launch_gemma_attn(ap, a->D, stream))
+        return fail(LTX_ATTN_EHIP, "gemma attention launch: %s", hipGetErrorString((hipError_t)e));
     return LTX_ATTN_OK;
 }
 

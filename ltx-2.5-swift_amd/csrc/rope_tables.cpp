@@ -146,4 +146,36 @@ int32_t ltx_rope_tables(const float *positions, int32_t n_pos, int32_t tokens, i
     return 0;
 }
 
+// GemmaAttentionSpec.inverseFrequencies (GemmaAttentionSpec.swift:88-121), in double, then
+// GemmaTextEncoder.positionEmbeddings (GemmaTextEncoder.swift:135-145): the frequencies are
+// narrowed to float, the angle is the float product position * inv, and cos/sin are taken of
+// that float angle in float.
+int32_t ltx_gemma_rope_tables(int32_t tokens, int32_t head_dim, double theta,
+                              double partial_factor, int32_t proportional, float *cos_out,
+                              float *sin_out) {
+    if (tokens < 1 || head_dim < 2 || (head_dim & 1) || !(theta > 0.0) ||
+        !(partial_factor > 0.0 && partial_factor <= 1.0) || !cos_out || !sin_out)
+        return -1;
+    const int32_t half = head_dim / 2;
+    std::vector<double> inv(half, 0.0);
+    if (proportional) {
+        // denominator: the full head dim; int(factor * headDim / 2) real angles
+        const int32_t n = (int32_t)(partial_factor * (double)head_dim / 2.0);
+        for (int32_t i = 0; i < n && i < half; ++i)
+            inv[i] = 1.0 / pow(theta, (double)(2 * i) / (double)head_dim);
+    } else {
+        // denominator: the rotated width; its frequencies, zero beyond
+        const int32_t dim = (int32_t)((double)head_dim * partial_factor);
+        for (int32_t i = 0; i < dim / 2 && i < half; ++i)
+            inv[i] = 1.0 / pow(theta, (double)(2 * i) / (double)dim);
+    }
+    for (int32_t t = 0; t < tokens; ++t)
+        for (int32_t i = 0; i < half; ++i) {
+            const float angle = (float)t * (float)inv[i];
+            cos_out[(int64_t)t * half + i] = cosf(angle);
+            sin_out[(int64_t)t * half + i] = sinf(angle);
+        }
+    return 0;
+}
+
 }  // extern "C"

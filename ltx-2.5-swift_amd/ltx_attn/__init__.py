@@ -83,12 +83,43 @@ class LinearArgs(ctypes.Structure):
 SUMSQ_COLS = 256   # LTX_LINEAR_SUMSQ_COLS: columns of y per partial sum of squares
 
 
+class GemmaArgs(ctypes.Structure):
+    """``ltx_gemma_attn_args`` (field order and types as in include/ltx_attn.h)."""
+
+    _fields_ = [
+        ("B", ctypes.c_int32), ("T", ctypes.c_int32),
+        ("Hq", ctypes.c_int32), ("Hkv", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("q_bs", ctypes.c_int64), ("q_rs", ctypes.c_int64),
+        ("k_bs", ctypes.c_int64), ("k_rs", ctypes.c_int64),
+        ("v_bs", ctypes.c_int64), ("v_rs", ctypes.c_int64),
+        ("q_norm_w", ctypes.c_void_p), ("k_norm_w", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("cos", ctypes.c_void_p), ("sin", ctypes.c_void_p),
+        ("window", ctypes.c_int32),
+        ("first_valid", ctypes.POINTER(ctypes.c_int32)),
+        ("scale", ctypes.c_float),
+        ("out", ctypes.c_void_p),
+        ("o_bs", ctypes.c_int64), ("o_rs", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+# GemmaAttentionSpec.ltx25 (Sources/LTXFoundation/GemmaAttentionSpec.swift:67-71) and the
+# text-encoder topology (Tests/LTXCatalogTests/TextEncoderTopologyTests.swift:53-68)
+GEMMA_SLIDING = dict(head_dim=256, q_heads=16, kv_heads=8, theta=10_000.0, partial=1.0,
+                     proportional=False, window=1024, shares_kv=False)
+GEMMA_FULL = dict(head_dim=512, q_heads=16, kv_heads=1, theta=1_000_000.0, partial=0.25,
+                  proportional=True, window=0, shares_kv=True)
+
+
 EXPORTED_SYMBOLS = (
     "ltx_attn_args_init", "ltx_attn_workspace_bytes", "ltx_attn_validate", "ltx_attn_fwd",
     "ltx_attn_status_string", "ltx_attn_last_error", "ltx_attn_provenance",
     "ltx_attn_abi_version", "ltx_attn_args_size", "ltx_rope_frequency_grid", "ltx_rope_video_positions",
     "ltx_rope_audio_positions", "ltx_rope_tables", "ltx_rope_tables_device",
-    "ltx_linear", "ltx_linear_sumsq_blocks",
+    "ltx_linear", "ltx_linear_sumsq_blocks", "ltx_gemma_attn_workspace_bytes",
+    "ltx_gemma_attn_fwd", "ltx_gemma_rope_tables",
 )
 
 _lib = None
@@ -148,6 +179,14 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ltx_linear.restype = ctypes.c_int
     lib.ltx_linear_sumsq_blocks.argtypes = [ctypes.c_int32]
     lib.ltx_linear_sumsq_blocks.restype = ctypes.c_int32
+    lib.ltx_gemma_attn_workspace_bytes.argtypes = [ctypes.POINTER(GemmaArgs)]
+    lib.ltx_gemma_attn_workspace_bytes.restype = ctypes.c_size_t
+    lib.ltx_gemma_attn_fwd.argtypes = [ctypes.POINTER(GemmaArgs), ctypes.c_void_p]
+    lib.ltx_gemma_attn_fwd.restype = ctypes.c_int
+    lib.ltx_gemma_rope_tables.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_double,
+                                          ctypes.c_double, ctypes.c_int32, ctypes.c_void_p,
+                                          ctypes.c_void_p]
+    lib.ltx_gemma_rope_tables.restype = ctypes.c_int32
     _lib = lib
     return lib
 
@@ -701,3 +740,68 @@ def rotaries(frames: int, height: int, width: int, frame_rate: float = 24.0,
         "videoCross": rope_tables(video[0:1], audio_width, [20], heads, theta),
         "audioCross": rope_tables(audio, audio_width, [20], heads, theta),
     }
+
+
+# --------------------------------------------------------------------------------------
+# Gemma-4 text-encoder attention (GemmaTextEncoder.swift:158-239, mask :288-321)
+# --------------------------------------------------------------------------------------
+
+def gemma_rope_tables(tokens: int, head_dim: int, theta: float, partial: float = 1.0,
+                      proportional: bool = False):
+    """fp32 ``(cos, sin)`` ``[tokens, head_dim/2]`` for positions ``0 .. tokens-1``
+    (GemmaTextEncoder.positionEmbeddings, GemmaTextEncoder.swift:135-145)."""
+    lib = load_library()
+    cos = np.zeros((tokens, head_dim // 2), dtype=np.float32)
+    sin = np.zeros_like(cos)
+    if lib.ltx_gemma_rope_tables(tokens, head_dim, theta, partial, int(bool(proportional)),
+                                 cos.ctypes.data, sin.ctypes.data) != 0:
+        raise Failure(EINVAL, "bad Gemma rotary-table arguments")
+    return cos, sin
+
+
+def gemma_attention_fwd(q, k, v, *, q_heads: int, kv_heads: int, q_norm_w, k_norm_w, cos, sin,
+                        window: int = 0, first_valid=None, scale: float = 1.0, eps: float = 1e-6,
+                        out=None, workspace=None, stream=None):
+    """One Gemma-4 attention from the projections: ``q`` ``[B, T, Hq*D]``, ``k``/``v``
+    ``[B, T, Hkv*D]`` bf16 (pass ``v = k`` on the K-shares-V layers), norm weights ``[D]``,
+    ``cos``/``sin`` fp32 device tensors ``[T, D/2]``; ``first_valid`` per batch row (keys
+    before it are left padding). Returns ``out`` ``[B, T, Hq*D]`` fp32 (the dtype of the
+    reference's explicit path)."""
+    import torch
+
+    lib = load_library()
+    B, T, qw = q.shape
+    D = qw // q_heads
+    for t in (q, k, v):
+        if t.stride(-1) != 1:
+            raise Failure(EINVAL, "projection rows must be contiguous")
+    if out is None:
+        out = torch.empty((B, T, q_heads * D), dtype=torch.float32, device=q.device)
+    a = GemmaArgs()
+    a.B, a.T, a.Hq, a.Hkv, a.D = B, T, q_heads, kv_heads, D
+    a.q, a.k, a.v = _ptr(q), _ptr(k), _ptr(v)
+    a.q_bs, a.q_rs = q.stride(0), q.stride(1)
+    a.k_bs, a.k_rs = k.stride(0), k.stride(1)
+    a.v_bs, a.v_rs = v.stride(0), v.stride(1)
+    a.q_norm_w, a.k_norm_w = _ptr(q_norm_w), _ptr(k_norm_w)
+    a.eps = eps
+    a.cos, a.sin = _ptr(cos), _ptr(sin)
+    a.window = window
+    fv = None
+    if first_valid is not None:
+        fv = (ctypes.c_int32 * B)(*[int(x) for x in first_valid])
+        a.first_valid = ctypes.cast(fv, ctypes.POINTER(ctypes.c_int32))
+    a.scale = scale
+    a.out = _ptr(out)
+    a.o_bs, a.o_rs = out.stride(0), out.stride(1)
+    need = lib.ltx_gemma_attn_workspace_bytes(ctypes.byref(a))
+    if need == 0:
+        _check(lib.ltx_gemma_attn_fwd(ctypes.byref(a), None))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    a.workspace, a.workspace_bytes = _ptr(workspace), workspace.numel()
+    if stream is None:
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+    _check(lib.ltx_gemma_attn_fwd(ctypes.byref(a), ctypes.c_void_p(stream)))
+    out._ltx_keepalive = (workspace, fv)  # noqa: SLF001 -- until the stream has run
+    return out

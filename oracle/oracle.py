@@ -31,6 +31,21 @@ This is a numpy restatement of the reference's arithmetic:
                         ``:486-520`` (``videoPositions``), ``:606-619`` (``audioPositions``),
                         ``:641-678`` (``rotary``), ``:698-738`` (``rotaries``).
 
+Gemma-4 text-encoder attention (``Sources/LTXModules/GemmaTextEncoder.swift``):
+
+* ``gemma_inverse_frequencies`` -- ``Sources/LTXFoundation/GemmaAttentionSpec.swift:88-121``
+                        (``default`` divides by the rotated width, ``proportional`` by the full
+                        head dim and zero-pads the non-rotating tail).
+* ``gemma_rope_tables`` -- ``GemmaTextEncoder.swift:135-145``: fp32 angles ``position *
+                        inv_freq``, fp32 cos/sin, per token, shared by the heads.
+* ``gemma_attention``   -- ``GemmaTextEncoder.swift:158-239`` (per-head q/k RMS norm with
+                        ``pow(mean + eps, -0.5)`` and the weight, no ``1 +``; ``rotate_half``
+                        RoPE; V normed by a weightless norm and never rotated, taken from the
+                        pre-norm K projection on the K-shares-V layers; GQA by repeating KV
+                        heads; scale 1.0; the explicit fp32 path) with the mask of
+                        ``:288-321`` (causal, sliding window, key padding, fully-masked rows
+                        un-masked).
+
 Two arithmetic modes:
 
 * ``mode="exact"``     float64 everywhere from the bf16 inputs (norm, RoPE and SDPA in
@@ -467,6 +482,107 @@ def rotaries(frames: int, height: int, width: int, frame_rate: float = 24.0,
 # --------------------------------------------------------------------------------------
 # Comparison (BenchComparison, Sources/ltx/Bench.swift:508-536)
 # --------------------------------------------------------------------------------------
+
+# ---------------------------------------------------------------------------------------
+# Gemma-4 text-encoder attention
+# ---------------------------------------------------------------------------------------
+
+def gemma_inverse_frequencies(head_dim: int, theta: float, partial_factor: float,
+                              rope_type: str) -> np.ndarray:
+    """``GemmaAttentionSpec.inverseFrequencies`` (GemmaAttentionSpec.swift:88-121), float64,
+    length ``head_dim / 2``."""
+    half = head_dim // 2
+    out = np.zeros(half, dtype=np.float64)
+    if rope_type == "proportional":
+        n = int(partial_factor * head_dim / 2.0)
+        for i in range(min(n, half)):
+            out[i] = 1.0 / theta ** (2.0 * i / head_dim)
+        return out
+    dim = int(head_dim * partial_factor)
+    res = np.zeros(dim // 2, dtype=np.float64)
+    for i in range(dim // 2):
+        res[i] = 1.0 / theta ** (2.0 * i / dim)
+    return res
+
+
+def gemma_rope_tables(tokens: int, inv_freq: np.ndarray):
+    """fp32 ``cos``, ``sin`` ``[tokens, head_dim/2]`` (GemmaTextEncoder.swift:135-145): the
+    frequencies narrowed to fp32, fp32 angles ``position * inv``, fp32 cos/sin (the table is
+    duplicated over the two halves of a head, which ``rotate_half`` pairs)."""
+    inv = np.asarray(inv_freq, dtype=np.float32)
+    pos = np.arange(tokens, dtype=np.float32)[:, None]
+    ang = (pos * inv[None, :]).astype(np.float32)
+    return (np.cos(ang.astype(np.float64)).astype(np.float32),
+            np.sin(ang.astype(np.float64)).astype(np.float32))
+
+
+def gemma_mask(tokens: int, window: int = 0, first_valid: int = 0) -> np.ndarray:
+    """Allowed (query, key) pairs (GemmaTextEncoder.swift:288-321): causal, keys within the
+    sliding window when one is set, keys before ``first_valid`` (left padding) never; rows
+    left with no allowed key are un-masked entirely."""
+    rows = np.arange(tokens)[:, None]
+    cols = np.arange(tokens)[None, :]
+    allowed = cols <= rows
+    if window > 0:
+        allowed &= (rows - cols) < window
+    allowed &= cols >= first_valid
+    empty = ~allowed.any(axis=1, keepdims=True)
+    return allowed | empty
+
+
+def gemma_attention(q_bits, k_bits, v_bits, q_heads: int, kv_heads: int, q_norm_w, k_norm_w,
+                    cos, sin, *, eps: float = 1e-6, window: int = 0, first_valid=None,
+                    scale: float = 1.0, mode: str = "exact") -> np.ndarray:
+    """One Gemma-4 attention from its projections to the merged output before ``o_proj``
+    (GemmaTextEncoder.swift:158-239). ``q_bits`` ``[B, T, Hq*D]``, ``k_bits``/``v_bits``
+    ``[B, T, Hkv*D]`` bf16 bits (``v_bits`` is ``k_bits`` on the K-shares-V layers: V is
+    the weightless norm of the PRE-norm K projection); norm weights ``[D]`` bits; ``cos``,
+    ``sin`` fp32 ``[T, D/2]``; ``first_valid`` per batch row (left padding). Returns float64
+    ``[B, T, Hq*D]``.
+
+    ``mode="exact"``: float64 throughout. ``mode="reference"``: the norms round to bf16 (the
+    reference casts back to the input dtype), RoPE in fp32 (bf16 x fp32 tables promote), and
+    the explicit path's fp32 logits/softmax/P.V."""
+    B, T, _ = q_bits.shape
+    D = q_bits.shape[2] // q_heads
+    rep = q_heads // kv_heads
+
+    def heads(bits, h):
+        return bf16_bits_to_f32(bits).astype(np.float64).reshape(B, T, h, D)
+
+    def norm(x, w):
+        ms = (x * x).mean(axis=-1, keepdims=True)
+        y = x * (ms + eps) ** -0.5
+        if w is not None:
+            y = y * bf16_bits_to_f32(w).astype(np.float64)
+        return round_bf16(y).astype(np.float64) if mode == "reference" else y
+
+    def rope(x):
+        c = np.asarray(cos, dtype=np.float64)[None, :, None, :]
+        s_ = np.asarray(sin, dtype=np.float64)[None, :, None, :]
+        x1, x2 = x[..., : D // 2], x[..., D // 2:]
+        return np.concatenate([x1 * c - x2 * s_, x2 * c + x1 * s_], axis=-1)
+
+    q = rope(norm(heads(q_bits, q_heads), q_norm_w))
+    kp = heads(k_bits, kv_heads)
+    k = rope(norm(kp, k_norm_w))
+    v = norm(heads(v_bits, kv_heads), None)
+    if mode == "reference":
+        q, k = q.astype(np.float32).astype(np.float64), k.astype(np.float32).astype(np.float64)
+    out = np.zeros((B, T, q_heads, D), dtype=np.float64)
+    fv = [0] * B if first_valid is None else list(first_valid)
+    for b in range(B):
+        allowed = gemma_mask(T, window, fv[b])
+        for h in range(q_heads):
+            kh = h // rep
+            logits = (q[b, :, h, :] @ k[b, :, kh, :].T) * scale
+            logits = np.where(allowed, logits, -np.inf)
+            logits -= logits.max(axis=1, keepdims=True)
+            p = np.exp(logits)
+            p /= p.sum(axis=1, keepdims=True)
+            out[b, :, h, :] = p @ v[b, :, kh, :]
+    return out.reshape(B, T, q_heads * D)
+
 
 def compare(candidate, reference) -> dict:
     """relRMS = sqrt(sum (a-b)^2 / sum b^2), maxAbs, bit-identical fraction (on bf16)."""

@@ -23,7 +23,7 @@ GOLDEN = os.path.join(ROOT, "tests", "golden")
 def _declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ltx_(?:attn_|rope_|linear)\w*)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(ltx_(?:attn_|rope_|linear|gemma_)\w*)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layout_and_version():
     lib = L.load_library()
     assert lib.ltx_attn_args_size() == ctypes.sizeof(L.Args)
-    assert lib.ltx_attn_abi_version() == 4
+    assert lib.ltx_attn_abi_version() == 5
     assert "gfx950" in L.provenance()
     for s in range(5):
         assert lib.ltx_attn_status_string(s)
@@ -459,3 +459,58 @@ def test_connector_rope_tables():
         for got, want in ((cos, want_c), (sin, want_s)):
             g = O.bf16_bits_to_f32(got).astype(np.float64)
             assert np.all(np.abs(g - want) <= 2.0 ** -7 * np.abs(want) + 1e-7)
+
+
+def test_gemma_rope_tables_match_oracle():
+    """ltx_gemma_rope_tables against the oracle (GemmaTextEncoder.swift:135-145): both the
+    sliding (default, theta 1e4, D 256) and full (proportional 0.25, theta 1e6, D 512) kinds;
+    float cos/sin of the same float angle, within one float step of the correctly rounded
+    value; the zero-frequency tail is exactly cos 1, sin 0."""
+    for D, theta, part, prop, kind in ((256, 1e4, 1.0, False, "default"),
+                                       (512, 1e6, 0.25, True, "proportional")):
+        cos, sin = L.gemma_rope_tables(1024, D, theta, part, prop)
+        oc, os_ = O.gemma_rope_tables(1024, O.gemma_inverse_frequencies(D, theta, part, kind))
+        assert np.all(np.abs(cos - oc) <= 2.0 ** -23 * np.abs(oc) + 2.0 ** -30)
+        assert np.all(np.abs(sin - os_) <= 2.0 ** -23 * np.abs(os_) + 2.0 ** -30)
+        if prop:
+            assert np.all(cos[:, 64:] == 1.0) and np.all(sin[:, 64:] == 0.0)
+
+
+def test_gemma_attention_rejects_bad_arguments():
+    lib = L.load_library()
+
+    def args(**kw):
+        a = L.GemmaArgs()
+        a.B, a.T, a.Hq, a.Hkv, a.D = 1, 1024, 16, 8, 256
+        a.q = a.k = a.v = FAKE
+        a.q_bs = 1024 * 4096
+        a.q_rs = 4096
+        a.k_bs = a.v_bs = 1024 * 2048
+        a.k_rs = a.v_rs = 2048
+        a.q_norm_w = a.k_norm_w = FAKE
+        a.eps, a.scale = 1e-6, 1.0
+        a.cos = a.sin = FAKE
+        a.window = 1024
+        a.out = FAKE
+        a.o_bs, a.o_rs = 1024 * 4096, 4096
+        for n, val in kw.items():
+            setattr(a, n, val)
+        return a
+
+    def status(a):
+        st = lib.ltx_gemma_attn_fwd(ctypes.byref(a), None)
+        return st, lib.ltx_attn_last_error().decode()
+
+    a = args()
+    need = lib.ltx_gemma_attn_workspace_bytes(ctypes.byref(a))
+    assert need == 2 * 1024 * 256 * (2 * 16 + 8 + 8)      # q' (hi, lo), k', v'^T
+    assert status(a)[0] == L.EWORKSPACE
+    assert status(args(D=128))[0] == L.EUNSUPPORTED
+    assert status(args(Hkv=3))[0] == L.EINVAL
+    assert status(args(T=1022))[0] == L.EUNSUPPORTED
+    assert status(args(window=-1))[0] == L.EINVAL
+    assert status(args(cos=None))[0] == L.EINVAL
+    assert status(args(q_rs=2048))[0] == L.EINVAL        # row narrower than Hq*D
+    fv = (ctypes.c_int32 * 1)(1025)
+    st, msg = status(args(first_valid=ctypes.cast(fv, ctypes.POINTER(ctypes.c_int32))))
+    assert st == L.EINVAL and "first_valid" in msg

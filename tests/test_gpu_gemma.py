@@ -1,0 +1,84 @@
+"""GPU parity of the Gemma-4 text-encoder attention (``ltx_gemma_attn_fwd``) against the
+oracle's restatement of GemmaTextEncoder.swift:158-239 with the mask of :288-321.
+
+Tolerance (the target's): relative RMS error <= 5e-3 and max-abs <= 2e-2 on the outputs
+(fp32 here, the dtype of the reference's explicit path) against the float64 oracle of the same
+inputs; in addition the kernel may be at most 1.25x as far from the truth as the reference's
+own arithmetic (``mode="reference"``: bf16 norms, fp32 RoPE and softmax), with a 2.5e-3
+floor.
+"""
+
+import numpy as np
+import pytest
+
+import ltx_attn as L
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _dev(bits, device):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(device).view(
+        torch.bfloat16)
+
+
+def _run(device, case):
+    import torch
+
+    B, T, kind, fv, seed = case["B"], case["T"], case["kind"], case["fv"], case["seed"]
+    spec = dict(L.GEMMA_SLIDING if kind == "sliding" else L.GEMMA_FULL)
+    if "window" in case:
+        spec["window"] = case["window"]
+    D, Hq, Hkv = spec["head_dim"], spec["q_heads"], spec["kv_heads"]
+    q = O.randn_bf16_bits((B, T, Hq * D), seed)
+    k = O.randn_bf16_bits((B, T, Hkv * D), seed + 1)
+    v = k if spec["shares_kv"] else O.randn_bf16_bits((B, T, Hkv * D), seed + 2)
+    # weights at the checkpoint's magnitudes: q_norm ~1.03, k_norm ~0.12 (D 256) / ~0.06 (D 512)
+    wq = O.randn_bf16_bits((D,), seed + 3, mean=1.03, std=0.02)
+    wk = O.randn_bf16_bits((D,), seed + 4, mean=0.12 if D == 256 else 0.06, std=0.01)
+    cos, sin = L.gemma_rope_tables(T, D, spec["theta"], spec["partial"], spec["proportional"])
+    tq, tk = _dev(q, device), _dev(k, device)
+    tv = tk if spec["shares_kv"] else _dev(v, device)
+    out = L.gemma_attention_fwd(tq, tk, tv, q_heads=Hq, kv_heads=Hkv,
+                                q_norm_w=_dev(wq, device), k_norm_w=_dev(wk, device),
+                                cos=torch.from_numpy(cos).to(device),
+                                sin=torch.from_numpy(sin).to(device),
+                                window=spec["window"], first_valid=fv)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    kw = dict(window=spec["window"], first_valid=fv)
+    truth = O.gemma_attention(q, k, v, Hq, Hkv, wq, wk, cos, sin, mode="exact", **kw)
+    ref = O.gemma_attention(q, k, v, Hq, Hkv, wq, wk, cos, sin, mode="reference", **kw)
+    return got, truth, ref
+
+
+CASES = {
+    # the layers at the encoder's 1024 tokens: 94 real tokens left-padded to 1024, and none
+    "sliding_1024_pad930": dict(B=1, T=1024, kind="sliding", fv=[930], seed=0x5EED + 400),
+    "full_1024_pad930": dict(B=1, T=1024, kind="full", fv=[930], seed=0x5EED + 410),
+    "sliding_1024_nopad": dict(B=1, T=1024, kind="sliding", fv=[0], seed=0x5EED + 420),
+    "full_1024_nopad": dict(B=1, T=1024, kind="full", fv=[0], seed=0x5EED + 430),
+    # a window shorter than the sequence, ragged T, two prompts with different padding
+    "sliding_window40_T100_B2": dict(B=2, T=100, kind="sliding", fv=[0, 37], window=40,
+                                     seed=0x5EED + 440),
+    "full_T68_B2": dict(B=2, T=68, kind="full", fv=[67, 3], seed=0x5EED + 450),
+}
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_gemma_attention(device, name):
+    _say(f"gemma {name}")
+    got, truth, ref = _run(device, CASES[name])
+    c = O.compare(got, truth)
+    r = O.compare(ref, truth)
+    _say(f"  relRMS {c['rel_rms']:.3e} maxAbs {c['max_abs']:.3e} "
+         f"(reference arithmetic relRMS {r['rel_rms']:.3e})")
+    assert c["rel_rms"] <= 5e-3, c
+    assert c["max_abs"] <= 2e-2, c
+    assert c["rel_rms"] <= max(r["rel_rms"], 2.5e-3) * 1.25, (c, r)

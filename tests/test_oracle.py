@@ -479,3 +479,118 @@ def test_golden_fixtures_reproduce():
         out = O.attention(g["q"], g["k"], g["v"], meta["heads"], mode="exact", **kw)
         np.testing.assert_allclose(out.astype(np.float32), g["out_exact"], rtol=0, atol=1e-6,
                                    err_msg=name)
+
+
+# ---------------------------------------------------------------------------------------
+# Gemma-4 text-encoder attention (GemmaTextEncoder.swift:158-239, mask :288-321)
+# ---------------------------------------------------------------------------------------
+
+def test_gemma_inverse_frequencies_match_reference_goldens():
+    """The reference's own expected values (Tests/LTXFoundationTests/
+    GemmaAttentionSpecTests.swift:37-90), to its 1e-6 relative bound."""
+    sl = O.gemma_inverse_frequencies(256, 1e4, 1.0, "default")
+    assert sl.size == 128 and np.all(sl > 0)
+    for i, want in ((0, 1.0), (1, 0.9305720329284668), (2, 0.8659643530845642),
+                    (126, 0.00011547819303814322), (127, 0.00010746077896328643)):
+        assert abs(sl[i] - want) / want < 1e-6, (i, sl[i])
+    assert sl[1] == 1.0 / 10000.0 ** (1.0 / 128.0)
+    fu = O.gemma_inverse_frequencies(512, 1e6, 0.25, "proportional")
+    assert fu.size == 256 and np.count_nonzero(fu) == 64
+    for i, want in ((0, 1.0), (1, 0.9474635124206543), (62, 0.03522694483399391),
+                    (63, 0.03337624669075012)):
+        assert abs(fu[i] - want) / want < 1e-6, (i, fu[i])
+    assert np.all(fu[64:] == 0.0)
+    # the default formula on a partial spec would divide by the rotated width: far off
+    assert abs(1.0 / 1e6 ** (2.0 / 128.0) - fu[1]) > 0.1
+
+
+def test_gemma_mask_rules():
+    """Causal, window, left padding, and rows with no allowed key un-masked entirely
+    (GemmaTextEncoder.swift:288-321), against a brute-force statement of each rule."""
+    T = 12
+    for window, fv in ((0, 0), (4, 0), (0, 5), (3, 5), (1, 0)):
+        m = O.gemma_mask(T, window, fv)
+        for q in range(T):
+            allowed = [k <= q and (window == 0 or q - k < window) and k >= fv for k in range(T)]
+            if not any(allowed):
+                allowed = [True] * T
+            assert list(m[q]) == allowed, (window, fv, q)
+    # at T == window the sliding mask equals the causal one (the reference's coincidence)
+    assert np.array_equal(O.gemma_mask(16, 16, 3), O.gemma_mask(16, 0, 3))
+
+
+def _gemma_case(B, T, Hq, Hkv, D, seed, shared=False):
+    q = O.randn_bf16_bits((B, T, Hq * D), seed)
+    k = O.randn_bf16_bits((B, T, Hkv * D), seed + 1)
+    v = k if shared else O.randn_bf16_bits((B, T, Hkv * D), seed + 2)
+    wq = O.randn_bf16_bits((D,), seed + 3, mean=1.03, std=0.02)
+    wk = O.randn_bf16_bits((D,), seed + 4, mean=0.12, std=0.01)
+    inv = O.gemma_inverse_frequencies(D, 1e4, 1.0, "default")
+    cos, sin = O.gemma_rope_tables(T, inv)
+    return q, k, v, wq, wk, cos, sin
+
+
+def test_gemma_attention_brute_force():
+    """The vectorised oracle against a per-(query, key) loop with math.exp on a tiny case:
+    per-head norms (pow(mean + eps, -0.5), weight; none on v), rotate_half RoPE, GQA by
+    head // (Hq / Hkv), the mask, scale 1."""
+    import math
+
+    B, T, Hq, Hkv, D = 1, 7, 4, 2, 8
+    q, k, v, wq, wk, cos, sin = _gemma_case(B, T, Hq, Hkv, D, 11)
+    got = O.gemma_attention(q, k, v, Hq, Hkv, wq, wk, cos, sin, window=3,
+                            first_valid=[2]).reshape(T, Hq, D)
+    qf = O.bf16_bits_to_f32(q).astype(np.float64).reshape(T, Hq, D)
+    kf = O.bf16_bits_to_f32(k).astype(np.float64).reshape(T, Hkv, D)
+    vf = O.bf16_bits_to_f32(v).astype(np.float64).reshape(T, Hkv, D)
+    wqf, wkf = (O.bf16_bits_to_f32(w).astype(np.float64) for w in (wq, wk))
+
+    def norm(x, w):
+        ms = sum(e * e for e in x) / len(x)
+        return [e * (ms + 1e-6) ** -0.5 * (1.0 if w is None else w[i]) for i, e in enumerate(x)]
+
+    def rope(x, t):
+        h = D // 2
+        return ([x[i] * cos[t, i] - x[i + h] * sin[t, i] for i in range(h)] +
+                [x[i + h] * cos[t, i] + x[i] * sin[t, i] for i in range(h)])
+
+    for h in range(Hq):
+        kh = h // (Hq // Hkv)
+        for t in range(T):
+            qq = rope(norm(qf[t, h], wqf), t)
+            keys = [kk for kk in range(T) if kk <= t and t - kk < 3 and kk >= 2] or list(range(T))
+            logits = [sum(a * b for a, b in zip(qq, rope(norm(kf[kk, kh], wkf), kk)))
+                      for kk in keys]
+            mx = max(logits)
+            w = [math.exp(x - mx) for x in logits]
+            want = [sum(w[j] * norm(vf[kk, kh], None)[c] for j, kk in enumerate(keys)) / sum(w)
+                    for c in range(D)]
+            assert np.allclose(got[t, h], want, rtol=1e-9, atol=1e-12), (h, t)
+
+
+def test_gemma_attention_invariants():
+    """Future keys, keys past the window and padding keys do not reach a valid row; a
+    padding row attends to every key unmasked; the K-shares-V layers take V from the
+    PRE-norm K projection (so V differs from the finished K)."""
+    B, T, Hq, Hkv, D = 1, 40, 2, 1, 16
+    q, k, v, wq, wk, cos, sin = _gemma_case(B, T, Hq, Hkv, D, 21)
+    base = O.gemma_attention(q, k, v, Hq, Hkv, wq, wk, cos, sin, window=8, first_valid=[5])
+    k2, v2 = k.copy(), v.copy()
+    k2[0, 30:] ^= 0x0040            # perturb keys/values after query 29
+    v2[0, 30:] ^= 0x0040
+    k2[0, :5] ^= 0x0040             # and the padding keys
+    v2[0, :5] ^= 0x0040
+    k2[0, 10:12] ^= 0x0040          # and keys more than 8 behind query 20
+    v2[0, 10:12] ^= 0x0040
+    alt = O.gemma_attention(q, k2, v2, Hq, Hkv, wq, wk, cos, sin, window=8, first_valid=[5])
+    assert np.array_equal(base[0, 20:30], alt[0, 20:30])
+    # a padding row == unmasked attention over all keys
+    full = O.gemma_attention(q, k, v, Hq, Hkv, wq, wk, cos, sin, window=0, first_valid=[0])
+    free = O.gemma_attention(q, k, v, Hq, Hkv, wq, wk, cos, sin, window=8, first_valid=[40])
+    assert not np.allclose(full[0, 3], free[0, 3])          # causal vs all keys differ
+    qq = O.gemma_attention(q, k, v, Hq, Hkv, wq, wk, cos, sin, window=0, first_valid=[5])
+    # rows 0..4 of first_valid=5 equal rows of a call where every row is free
+    assert np.allclose(qq[0, :5], free[0, :5], rtol=0, atol=0)
+    # shared K/V: V is the weightless norm of the raw K projection, not of the finished K
+    sh = O.gemma_attention(q, k, k, Hq, Hkv, wq, wk, cos, sin)
+    assert not np.allclose(sh, O.gemma_attention(q, k, v, Hq, Hkv, wq, wk, cos, sin))
