@@ -156,19 +156,42 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
 #pragma unroll
     for (int db = 0; db < NDS; ++db) o[db] = splat16(0.f);
     float m = -INFINITY, l = 0.f;
+    // Operands in flight: the block's K' rows are fetched one block ahead, its V'^T rows at
+    // the top of the block, so their latency overlaps the products, the exchange and the
+    // softmax instead of stalling each step.
+    auto load_k = [&](int kb, u32x4 (&kx)[NCS]) __attribute__((always_inline)) {
+        const int kr = min(kb * 32 + r, T - 1);     // keys past T read key T-1 (masked)
+#pragma unroll
+        for (int c = 0; c < NCS; ++c) kx[c] = ldg16(Kh + (int64_t)kr * D + 16 * c + 8 * g);
+    };
+    u32x4 kx[NCS];
+    load_k(kb_lo, kx);
     for (int kb = kb_lo, it = 0; kb <= kb_hi; ++kb, ++it) {
-        // partial S^T over this wave's channels (keys past T read key T-1; masked below)
-        f32x16 sp = splat16(0.f);
-        const int kr = min(kb * 32 + r, T - 1);
+        // V'^T operands of this block: channel wave*DS + 32db + r, keys 32kb + 16hf + 4g + 0..3
+        // and + 8 (clamped into the row: past T only for masked keys, T a multiple of 4)
+        u32x2 vx[2][NDS][2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int k0 = 32 * kb + 16 * hf + 4 * g;
+#pragma unroll
+            for (int db = 0; db < NDS; ++db) {
+                const bf16 *vrow = Vt + (int64_t)(32 * db + r) * T;
+                vx[hf][db][0] = *(const u32x2 *)(vrow + min(k0, T - 4));
+                vx[hf][db][1] = *(const u32x2 *)(vrow + min(k0 + 8, T - 4));
+            }
+        }
+        // partial S^T over this wave's channels: the hi and lo parts of q' in two chains
+        f32x16 sh = splat16(0.f), sl = splat16(0.f);
 #pragma unroll
         for (int c = 0; c < NCS; ++c) {
-            const bf16x8 a = __builtin_bit_cast(bf16x8, ldg16(Kh + (int64_t)kr * D + 16 * c + 8 * g));
-            sp = mfma32(a, qf[c], sp);
-            sp = mfma32(a, ql[c], sp);
+            const bf16x8 a = __builtin_bit_cast(bf16x8, kx[c]);
+            sh = mfma32(a, qf[c], sh);
+            sl = mfma32(a, ql[c], sl);
         }
+        if (kb < kb_hi) load_k(kb + 1, kx);
         const int buf = it & 1;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sS[buf][wave][i][lane] = sp[i];
+        for (int i = 0; i < 16; ++i) sS[buf][wave][i][lane] = sh[i] + sl[i];
         __syncthreads();
         f32x16 s;
 #pragma unroll
@@ -211,20 +234,16 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
         l = l * alpha + ts;
 #pragma unroll
         for (int db = 0; db < NDS; ++db) o[db] *= splat16(alpha);
-        // O^T += V^T.P^T: channel wave*DS + 32db + r, keys 32kb + 16hf + 4g + 0..3, then + 8
+        // O^T += V^T.P^T
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const int k0 = 32 * kb + 16 * hf + 4 * g;
+        for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
             for (int db = 0; db < NDS; ++db) {
-                const bf16 *vrow = Vt + (int64_t)(32 * db + r) * T;
-                const u32x2 lo = *(const u32x2 *)(vrow + min(k0, T - 4));
-                const u32x2 hi = *(const u32x2 *)(vrow + min(k0 + 8, T - 4));
+                const u32x2 lo = vx[hf][db][0], hi = vx[hf][db][1];
                 const bf16x8 a = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
                 o[db] = mfma32(a, __builtin_bit_cast(bf16x8, wh[hf]), o[db]);
                 o[db] = mfma32(a, __builtin_bit_cast(bf16x8, wl[hf]), o[db]);
             }
-        }
     }
 
     // ---- epilogue: O / l in fp32 (the reference's dtype here), this wave's channels ------
