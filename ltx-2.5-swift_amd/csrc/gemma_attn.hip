@@ -2,15 +2,16 @@
 // :288-321) for gfx950: head dims 256 / 512, 16 query heads over 8 or 1 KV heads, causal +
 // sliding-window + left-padding mask, scale 1.0, 1024 tokens per prompt.
 //
-// Two launches:
-//   gemma_prep_kernel   one wave per (batch row, token, head) row of q, k or v: the per-head
-//                       RMS norm (fp32, pow(mean + eps, -0.5), times the weight for q and k,
-//                       weightless for v), rotate_half RoPE with the fp32 tables for q and k,
+// Three launches:
+//   gemma_prep_kernel   one wave per (batch row, token, head) row of q or k: the per-head
+//                       RMS norm (fp32, pow(mean + eps, -0.5), times the weight), rotate_half
+//                       RoPE with the fp32 tables,
 //                       q scaled by scale*log2(e). Writes q' as two bf16 parts (hi + lo)
 //                       [B][Hq][T][D], k' [B][Hkv][T][D] (one bf16 rounding, as the
-//                       reference rounds its normed k) and v' TRANSPOSED, [B][Hkv][D][T], so
-//                       that the P.V operand (one channel, eight keys per lane) is two 8-byte
-//                       loads.
+//                       reference rounds its normed k).
+//   gemma_vt_kernel     v with the weightless per-head norm, written TRANSPOSED,
+//                       [B][Hkv][D][T] (through an LDS tile of 64 tokens), so that the P.V
+//                       operand (one channel, eight keys per lane) is two 8-byte loads.
 //   gemma_attn_kernel   one workgroup of four waves per (batch row, query head, 32 queries);
 //                       the waves split the head dim into four slices of D/4 channels. Per
 //                       32-key block each wave forms the partial S^T = K.Q'^T over its slice
@@ -37,16 +38,15 @@ __global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p
     constexpr int E = D / 64;                       // channels per lane: 4 or 8
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int heads = p.Hq + 2 * p.Hkv;             // q heads, k heads, v heads per token
+    const int heads = p.Hq + p.Hkv;                 // q heads, then k heads, per token
     if (row >= (int64_t)p.B * p.T * heads) return;
     const int hr = (int)(row % heads);
     const int64_t bt = row / heads;
     const int t = (int)(bt % p.T), b = (int)(bt / p.T);
-    const int kind = hr < p.Hq ? 0 : hr < p.Hq + p.Hkv ? 1 : 2;   // q, k, v
-    const int h = kind == 0 ? hr : kind == 1 ? hr - p.Hq : hr - p.Hq - p.Hkv;
+    const int kind = hr < p.Hq ? 0 : 1;             // q, k
+    const int h = kind == 0 ? hr : hr - p.Hq;
     const bf16 *src = kind == 0 ? (const bf16 *)p.q + (int64_t)b * p.q_bs + (int64_t)t * p.q_rs
-                    : kind == 1 ? (const bf16 *)p.k + (int64_t)b * p.k_bs + (int64_t)t * p.k_rs
-                                : (const bf16 *)p.v + (int64_t)b * p.v_bs + (int64_t)t * p.v_rs;
+                                : (const bf16 *)p.k + (int64_t)b * p.k_bs + (int64_t)t * p.k_rs;
     src += (int64_t)h * D + lane * E;
     float x[E];
     if constexpr (E == 8) {
@@ -61,13 +61,6 @@ __global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
     const float rs = powf(ss / (float)D + p.eps, -0.5f);
-    if (kind == 2) {
-        // v: weightless norm, no rotation; stored transposed (channel rows of T keys)
-        bf16 *dst = (bf16 *)p.vt + (((int64_t)b * p.Hkv + h) * D + lane * E) * p.T + t;
-#pragma unroll
-        for (int e = 0; e < E; ++e) dst[(int64_t)e * p.T] = (bf16)(x[e] * rs);
-        return;
-    }
     const bf16 *w = (const bf16 *)(kind == 0 ? p.q_w : p.k_w) + lane * E;
 #pragma unroll
     for (int e = 0; e < E; ++e) x[e] = (x[e] * rs) * (float)w[e];
@@ -101,6 +94,55 @@ __global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p
 #pragma unroll
         for (int e = 0; e < E; ++e) lo[e] = y[e] - (float)(bf16)y[e];
         put((bf16 *)p.qp_lo + off, lo);
+    }
+}
+
+// v: the weightless per-head norm, stored transposed (channel rows of T keys). One workgroup
+// per (batch row, KV head, 64 tokens): each wave normalises 16 token rows into an LDS tile,
+// then the tile leaves as runs of 8 tokens of one channel.
+template <int D>
+__global__ __launch_bounds__(256) void gemma_vt_kernel(const GemmaPrepParams p) {
+    constexpr int E = D / 64;
+    constexpr int TT = 64;                          // tokens per workgroup
+    __shared__ __attribute__((aligned(16))) bf16 tile[TT][D + 8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ntb = (p.T + TT - 1) / TT;
+    const int t0 = (int)(blockIdx.x % ntb) * TT;
+    const int bh = (int)(blockIdx.x / ntb);
+    const int h = bh % p.Hkv, b = bh / p.Hkv;
+    for (int j = 0; j < TT / 4; ++j) {
+        const int tl = wave * (TT / 4) + j, t = t0 + tl;
+        if (t >= p.T) break;
+        const bf16 *src = (const bf16 *)p.v + (int64_t)b * p.v_bs + (int64_t)t * p.v_rs +
+                          (int64_t)h * D + lane * E;
+        float x[E];
+        if constexpr (E == 8) {
+            unpack8(ldg16(src), x);
+        } else {
+            const u32x2 w = *(const u32x2 *)src;
+            x[0] = bf_lo(w[0]); x[1] = bf_hi(w[0]); x[2] = bf_lo(w[1]); x[3] = bf_hi(w[1]);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) ss += x[e] * x[e];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        const float rs = powf(ss / (float)D + p.eps, -0.5f);
+#pragma unroll
+        for (int e = 0; e < E; ++e) tile[tl][lane * E + e] = (bf16)(x[e] * rs);
+    }
+    __syncthreads();
+    const int nt = min(TT, p.T - t0);               // a multiple of 4 (T is)
+    for (int u = threadIdx.x; u < D * (TT / 8); u += 256) {
+        const int c = u / (TT / 8), j8 = 8 * (u % (TT / 8));
+        if (j8 >= nt) continue;
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = (float)tile[min(j8 + e, TT - 1)][c];
+        // 8-byte stores: channel rows are T * 2 bytes apart, T a multiple of 4
+        bf16 *dst = (bf16 *)p.vt + (((int64_t)b * p.Hkv + h) * D + c) * p.T + t0 + j8;
+        *(u32x2 *)dst = u32x2{pack_bf2(f[0], f[1]), pack_bf2(f[2], f[3])};
+        if (j8 + 8 <= nt) *(u32x2 *)(dst + 4) = u32x2{pack_bf2(f[4], f[5]), pack_bf2(f[6], f[7])};
     }
 }
 
@@ -266,11 +308,17 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
 }  // namespace
 
 int launch_gemma_prep(const GemmaPrepParams &p, int D, void *stream) {
-    const int64_t rows = (int64_t)p.B * p.T * (p.Hq + 2 * p.Hkv);
+    const int64_t rows = (int64_t)p.B * p.T * (p.Hq + p.Hkv);
     const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    const dim3 vgrid((unsigned)((int64_t)p.B * p.Hkv * ((p.T + 63) / 64)));
     hipStream_t st = (hipStream_t)stream;
-    if (D == 512) hipLaunchKernelGGL(gemma_prep_kernel<512>, grid, block, 0, st, p);
-    else hipLaunchKernelGGL(gemma_prep_kernel<256>, grid, block, 0, st, p);
+    if (D == 512) {
+        hipLaunchKernelGGL(gemma_prep_kernel<512>, grid, block, 0, st, p);
+        hipLaunchKernelGGL(gemma_vt_kernel<512>, vgrid, block, 0, st, p);
+    } else {
+        hipLaunchKernelGGL(gemma_prep_kernel<256>, grid, block, 0, st, p);
+        hipLaunchKernelGGL(gemma_vt_kernel<256>, vgrid, block, 0, st, p);
+    }
     return (int)hipGetLastError();
 }
 
