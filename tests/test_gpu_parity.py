@@ -298,12 +298,12 @@ def test_rebase_path_large_logits(device):
 @pytest.mark.parametrize("B,H,Lq,Lk,D,valid,rope", [
     (2, 4, 1000, 1024, 128, [128, 1], False),   # most keys kept at D=128; a single key
     (2, 4, 1000, 300, 64, [256, 129], True),    # most keys kept at D=64, norm + RoPE
-    (2, 32, 4100, 77, 64, None, True),          # 65 query blocks per head: 4-5 per wave
+    (2, 32, 4100, 77, 64, None, True),          # 129 query blocks of 32 per head: 4-5 per wave
     (1, 2, 1, 3, 128, None, False),             # one query
 ])
 def test_short_key_kernel(device, B, H, Lq, Lk, D, valid, rope):
-    """The short-key kernel (the head's keys resident in LDS, queries streamed by blocks of
-    64 with the next block's Q in flight) against the oracle, and the LDS-DMA kernel on the
+    """The short-key kernel (the head's keys resident in LDS, eight waves per workgroup each
+    streaming blocks of 32 queries past them) against the oracle, and the LDS-DMA kernel on the
     same call, with norm on both sides (its gated epilogue: test_output_gate)."""
     _say(f"short keys B={B} H={H} Lq={Lq} Lk={Lk} D={D} valid={valid} rope={rope}")
     seed = 0x5EED + 90 + Lq
