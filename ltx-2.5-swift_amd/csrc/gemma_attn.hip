@@ -87,9 +87,17 @@ __global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p
             *(u32x2 *)dst = u32x2{pack_bf2(z[0], z[1]), pack_bf2(z[2], z[3])};
         }
     };
-    const int64_t off = (((int64_t)b * (kind == 0 ? p.Hq : p.Hkv) + h) * p.T + t) * D + lane * E;
-    put((bf16 *)(kind == 0 ? p.qp : p.kp) + off, y);
-    if (kind == 0) {
+    if (kind == 1) {
+        // k' in operand order: 32-key block t/32, 16-channel chunk c, lane (t%32) + 32g holds
+        // channels 16c + 8g .. +7 of key t
+        const int ch = lane * E, c = ch >> 4, g = (ch >> 3) & 1;
+        const int nkb = (p.T + 31) / 32;
+        const int64_t off = ((((int64_t)b * p.Hkv + h) * nkb + (t >> 5)) * (D / 16) + c) * 512 +
+                            ((t & 31) + 32 * g) * 8 + (ch & 7);
+        put((bf16 *)p.kp + off, y);
+    } else {
+        const int64_t off = (((int64_t)b * p.Hq + h) * p.T + t) * D + lane * E;
+        put((bf16 *)p.qp + off, y);
         float lo[E];
 #pragma unroll
         for (int e = 0; e < E; ++e) lo[e] = y[e] - (float)(bf16)y[e];
@@ -97,9 +105,9 @@ __global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p
     }
 }
 
-// v: the weightless per-head norm, stored transposed (channel rows of T keys). One workgroup
-// per (batch row, KV head, 64 tokens): each wave normalises 16 token rows into an LDS tile,
-// then the tile leaves as runs of 8 tokens of one channel.
+// v: the weightless per-head norm, stored transposed in operand order. One workgroup per
+// (batch row, KV head, 64 tokens): each wave normalises 16 token rows into an LDS tile, then
+// the tile leaves as the P.V operand units of its two 32-key blocks.
 template <int D>
 __global__ __launch_bounds__(256) void gemma_vt_kernel(const GemmaPrepParams p) {
     constexpr int E = D / 64;
@@ -132,17 +140,32 @@ __global__ __launch_bounds__(256) void gemma_vt_kernel(const GemmaPrepParams p) 
         for (int e = 0; e < E; ++e) tile[tl][lane * E + e] = (bf16)(x[e] * rs);
     }
     __syncthreads();
-    const int nt = min(TT, p.T - t0);               // a multiple of 4 (T is)
-    for (int u = threadIdx.x; u < D * (TT / 8); u += 256) {
-        const int c = u / (TT / 8), j8 = 8 * (u % (TT / 8));
-        if (j8 >= nt) continue;
+    // The tile leaves in operand order: per 32-key block kb, key half hf and 32-channel block
+    // cb one 1 KB unit whose lane r + 32g holds channel 32cb + r at keys
+    // 32kb + 16hf + 4g + {0..3, 8..11}. Keys past T are written as zeros (their weights are 0,
+    // and 0 * 0 keeps the products finite). The last block's k' rows past T are zeroed too.
+    const int nkb = (p.T + 31) / 32;
+    bf16 *vbase = (bf16 *)p.vt + ((int64_t)b * p.Hkv + h) * nkb * (D * 32);
+    for (int u = threadIdx.x; u < 2 * 2 * (D / 32) * 64; u += 256) {
+        const int l = u & 63, rest = u >> 6;
+        const int cb = rest % (D / 32), hf = (rest / (D / 32)) & 1, kbl = rest / (D / 16);
+        const int kb = t0 / 32 + kbl;
+        if (kb >= nkb) continue;
+        const int r = l & 31, g = l >> 5;
         float f[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = (float)tile[min(j8 + e, TT - 1)][c];
-        // 8-byte stores: channel rows are T * 2 bytes apart, T a multiple of 4
-        bf16 *dst = (bf16 *)p.vt + (((int64_t)b * p.Hkv + h) * D + c) * p.T + t0 + j8;
-        *(u32x2 *)dst = u32x2{pack_bf2(f[0], f[1]), pack_bf2(f[2], f[3])};
-        if (j8 + 8 <= nt) *(u32x2 *)(dst + 4) = u32x2{pack_bf2(f[4], f[5]), pack_bf2(f[6], f[7])};
+        for (int e = 0; e < 8; ++e) {
+            const int tl = 32 * kbl + 16 * hf + 4 * g + (e & 3) + 8 * (e >> 2);
+            f[e] = t0 + tl < p.T ? (float)tile[tl][32 * cb + r] : 0.f;
+        }
+        *(u32x4 *)(vbase + (((int64_t)kb * 2 + hf) * (D / 32) + cb) * 512 + l * 8) = pack8(f);
+    }
+    if ((p.T & 31) && t0 / 32 <= nkb - 1 && nkb - 1 < t0 / 32 + 2) {
+        bf16 *kbase = (bf16 *)p.kp + (((int64_t)b * p.Hkv + h) * nkb + nkb - 1) * (D * 32);
+        for (int u = threadIdx.x; u < (D / 16) * 64; u += 256) {
+            const int l = u & 63;
+            if (32 * (nkb - 1) + (l & 31) >= p.T) *(u32x4 *)(kbase + u * 8) = u32x4{0, 0, 0, 0};
+        }
     }
 }
 
@@ -177,8 +200,13 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
         qf[c] = __builtin_bit_cast(bf16x8, ldg16(Qh + (int64_t)qr * D + 16 * c + 8 * g));
         ql[c] = __builtin_bit_cast(bf16x8, ldg16(Ql + (int64_t)qr * D + 16 * c + 8 * g));
     }
-    const bf16 *Kh = (const bf16 *)p.kp + ((int64_t)b * p.Hkv + kvh) * T * D + wave * DS;
-    const bf16 *Vt = (const bf16 *)p.vt + (((int64_t)b * p.Hkv + kvh) * D + wave * DS) * T;
+    // K' and V'^T of this KV head in operand order: per 32-key block, one 1 KB unit (64 lanes x
+    // 16 bytes) per operand, so each operand is one coalesced 16-byte load per lane.
+    const int nkb_all = (T + 31) / 32;
+    const bf16 *Kt = (const bf16 *)p.kp + ((int64_t)b * p.Hkv + kvh) * nkb_all * (D * 32) +
+                     (wave * NCS) * 512 + lane * 8;
+    const bf16 *Vt = (const bf16 *)p.vt + ((int64_t)b * p.Hkv + kvh) * nkb_all * (D * 32) +
+                     (wave * NDS) * 512 + lane * 8;
 
     // Key blocks: causal / window / padding bounds; a block with rows inside the left padding
     // (their rows have no allowed key) runs over all keys, those rows unmasked.
@@ -193,6 +221,11 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
     }
     const int q = q0 + r;                           // this lane's query row
     const bool free_row = q < fv;
+    // The row's allowed keys as one range [k_lo, k_hi]: all keys for a row inside the left
+    // padding, else causal (k <= q), past the padding (k >= fv) and inside the window
+    // (q - k < window); k_hi <= T - 1 also masks the keys past T of the last block.
+    const int k_lo = free_row ? 0 : max(fv, p.window > 0 ? q - p.window + 1 : 0);
+    const int k_hi = free_row ? T - 1 : min(q, T - 1);
 
     f32x16 o[NDS];
 #pragma unroll
@@ -202,26 +235,33 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
     // the top of the block, so their latency overlaps the products, the exchange and the
     // softmax instead of stalling each step.
     auto load_k = [&](int kb, u32x4 (&kx)[NCS]) __attribute__((always_inline)) {
-        const int kr = min(kb * 32 + r, T - 1);     // keys past T read key T-1 (masked)
 #pragma unroll
-        for (int c = 0; c < NCS; ++c) kx[c] = ldg16(Kh + (int64_t)kr * D + 16 * c + 8 * g);
+        for (int c = 0; c < NCS; ++c) kx[c] = ldg16(Kt + ((int64_t)kb * (D / 16) + c) * 512);
     };
+    // V'^T operand units of a block: channel block wave*NDS + db, key half hf
+    auto load_v = [&](int kb, u32x4 (&vx)[2][NDS]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int db = 0; db < NDS; ++db)
+                vx[hf][db] = ldg16(Vt + (((int64_t)kb * 2 + hf) * (D / 32) + db) * 512);
+    };
+    // D = 256 has the registers to hold the next block's V'^T as well (one block ahead, like
+    // K', in two buffers that alternate by block parity); D = 512 loads it at the top of its
+    // block.
+    constexpr bool kVAhead = D <= 256;
     u32x4 kx[NCS];
+    u32x4 va[2][NDS], vb[2][NDS];
     load_k(kb_lo, kx);
-    for (int kb = kb_lo, it = 0; kb <= kb_hi; ++kb, ++it) {
-        // V'^T operands of this block: channel wave*DS + 32db + r, keys 32kb + 16hf + 4g + 0..3
-        // and + 8 (clamped into the row: past T only for masked keys, T a multiple of 4)
-        u32x2 vx[2][NDS][2];
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const int k0 = 32 * kb + 16 * hf + 4 * g;
-#pragma unroll
-            for (int db = 0; db < NDS; ++db) {
-                const bf16 *vrow = Vt + (int64_t)(32 * db + r) * T;
-                vx[hf][db][0] = *(const u32x2 *)(vrow + min(k0, T - 4));
-                vx[hf][db][1] = *(const u32x2 *)(vrow + min(k0 + 8, T - 4));
-            }
-        }
+    if constexpr (kVAhead) load_v(kb_lo, va);
+    // One 32-key block; `buf` selects the LDS exchange buffer, vc holds this block's V'^T
+    // (when loaded ahead) and vn receives the next block's.
+    auto block = [&](int kb, auto bufc, u32x4 (&vc)[2][NDS], u32x4 (&vn)[2][NDS])
+        __attribute__((always_inline)) {
+        constexpr int buf = decltype(bufc)::value;
+        u32x4 vl[2][NDS];
+        if constexpr (!kVAhead) load_v(kb, vl);
+        u32x4 (&vx)[2][NDS] = kVAhead ? vc : vl;
         // partial S^T over this wave's channels: the hi and lo parts of q' in two chains
         f32x16 sh = splat16(0.f), sl = splat16(0.f);
 #pragma unroll
@@ -230,8 +270,10 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
             sh = mfma32(a, qf[c], sh);
             sl = mfma32(a, ql[c], sl);
         }
-        if (kb < kb_hi) load_k(kb + 1, kx);
-        const int buf = it & 1;
+        if (kb < kb_hi) {
+            load_k(kb + 1, kx);
+            if constexpr (kVAhead) load_v(kb + 1, vn);
+        }
 #pragma unroll
         for (int i = 0; i < 16; ++i) sS[buf][wave][i][lane] = sh[i] + sl[i];
         __syncthreads();
@@ -245,9 +287,7 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int k = 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
-            const bool ok = k < T && (free_row || (k <= q && k >= fv &&
-                                                   (p.window <= 0 || q - k < p.window)));
-            s[i] = ok ? s[i] : -INFINITY;
+            s[i] = ((k >= k_lo) & (k <= k_hi)) ? s[i] : -INFINITY;
             mx = fmaxf(mx, s[i]);
         }
         mx = fmaxf(mx, xlane32(mx));
@@ -281,11 +321,14 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
         for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
             for (int db = 0; db < NDS; ++db) {
-                const u32x2 lo = vx[hf][db][0], hi = vx[hf][db][1];
-                const bf16x8 a = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+                const bf16x8 a = __builtin_bit_cast(bf16x8, vx[hf][db]);
                 o[db] = mfma32(a, __builtin_bit_cast(bf16x8, wh[hf]), o[db]);
                 o[db] = mfma32(a, __builtin_bit_cast(bf16x8, wl[hf]), o[db]);
             }
+    };
+    for (int kb = kb_lo; kb <= kb_hi; kb += 2) {
+        block(kb, std::integral_constant<int, 0>{}, va, vb);
+        if (kb + 1 <= kb_hi) block(kb + 1, std::integral_constant<int, 1>{}, vb, va);
     }
 
     // ---- epilogue: O / l in fp32 (the reference's dtype here), this wave's channels ------

@@ -349,7 +349,8 @@ ltx_attn_status gemma_plan(const ltx_gemma_attn_args *a, GemmaPlan *pl) {
         return fail(LTX_ATTN_EINVAL, "out must be 16-byte aligned with strides that are "
                     "multiples of 4 and a row of at least Hq*D");
     const size_t qn = 2 * (size_t)a->B * a->Hq * a->T * D;
-    const size_t kn = 2 * (size_t)a->B * a->Hkv * a->T * D;
+    // k' and v'^T are stored by whole 32-key blocks (operand order), the last one zero-padded
+    const size_t kn = 2 * (size_t)a->B * a->Hkv * ((a->T + 31) / 32 * 32) * D;
     pl->off_q = 0;
     pl->off_qlo = align_up(qn, 256);
     pl->off_k = pl->off_qlo + align_up(qn, 256);
