@@ -106,65 +106,71 @@ __global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p
 }
 
 // v: the weightless per-head norm, stored transposed in operand order. One workgroup per
-// (batch row, KV head, 64 tokens): each wave normalises 16 token rows into an LDS tile, then
-// the tile leaves as the P.V operand units of its two 32-key blocks.
+// (batch row, KV head, 32-key block): each wave loads its 8 token rows at once, normalises
+// them into an LDS tile, then the tile leaves as the block's P.V operand units.
 template <int D>
 __global__ __launch_bounds__(256) void gemma_vt_kernel(const GemmaPrepParams p) {
     constexpr int E = D / 64;
-    constexpr int TT = 64;                          // tokens per workgroup
+    constexpr int TT = 32;                          // tokens per workgroup: one key block
+    constexpr int RW = TT / 4;                      // rows per wave
     __shared__ __attribute__((aligned(16))) bf16 tile[TT][D + 8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int ntb = (p.T + TT - 1) / TT;
-    const int t0 = (int)(blockIdx.x % ntb) * TT;
-    const int bh = (int)(blockIdx.x / ntb);
+    const int nkb = (p.T + TT - 1) / TT;
+    const int kb = (int)(blockIdx.x % nkb), t0 = kb * TT;
+    const int bh = (int)(blockIdx.x / nkb);
     const int h = bh % p.Hkv, b = bh / p.Hkv;
-    for (int j = 0; j < TT / 4; ++j) {
-        const int tl = wave * (TT / 4) + j, t = t0 + tl;
-        if (t >= p.T) break;
-        const bf16 *src = (const bf16 *)p.v + (int64_t)b * p.v_bs + (int64_t)t * p.v_rs +
-                          (int64_t)h * D + lane * E;
-        float x[E];
-        if constexpr (E == 8) {
-            unpack8(ldg16(src), x);
-        } else {
-            const u32x2 w = *(const u32x2 *)src;
-            x[0] = bf_lo(w[0]); x[1] = bf_hi(w[0]); x[2] = bf_lo(w[1]); x[3] = bf_hi(w[1]);
+    float x[RW][E];
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+        const int t = t0 + wave * RW + j;
+#pragma unroll
+        for (int e = 0; e < E; ++e) x[j][e] = 0.f;
+        if (t < p.T) {
+            const bf16 *src = (const bf16 *)p.v + (int64_t)b * p.v_bs + (int64_t)t * p.v_rs +
+                              (int64_t)h * D + lane * E;
+            if constexpr (E == 8) {
+                unpack8(ldg16(src), x[j]);
+            } else {
+                const u32x2 w = *(const u32x2 *)src;
+                x[j][0] = bf_lo(w[0]); x[j][1] = bf_hi(w[0]);
+                x[j][2] = bf_lo(w[1]); x[j][3] = bf_hi(w[1]);
+            }
         }
+    }
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
         float ss = 0.f;
 #pragma unroll
-        for (int e = 0; e < E; ++e) ss += x[e] * x[e];
+        for (int e = 0; e < E; ++e) ss += x[j][e] * x[j][e];
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
         const float rs = powf(ss / (float)D + p.eps, -0.5f);
 #pragma unroll
-        for (int e = 0; e < E; ++e) tile[tl][lane * E + e] = (bf16)(x[e] * rs);
+        for (int e = 0; e < E; ++e) tile[wave * RW + j][lane * E + e] = (bf16)(x[j][e] * rs);
     }
     __syncthreads();
-    // The tile leaves in operand order: per 32-key block kb, key half hf and 32-channel block
-    // cb one 1 KB unit whose lane r + 32g holds channel 32cb + r at keys
-    // 32kb + 16hf + 4g + {0..3, 8..11}. Keys past T are written as zeros (their weights are 0,
-    // and 0 * 0 keeps the products finite). The last block's k' rows past T are zeroed too.
-    const int nkb = (p.T + 31) / 32;
-    bf16 *vbase = (bf16 *)p.vt + ((int64_t)b * p.Hkv + h) * nkb * (D * 32);
-    for (int u = threadIdx.x; u < 2 * 2 * (D / 32) * 64; u += 256) {
+    // Operand units of the block: per key half hf and 32-channel block cb one 1 KB unit whose
+    // lane r + 32g holds channel 32cb + r at keys 32kb + 16hf + 4g + {0..3, 8..11}. Keys past T
+    // are written as zeros (their weights are 0, and 0 * 0 keeps the products finite); the
+    // last block's k' rows past T are zeroed too.
+    bf16 *vbase = (bf16 *)p.vt + (((int64_t)b * p.Hkv + h) * nkb + kb) * (D * 32);
+    for (int u = threadIdx.x; u < 2 * (D / 32) * 64; u += 256) {
         const int l = u & 63, rest = u >> 6;
-        const int cb = rest % (D / 32), hf = (rest / (D / 32)) & 1, kbl = rest / (D / 16);
-        const int kb = t0 / 32 + kbl;
-        if (kb >= nkb) continue;
+        const int cb = rest % (D / 32), hf = rest / (D / 32);
         const int r = l & 31, g = l >> 5;
         float f[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int tl = 32 * kbl + 16 * hf + 4 * g + (e & 3) + 8 * (e >> 2);
+            const int tl = 16 * hf + 4 * g + (e & 3) + 8 * (e >> 2);
             f[e] = t0 + tl < p.T ? (float)tile[tl][32 * cb + r] : 0.f;
         }
-        *(u32x4 *)(vbase + (((int64_t)kb * 2 + hf) * (D / 32) + cb) * 512 + l * 8) = pack8(f);
+        *(u32x4 *)(vbase + ((int64_t)hf * (D / 32) + cb) * 512 + l * 8) = pack8(f);
     }
-    if ((p.T & 31) && t0 / 32 <= nkb - 1 && nkb - 1 < t0 / 32 + 2) {
-        bf16 *kbase = (bf16 *)p.kp + (((int64_t)b * p.Hkv + h) * nkb + nkb - 1) * (D * 32);
+    if ((p.T & 31) && kb == nkb - 1) {
+        bf16 *kbase = (bf16 *)p.kp + (((int64_t)b * p.Hkv + h) * nkb + kb) * (D * 32);
         for (int u = threadIdx.x; u < (D / 16) * 64; u += 256) {
             const int l = u & 63;
-            if (32 * (nkb - 1) + (l & 31) >= p.T) *(u32x4 *)(kbase + u * 8) = u32x4{0, 0, 0, 0};
+            if (t0 + (l & 31) >= p.T) *(u32x4 *)(kbase + u * 8) = u32x4{0, 0, 0, 0};
         }
     }
 }
@@ -175,7 +181,9 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
     constexpr int DS = D / 4;                       // channels per wave
     constexpr int NCS = DS / 16;                    // 16-channel chunks of the wave's S slice
     constexpr int NDS = DS / 32;                    // 32-channel blocks of the wave's O slice
-    __shared__ float sS[2][4][16][64];              // partial S per wave, double-buffered
+    // partial S per wave, double-buffered; 20-float lane rows keep the 16-byte accesses of
+    // 16 lanes on distinct banks
+    __shared__ __attribute__((aligned(16))) float sS[2][4][64][20];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -275,13 +283,21 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
             if constexpr (kVAhead) load_v(kb + 1, vn);
         }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sS[buf][wave][i][lane] = sh[i] + sl[i];
+        for (int i4 = 0; i4 < 4; ++i4)
+            *(f32x4 *)&sS[buf][wave][lane][4 * i4] =
+                f32x4{sh[4 * i4] + sl[4 * i4], sh[4 * i4 + 1] + sl[4 * i4 + 1],
+                      sh[4 * i4 + 2] + sl[4 * i4 + 2], sh[4 * i4 + 3] + sl[4 * i4 + 3]};
         __syncthreads();
         f32x16 s;
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-            s[i] = ((sS[buf][0][i][lane] + sS[buf][1][i][lane]) + sS[buf][2][i][lane]) +
-                   sS[buf][3][i][lane];
+        for (int i4 = 0; i4 < 4; ++i4) {
+            const f32x4 p0 = *(const f32x4 *)&sS[buf][0][lane][4 * i4];
+            const f32x4 p1 = *(const f32x4 *)&sS[buf][1][lane][4 * i4];
+            const f32x4 p2 = *(const f32x4 *)&sS[buf][2][lane][4 * i4];
+            const f32x4 p3 = *(const f32x4 *)&sS[buf][3][lane][4 * i4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[4 * i4 + e] = ((p0[e] + p1[e]) + p2[e]) + p3[e];
+        }
         // mask: key k = 32kb + 8(i>>2) + 4g + (i&3) for query q
         float mx = -INFINITY;
 #pragma unroll
@@ -353,7 +369,7 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
 int launch_gemma_prep(const GemmaPrepParams &p, int D, void *stream) {
     const int64_t rows = (int64_t)p.B * p.T * (p.Hq + p.Hkv);
     const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-    const dim3 vgrid((unsigned)((int64_t)p.B * p.Hkv * ((p.T + 63) / 64)));
+    const dim3 vgrid((unsigned)((int64_t)p.B * p.Hkv * ((p.T + 31) / 32)));
     hipStream_t st = (hipStream_t)stream;
     if (D == 512) {
         hipLaunchKernelGGL(gemma_prep_kernel<512>, grid, block, 0, st, p);
