@@ -581,6 +581,9 @@ def main():
                     help="only run the short-key calls (text cross-attention, the cross-modal "
                          "pair, the block set's video->text and video->audio-keys calls), "
                          "--steps times each (for counter passes)")
+    ap.add_argument("--gemma-only", action="store_true",
+                    help="only run the Gemma-4 encoder attention (sliding and full layer at "
+                         "1024 tokens), --steps timed calls each")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB, --steps times "
                          "(the known-size kernel that scales FETCH_SIZE / WRITE_SIZE counters)")
@@ -621,6 +624,11 @@ def main():
             L.linear(xin, w, out=y, sumsq=True)
         torch.cuda.synchronize()
         print(json.dumps({"projection": [12480, 4096, 4096], "launches": args.steps}), flush=True)
+        return
+
+    if args.gemma_only:
+        res = bench_gemma(device, args.steps, args.warmup)
+        print(json.dumps({"gemma_text_encoder_attn": res}), flush=True)
         return
 
     if args.short_keys_only:
