@@ -7,11 +7,15 @@
 //                       RMS norm (fp32, pow(mean + eps, -0.5), times the weight), rotate_half
 //                       RoPE with the fp32 tables,
 //                       q scaled by scale*log2(e). Writes q' as two bf16 parts (hi + lo)
-//                       [B][Hq][T][D], k' [B][Hkv][T][D] (one bf16 rounding, as the
-//                       reference rounds its normed k).
-//   gemma_vt_kernel     v with the weightless per-head norm, written TRANSPOSED,
-//                       [B][Hkv][D][T] (through an LDS tile of 64 tokens), so that the P.V
-//                       operand (one channel, eight keys per lane) is two 8-byte loads.
+//                       [B][Hq][T][D], and k' (one bf16 rounding, as the reference rounds its
+//                       normed k) in MFMA operand order: per (batch row, KV head, 32-key block)
+//                       D/16 units of 1 KB, lane r + 32g of unit c holding channels
+//                       16c + 8g .. +7 of key r.
+//   gemma_vt_kernel     v with the weightless per-head norm, transposed through an LDS tile of
+//                       one 32-key block into operand order: per key half hf and 32-channel
+//                       block cb one 1 KB unit, lane r + 32g holding channel 32cb + r at keys
+//                       16hf + 4g + {0..3, 8..11}. Keys past T are zeros in both layouts, and
+//                       every operand of the attention is one coalesced 16-byte load per lane.
 //   gemma_attn_kernel   one workgroup of four waves per (batch row, query head, 32 queries);
 //                       the waves split the head dim into four slices of D/4 channels. Per
 //                       32-key block each wave forms the partial S^T = K.Q'^T over its slice
