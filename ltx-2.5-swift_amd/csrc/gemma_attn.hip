@@ -39,9 +39,13 @@ constexpr int kGemmaQB = 32;       // queries per workgroup
 // ---- prologue ------------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p) {
-    constexpr int E = D / 64;                       // channels per lane: 4 or 8
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    // 8 channels per lane: a row of D = 512 takes a wave, a row of D = 256 half a wave
+    constexpr int E = 8;
+    constexpr int LPR = D / E;                      // lanes per row: 64 or 32
+    constexpr int RPW = 64 / LPR;                   // rows per wave
+    const int lane = threadIdx.x & (LPR - 1);       // lane within the row
+    const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW +
+                        ((threadIdx.x & 63) / LPR);
     const int heads = p.Hq + p.Hkv;                 // q heads, then k heads, per token
     if (row >= (int64_t)p.B * p.T * heads) return;
     const int hr = (int)(row % heads);
@@ -53,43 +57,35 @@ __global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p
                                 : (const bf16 *)p.k + (int64_t)b * p.k_bs + (int64_t)t * p.k_rs;
     src += (int64_t)h * D + lane * E;
     float x[E];
-    if constexpr (E == 8) {
-        unpack8(ldg16(src), x);
-    } else {
-        const u32x2 w = *(const u32x2 *)src;
-        x[0] = bf_lo(w[0]); x[1] = bf_hi(w[0]); x[2] = bf_lo(w[1]); x[3] = bf_hi(w[1]);
-    }
+    unpack8(ldg16(src), x);
+    // the reductions and the partner exchange stay within the row's lanes (offsets < LPR)
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < E; ++e) ss += x[e] * x[e];
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    for (int off = LPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
     const float rs = powf(ss / (float)D + p.eps, -0.5f);
     const bf16 *w = (const bf16 *)(kind == 0 ? p.q_w : p.k_w) + lane * E;
 #pragma unroll
     for (int e = 0; e < E; ++e) x[e] = (x[e] * rs) * (float)w[e];
     // rotate_half pairs channel c with c +- D/2: lane l holds channels E*l ..; its partner is
-    // lane l ^ 32. Table column of channel c is c mod D/2.
-    const int col = (lane & 31) * E;
+    // lane l ^ LPR/2. Table column of channel c is c mod D/2.
+    const int col = (lane & (LPR / 2 - 1)) * E;
     const float *cs = p.cos + (int64_t)t * (D / 2) + col;
     const float *sn = p.sin + (int64_t)t * (D / 2) + col;
-    const bool first = lane < 32;
+    const bool first = lane < LPR / 2;
     const float f = kind == 0 ? p.q_factor : 1.0f;
     float y[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        const float other = __shfl_xor(x[e], 32, 64);
+        const float other = __shfl_xor(x[e], LPR / 2, 64);
         const float c = cs[e], s = sn[e];
         // first half: x1 c - x2 s; second half: x2 c + x1 s
         y[e] = (first ? x[e] * c - other * s : x[e] * c + other * s) * f;
     }
     // q as two bf16 parts (hi + lo carries ~16 significant bits into the products); k as one
     auto put = [&](bf16 *dst, const float (&z)[E]) __attribute__((always_inline)) {
-        if constexpr (E == 8) {
-            *(u32x4 *)dst = pack8(z);
-        } else {
-            *(u32x2 *)dst = u32x2{pack_bf2(z[0], z[1]), pack_bf2(z[2], z[3])};
-        }
+        *(u32x4 *)dst = pack8(z);
     };
     if (kind == 1) {
         // k' in operand order: 32-key block t/32, 16-channel chunk c, lane (t%32) + 32g holds
@@ -371,8 +367,10 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
 }  // namespace
 
 int launch_gemma_prep(const GemmaPrepParams &p, int D, void *stream) {
+    // rows per workgroup: four waves of one (D = 512) or two (D = 256) rows
     const int64_t rows = (int64_t)p.B * p.T * (p.Hq + p.Hkv);
-    const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+    const int64_t rows_wg = D == 512 ? 4 : 8;
+    const dim3 grid((unsigned)((rows + rows_wg - 1) / rows_wg)), block(256);
     const dim3 vgrid((unsigned)((int64_t)p.B * p.Hkv * ((p.T + 31) / 32)));
     hipStream_t st = (hipStream_t)stream;
     if (D == 512) {
