@@ -21,8 +21,9 @@
  * Contract of ltx_attn_fwd (all of it checked on the host before anything is launched):
  *   - no allocation: scratch memory is the caller's `workspace`, sized by
  *     ltx_attn_workspace_bytes() for the same arguments;
- *   - no hidden global mutable state; reentrant across streams and threads (the detail
- *     string of the last failure is thread-local, like dlerror);
+ *   - no hidden global mutable state beyond a per-device cache of the CU count the work
+ *     split is planned over (written once per device, idempotent); reentrant across streams
+ *     and threads (the detail string of the last failure is thread-local, like dlerror);
  *   - asynchronous on `stream`; inputs must stay valid until the stream reaches the call.
  */
 #ifndef LTX_ATTN_H
@@ -35,7 +36,7 @@
 extern "C" {
 #endif
 
-#define LTX_ATTN_ABI_VERSION 5
+#define LTX_ATTN_ABI_VERSION 6
 
 /* Status codes. The reference throws `DiTAttention.Failure` for structural errors
  * (DiTAttention.swift:107-121); a Swift wrapper maps these onto thrown errors. */
@@ -289,6 +290,31 @@ ltx_attn_status ltx_gemma_attn_fwd(const ltx_gemma_attn_args *a, void *stream);
 int32_t ltx_gemma_rope_tables(int32_t tokens, int32_t head_dim, double theta,
                               double partial_factor, int32_t proportional, float *cos_out,
                               float *sin_out);
+
+/* ----------------------------------------------------------------------------------------
+ * The HIP device. The reference measures its machine rather than assuming it
+ * (Sources/LTXHardware/Machine.swift:12-30, Machine.detect()); a host that selects the HIP
+ * attention path explicitly describes the device it selected with these.
+ * -------------------------------------------------------------------------------------- */
+typedef struct ltx_device_info {
+    int32_t ordinal;
+    int32_t compute_units;        /* CUs (256 on an MI355X); the attention kernels run one     */
+                                  /* workgroup per CU and plan their tail splits over them     */
+    int64_t memory_bytes;         /* device memory (HBM) capacity                              */
+    int32_t clock_khz;            /* peak shader clock                                         */
+    int32_t lds_bytes_per_cu;     /* LDS per CU (160 KiB on gfx950)                            */
+    int32_t supported;            /* 1 if the device is gfx950, the architecture the library's */
+                                  /* kernels are built for; 0 otherwise                        */
+    char name[128];               /* marketing name                                            */
+    char arch[64];                /* gcnArchName, e.g. "gfx950:sramecc+:xnack-"               */
+} ltx_device_info;
+
+/* Visible HIP devices (0 when there is none or the runtime cannot start). */
+int32_t ltx_device_count(void);
+
+/* Describe device `ordinal` (LTX_ATTN_EINVAL for a bad ordinal or NULL, LTX_ATTN_EHIP if the
+ * runtime fails). Does not change the current device. */
+ltx_attn_status ltx_device_query(int32_t ordinal, ltx_device_info *out);
 
 #ifdef __cplusplus
 }

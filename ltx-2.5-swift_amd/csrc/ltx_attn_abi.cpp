@@ -13,6 +13,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <utility>
 
 #include "../../include/ltx_attn.h"
@@ -34,8 +35,32 @@ bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// Workgroups resident at once on an MI355X: 256 CUs, one 256-thread attention workgroup each.
-constexpr int64_t kConcurrentGroups = 256;
+// Attention workgroups resident at once: one per CU of the device current at the call (each
+// workgroup holds most of a CU's LDS). Queried once per device; an MI355X's 256 CUs when no
+// device is visible (pure host use of the planner, e.g. sizing a workspace ahead of time).
+constexpr int64_t kDefaultConcurrentGroups = 256;
+std::atomic<int32_t> g_device_cus[64];
+
+int64_t concurrent_groups() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+        (void)hipGetLastError();
+        return kDefaultConcurrentGroups;
+    }
+    if (dev >= 64) return kDefaultConcurrentGroups;
+    int32_t cus = g_device_cus[dev].load(std::memory_order_relaxed);
+    if (cus <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0) {
+            (void)hipGetLastError();
+            return kDefaultConcurrentGroups;
+        }
+        cus = n;
+        g_device_cus[dev].store(cus, std::memory_order_relaxed);
+    }
+    return cus;
+}
 // Charge per extra split of a tail item, in rounds: its fp32 partial O is written and read
 // back by the combine kernel.
 constexpr double kSplitCharge = 0.02;
@@ -195,6 +220,7 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
     // 32-bit byte offsets up to the key length padded to whole tiles; calls past that take
     // the register-staged kernel.
     const bool k_work = pl->k_norm || pl->k_rope;
+    const int64_t kConcurrentGroups = concurrent_groups();
     // Short key ranges (text cross-attention over its valid keys, video queries over the
     // audio keys) take the short-key kernel: the head's K (prepared by the prologue, only
     // its valid rows, when it needs norm/RoPE) and V stay in LDS while the queries stream
@@ -605,6 +631,37 @@ const char *ltx_attn_provenance(void) {
 int32_t ltx_attn_abi_version(void) { return LTX_ATTN_ABI_VERSION; }
 
 size_t ltx_attn_args_size(void) { return sizeof(ltx_attn_args); }
+
+int32_t ltx_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+ltx_attn_status ltx_device_query(int32_t ordinal, ltx_device_info *out) {
+    g_err[0] = 0;
+    if (!out) return fail(LTX_ATTN_EINVAL, "out is NULL");
+    const int32_t n = ltx_device_count();
+    if (ordinal < 0 || ordinal >= n)
+        return fail(LTX_ATTN_EINVAL, "device %d outside [0, %d)", ordinal, n);
+    hipDeviceProp_t prop;
+    if (hipError_t e = hipGetDeviceProperties(&prop, ordinal))
+        return fail(LTX_ATTN_EHIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    memset(out, 0, sizeof *out);
+    out->ordinal = ordinal;
+    out->compute_units = prop.multiProcessorCount;
+    out->memory_bytes = (int64_t)prop.totalGlobalMem;
+    out->clock_khz = prop.clockRate;
+    out->lds_bytes_per_cu = (int32_t)prop.maxSharedMemoryPerMultiProcessor;
+    snprintf(out->name, sizeof out->name, "%s", prop.name);
+    snprintf(out->arch, sizeof out->arch, "%s", prop.gcnArchName);
+    out->supported = strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
+                     (prop.gcnArchName[6] == 0 || prop.gcnArchName[6] == ':');
+    return LTX_ATTN_OK;
+}
 
 int32_t ltx_linear_sumsq_blocks(int32_t N) {
     return N <= 0 ? 0 : (N + LTX_LINEAR_SUMSQ_COLS - 1) / LTX_LINEAR_SUMSQ_COLS;

@@ -4,8 +4,12 @@
 //   phase 1  attn1 (video self), audio_attn1 (audio self)            :343-368
 //            each may be fully perturbed (STG passthrough, DiTForward.swift:1009-1010)
 //   phase 2  attn2 (video <- text), audio_attn2 (audio <- text)      :370-381
-//            text K/V with a valid length per batch row (CFG: the conditional and the
-//            unconditional prompt rows differ), never rotated
+//            text K/V (the modulated connector features, all 1024 tokens), never rotated.
+//            The reference attends over every text token with no mask (DiTForward.swift:38-42
+//            passes none; DiTAttention.swift:374-376 runs mask: .none), so a caller matching
+//            it passes text_valid_len = nullptr. Per-row valid lengths are an extension of
+//            this library (key padding, e.g. prompts whose padding was never modulated) and
+//            give different outputs from the reference's.
 //   phase 3  audio_to_video, then video_to_audio                     :383-435
 //            queries and contexts from the pre-cross-modal snapshot of both streams; pe is
 //            the query stream's cross grid, k_pe the other stream's (crossed over)
@@ -69,8 +73,9 @@ public:
             audioPerturbed, workspace, workspace_bytes, stream);
     }
 
-    // Phase 2: text cross-attention of both streams (:370-381). `text_valid_len`: host array
-    // of `batch` counts (the prompt rows' valid tokens), or null when every row is full.
+    // Phase 2: text cross-attention of both streams (:370-381). `text_valid_len`: null for
+    // the reference's arithmetic (every text token attended, no mask); or a host array of
+    // `batch` counts when the caller wants key padding (keys past the count ignored).
     void textCross(int32_t batch, const Call &video, const Call &audio,
                    const int32_t *text_valid_len, void *workspace, size_t workspace_bytes,
                    void *stream) const {

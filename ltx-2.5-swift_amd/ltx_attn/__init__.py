@@ -119,8 +119,18 @@ EXPORTED_SYMBOLS = (
     "ltx_attn_abi_version", "ltx_attn_args_size", "ltx_rope_frequency_grid", "ltx_rope_video_positions",
     "ltx_rope_audio_positions", "ltx_rope_tables", "ltx_rope_tables_device",
     "ltx_linear", "ltx_linear_sumsq_blocks", "ltx_gemma_attn_workspace_bytes",
-    "ltx_gemma_attn_fwd", "ltx_gemma_rope_tables",
+    "ltx_gemma_attn_fwd", "ltx_gemma_rope_tables", "ltx_device_count", "ltx_device_query",
 )
+
+
+class DeviceInfo(ctypes.Structure):
+    """``ltx_device_info`` (include/ltx_attn.h)."""
+    _fields_ = [
+        ("ordinal", ctypes.c_int32), ("compute_units", ctypes.c_int32),
+        ("memory_bytes", ctypes.c_int64), ("clock_khz", ctypes.c_int32),
+        ("lds_bytes_per_cu", ctypes.c_int32), ("supported", ctypes.c_int32),
+        ("name", ctypes.c_char * 128), ("arch", ctypes.c_char * 64),
+    ]
 
 _lib = None
 
@@ -187,8 +197,22 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                           ctypes.c_double, ctypes.c_int32, ctypes.c_void_p,
                                           ctypes.c_void_p]
     lib.ltx_gemma_rope_tables.restype = ctypes.c_int32
+    lib.ltx_device_count.argtypes = []
+    lib.ltx_device_count.restype = ctypes.c_int32
+    lib.ltx_device_query.argtypes = [ctypes.c_int32, ctypes.POINTER(DeviceInfo)]
+    lib.ltx_device_query.restype = ctypes.c_int
     _lib = lib
     return lib
+
+
+def device_info(ordinal: int = 0) -> dict:
+    """The HIP device as the library sees it (``ltx_device_query``)."""
+    info = DeviceInfo()
+    _check(load_library().ltx_device_query(ordinal, ctypes.byref(info)))
+    return {"ordinal": info.ordinal, "compute_units": info.compute_units,
+            "memory_bytes": info.memory_bytes, "clock_khz": info.clock_khz,
+            "lds_bytes_per_cu": info.lds_bytes_per_cu, "supported": bool(info.supported),
+            "name": info.name.decode(), "arch": info.arch.decode()}
 
 
 def provenance() -> str:
@@ -583,7 +607,10 @@ class DiTBlockAttention:
                   all_perturbed=audio_perturbed)
 
     def text_cross(self, video, audio, text_valid_len=None, workspace=None):
-        """attn2 and audio_attn2 (:370-381): text K/V, valid tokens per batch row (CFG)."""
+        """attn2 and audio_attn2 (:370-381): text K/V, never rotated. ``text_valid_len=None``
+        is the reference's arithmetic: every text token is attended, with no mask
+        (DiTForward.swift:38-42, DiTAttention.swift:374-376). A list of per-row counts adds key
+        padding, an extension whose outputs differ from the reference's."""
         self._run(Variant.videoCross, video, workspace, k_valid_len=text_valid_len)
         self._run(Variant.audioCross, audio, workspace, k_valid_len=text_valid_len)
 

@@ -61,6 +61,9 @@ shift, per-pair RoPE norm, relative-position property of the rotation), a pure-P
 brute-force SDPA on tiny inputs, the independent C restatement in ``attn_oracle.c``, and the
 tiny_v5 manifest digests of the reference's RoPE tables
 (``Tests/Fixtures/goldens/tiny_v5/manifest.json``, keys ``block_00.*.in.kw_pe*``).
+``compare`` (the pass/fail gate of every GPU test) is pinned by hand-worked cases including
+the zero-reference branch; ``splitmix64`` by the published splitmix64 outputs for seed 0 and
+``splitmix_bf16_bits`` by a hand-rounded word and the half-step bound.
 """
 
 from __future__ import annotations
@@ -71,7 +74,7 @@ import numpy as np
 
 __all__ = [
     "f32_to_bf16_bits", "bf16_bits_to_f32", "round_bf16", "randn_bf16_bits",
-    "splitmix_bf16_bits", "rms_norm", "split_rope", "sdpa", "head_gate", "attention",
+    "splitmix64", "splitmix_bf16_bits", "rms_norm", "split_rope", "sdpa", "head_gate", "attention",
     "linear", "sumsq_partials", "attention_module",
     "frequency_grid", "video_positions", "audio_positions", "rotary_tables",
     "rotaries", "compare",
@@ -110,24 +113,37 @@ def randn_bf16_bits(shape, seed: int, mean: float = 0.0, std: float = 1.0) -> np
     return f32_to_bf16_bits(x)
 
 
-def splitmix_bf16_bits(count: int, seed: int) -> np.ndarray:
-    """The reference bench's operand stream: splitmix64 -> uniform [-1, 1) -> bf16.
+SPLITMIX_GAMMA = 0x9E3779B97F4A7C15
 
-    Restates ``BenchOperand.bits(count:seed:)`` (``Sources/ltx/Bench.swift:479-493``).
+
+def splitmix64(count: int, seed: int) -> np.ndarray:
+    """The 64-bit words behind the reference bench's operands (``Bench.swift:479-490``).
+
+    The state starts at ``seed + gamma`` and is advanced by ``gamma`` BEFORE each word is
+    mixed, so word ``i`` is the standard splitmix64 output ``i + 1`` of a generator seeded
+    with ``seed`` (the first output of the standard generator is skipped).
     """
     mask = (1 << 64) - 1
-    golden = 0x9E3779B97F4A7C15
-    state = (seed + golden) & mask
-    out = np.empty(count, dtype=np.float32)
+    state = (seed + SPLITMIX_GAMMA) & mask
+    out = np.empty(count, dtype=np.uint64)
     for i in range(count):
-        state = (state + golden) & mask
+        state = (state + SPLITMIX_GAMMA) & mask
         z = state
         z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
         z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
-        z ^= z >> 31
-        unit = np.float32(z >> 40) / np.float32(1 << 24)
-        out[i] = (unit - np.float32(0.5)) * np.float32(2)
-    return f32_to_bf16_bits(out)
+        out[i] = z ^ (z >> 31)
+    return out
+
+
+def splitmix_bf16_bits(count: int, seed: int) -> np.ndarray:
+    """The reference bench's operand stream: splitmix64 -> uniform [-1, 1) -> bf16.
+
+    Restates ``BenchOperand.bits(count:seed:)`` (``Sources/ltx/Bench.swift:479-493``): the
+    top 24 bits of each word over 2^24 (exact in fp32), centred and doubled, RNE to bf16.
+    """
+    top = (splitmix64(count, seed) >> np.uint64(40)).astype(np.float32)
+    unit = top / np.float32(1 << 24)
+    return f32_to_bf16_bits((unit - np.float32(0.5)) * np.float32(2))
 
 
 # --------------------------------------------------------------------------------------

@@ -23,7 +23,7 @@ GOLDEN = os.path.join(ROOT, "tests", "golden")
 def _declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ltx_(?:attn_|rope_|linear|gemma_)\w*)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(ltx_(?:attn_|rope_|linear|gemma_|device_)\w*)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layout_and_version():
     lib = L.load_library()
     assert lib.ltx_attn_args_size() == ctypes.sizeof(L.Args)
-    assert lib.ltx_attn_abi_version() == 5
+    assert lib.ltx_attn_abi_version() == 6
     assert "gfx950" in L.provenance()
     for s in range(5):
         assert lib.ltx_attn_status_string(s)

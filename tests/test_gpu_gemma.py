@@ -68,6 +68,18 @@ CASES = {
     "sliding_window40_T100_B2": dict(B=2, T=100, kind="sliding", fv=[0, 37], window=40,
                                      seed=0x5EED + 440),
     "full_T68_B2": dict(B=2, T=68, kind="full", fv=[67, 3], seed=0x5EED + 450),
+    # a fully padded prompt (first_valid == T): no row has an allowed key, so every row
+    # attends to all keys unmasked (GemmaTextEncoder.swift:306-319)
+    "sliding_T100_fully_padded": dict(B=1, T=100, kind="sliding", fv=[100], seed=0x5EED + 460),
+    "full_T64_B2_one_fully_padded": dict(B=2, T=64, kind="full", fv=[64, 10],
+                                         seed=0x5EED + 470),
+    # windows below one 32-key block: the key range starts and ends inside a block
+    "sliding_window1_T92": dict(B=1, T=92, kind="sliding", fv=[0], window=1, seed=0x5EED + 480),
+    "sliding_window17_T92_B2": dict(B=2, T=92, kind="sliding", fv=[0, 50], window=17,
+                                    seed=0x5EED + 490),
+    # 8 KV heads at a ragged length with a window and padding in the same prompt
+    "sliding_window17_T76_pad5": dict(B=1, T=76, kind="sliding", fv=[5], window=17,
+                                      seed=0x5EED + 500),
 }
 
 

@@ -79,6 +79,20 @@ def run(device, q, k, v, heads, **kw):
     return host_f32(out)
 
 
+def test_device_query(device):
+    """ltx_device_query describes the MI355X the tests run on (the device a Swift host
+    selects explicitly, and whose CU count the work split is planned over)."""
+    info = L.device_info(0)
+    _say(f"device: {info}")
+    assert info["supported"] and info["arch"].startswith("gfx950")
+    assert info["compute_units"] == 256
+    assert info["memory_bytes"] > 250e9
+    assert info["lds_bytes_per_cu"] >= 160 * 1024
+    assert L.load_library().ltx_device_count() >= 1
+    with pytest.raises(L.Failure):
+        L.device_info(L.load_library().ltx_device_count())
+
+
 # ---------------------------------------------------------------------------------------
 # The reference's own attention test, through MLXFast's signature
 # ---------------------------------------------------------------------------------------
@@ -417,7 +431,7 @@ def test_dit_attention_core_rules(device):
 
 
 # ---------------------------------------------------------------------------------------
-# The BASELINE shapes at full size; the oracle checks sampled heads and query ranges
+# The benchmark shapes at full size: every head and every query row against the C oracle
 # ---------------------------------------------------------------------------------------
 
 def _gpu_bits(shape, seed, device, mean=0.0, std=1.0):
@@ -440,24 +454,33 @@ def _index_rotary(indices, inner, heads):
     return O.rotary_tables(pos, inner, [20], heads)
 
 
-def _sample_check(device, tq, tk, tv, heads, bits, kw_host, kw_dev, ranges, hsel, label,
-                  **call_kw):
+def check_heads(got, truth, ref_out, label):
+    """The tolerance per (batch row, head) -- a wrong head cannot hide in the average of the
+    others -- besides the whole-output check. All arrays [B, Lq, H, D]."""
+    check(got, truth, ref_out, label)
+    g, t, r = (np.asarray(x, dtype=np.float64) for x in (got, truth, ref_out))
+    ssr = np.sum(t * t, axis=(1, 3))
+    rel = np.sqrt(np.sum((g - t) ** 2, axis=(1, 3)) / ssr)
+    rel_ref = np.sqrt(np.sum((r - t) ** 2, axis=(1, 3)) / ssr)
+    worst = np.unravel_index(int(np.argmax(rel / np.maximum(rel_ref, 2.5e-3))), rel.shape)
+    _say(f"  {label}: worst (b, h) = {tuple(int(i) for i in worst)}: relRMS {rel[worst]:.3e} "
+         f"(reference arithmetic {rel_ref[worst]:.3e})")
+    assert np.all(rel <= REL_RMS), (label, float(rel.max()))
+    assert np.all(rel <= np.maximum(rel_ref, 2.5e-3) * 1.25), (label, worst, float(rel[worst]))
+
+
+def _full_check(device, tq, tk, tv, heads, bits, kw_host, kw_dev, label, **call_kw):
+    """One call on the GPU; the C oracle over all heads and query rows, exact (fp32 after
+    the bf16 inputs) and with the reference's rounding points."""
     import torch
 
     out = L.attention_fwd(tq, tk, tv, heads=heads, **kw_dev, **call_kw)
     torch.cuda.synchronize()
     got = host_f32(out)
-    B, Lq, inner = got.shape
-    D = inner // heads
     qb, kb, vb = bits
-    for (q0, q1) in ranges:
-        for h in hsel:
-            truth = O.c_attention(qb, kb, vb, heads, mode="exact", heads_range=(h, h + 1),
-                                  q_range=(q0, q1), **kw_host)
-            refm = O.c_attention(qb, kb, vb, heads, mode="reference", heads_range=(h, h + 1),
-                                 q_range=(q0, q1), **kw_host)
-            g = got[:, q0:q1, h * D:(h + 1) * D].reshape(truth.shape)
-            check(g, truth, O.round_bf16(refm), f"{label} h={h} q=[{q0},{q1})")
+    truth = O.c_attention(qb, kb, vb, heads, mode="exact", **kw_host)
+    refm = O.round_bf16(O.c_attention(qb, kb, vb, heads, mode="reference", **kw_host))
+    check_heads(got.reshape(truth.shape), truth, refm, label)
 
 
 def test_c1_video_self_3120(device):
@@ -466,8 +489,19 @@ def test_c1_video_self_3120(device):
     tq, qb = _gpu_bits(shape, 0x5EED, device)
     tk, kb = _gpu_bits(shape, 0x5EED + 1, device)
     tv, vb = _gpu_bits(shape, 0x5EED + 2, device)
-    _sample_check(device, tq, tk, tv, 32, (qb, kb, vb), {}, {}, [(0, 96), (3024, 3120)],
-                  [0, 31], "c1")
+    _full_check(device, tq, tk, tv, 32, (qb, kb, vb), {}, {}, "c1")
+
+
+def test_c1_splitmix_operands(device):
+    """The 3120-token self-attention on the reference bench's own operand stream (splitmix64
+    -> uniform [-1, 1) -> bf16, Bench.swift:479-493; seeds 0x5EED + k as BenchGEMM.swift
+    :627-632) instead of N(0, 1) draws."""
+    shape = (1, 3120, 4096)
+    n = int(np.prod(shape))
+    bits = [O.splitmix_bf16_bits(n, 0x5EED + i).reshape(shape) for i in range(3)]
+    _say("c1 with splitmix64 operands")
+    tq, tk, tv = (dev(b, device) for b in bits)
+    _full_check(device, tq, tk, tv, 32, tuple(bits), {}, {}, "c1 splitmix")
 
 
 @pytest.mark.parametrize("B,valid", [(1, [94]), (2, [94, 1])])
@@ -476,8 +510,8 @@ def test_c2_text_cross_masked(device, B, valid):
     tq, qb = _gpu_bits((B, 3120, 4096), 0x5EED + 10, device)
     tk, kb = _gpu_bits((B, 1024, 4096), 0x5EED + 11, device)
     tv, vb = _gpu_bits((B, 1024, 4096), 0x5EED + 12, device)
-    _sample_check(device, tq, tk, tv, 32, (qb, kb, vb), {"valid_len": valid},
-                  {"k_valid_len": valid}, [(0, 64), (3056, 3120)], [0, 13], "c2")
+    _full_check(device, tq, tk, tv, 32, (qb, kb, vb), {"valid_len": valid},
+                {"k_valid_len": valid}, "c2")
 
 
 @pytest.mark.parametrize("kprep", [L.KPREP_PROLOGUE, L.KPREP_FUSED])
@@ -491,9 +525,8 @@ def test_whole_and_tail_items_ragged(device, kprep):
     tq, qb = _gpu_bits((B, Lq, H * 128), 0x5EED + 40, device)
     tk, kb = _gpu_bits((B, Lk, H * 128), 0x5EED + 41, device)
     tv, vb = _gpu_bits((B, Lk, H * 128), 0x5EED + 42, device)
-    _sample_check(device, tq, tk, tv, H, (qb, kb, vb), {"valid_len": valid},
-                  {"k_valid_len": valid}, [(0, 64), (2036, 2100)], [0, 24, 31],
-                  "whole+tail", kprep=kprep)
+    _full_check(device, tq, tk, tv, H, (qb, kb, vb), {"valid_len": valid},
+                {"k_valid_len": valid}, "whole+tail", kprep=kprep)
 
 
 @pytest.mark.parametrize("direction", ["video_q", "audio_q"])
@@ -514,9 +547,7 @@ def test_c3_cross_modal(device, direction):
     kw_host = dict(q_cos=qt[0], q_sin=qt[1], k_cos=kt[0], k_sin=kt[1])
     kw_dev = dict(rotary=L.Rotary(dev(qt[0], device), dev(qt[1], device)),
                   key_rotary=L.Rotary(dev(kt[0], device), dev(kt[1], device)))
-    ranges = [(0, 64), (Lq - 62, Lq)]
-    _sample_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, ranges, [0, 31],
-                  f"c3 {direction}")
+    _full_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, f"c3 {direction}")
 
 
 @pytest.mark.parametrize("kprep", [L.KPREP_PROLOGUE, L.KPREP_FUSED])
@@ -531,57 +562,90 @@ def test_c4_stage2_self_12480_norm_rope(device, kprep):
     cos, sin = L.rope_tables(L.rope_video_positions(13, 24, 40), H * D, [20, 2048, 2048], H)
     kw_host = dict(q_norm_w=wqb, k_norm_w=wkb, q_cos=cos, q_sin=sin)
     kw_dev = dict(q_norm_w=wq, k_norm_w=wk, rotary=L.Rotary(dev(cos, device), dev(sin, device)))
-    _sample_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev,
-                  [(0, 64), (6200, 6264), (T - 64, T)], [0, 17, 31], "c4", kprep=kprep)
+    _full_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, "c4", kprep=kprep)
 
 
-def test_c5_block_set(device):
-    """One DiT block's six attentions at B=2 (15360 video, 152 audio, 1024 text with 94
-    valid), with norm + RoPE where the reference applies it (DiTBlock.swift:343-438)."""
+C5_CASES = [
+    # label, query stream (tokens, width), key stream, D, q table, k table, text keys valid
+    ("attn1", ("v", 4096), ("v", 4096), 128, "videoSelf", None, None),
+    ("audio_attn1", ("a", 2048), ("a", 2048), 64, "audioSelf", None, None),
+    ("attn2", ("v", 4096), ("t", 4096), 128, None, None, [94, 94]),
+    ("audio_attn2", ("a", 2048), ("t", 2048), 64, None, None, [94, 94]),
+    ("audio_to_video", ("v", 2048), ("a", 2048), 64, "videoCross", "audioCross", None),
+    ("video_to_audio", ("a", 2048), ("v", 2048), 64, "audioCross", "videoCross", None),
+]
+
+
+@pytest.mark.parametrize("case", C5_CASES, ids=[c[0] for c in C5_CASES])
+def test_c5_block_set(device, case):
+    """One DiT block's six attentions at B=2 (15360 video, 152 audio, 1024 text tokens of
+    which 94 valid), with norm + RoPE where the reference applies it (DiTBlock.swift:343-438).
+    Q, K and V are separate draws and q_norm / k_norm separate weights, as the module's
+    projections and norms are, so an operand mix-up changes the output."""
     import torch
 
+    label, (qs, qw), (ks, kwid), D, qtab, ktab, vl = case
     H = 32
-    Tv, Ta, Tt = 15360, 152, 1024
-    vt = L.rotaries(121, 768, 1280, audio_tokens=Ta)
-    tabs = {k: (dev(c, device), dev(s, device)) for k, (c, s) in vt.items()}
+    tokens = {"v": 15360, "a": 152, "t": 1024}
+    seed = 0x5EED + 50 + 10 * C5_CASES.index(case)
+    _say(f"c5 {label}: Lq {tokens[qs]} Lk {tokens[ks]} D {D}")
+    tq, qb = _gpu_bits((2, tokens[qs], qw), seed, device)
+    tk, kb = _gpu_bits((2, tokens[ks], kwid), seed + 1, device)
+    tv, vb = _gpu_bits((2, tokens[ks], kwid), seed + 2, device)
+    wq, wqb = _gpu_bits((qw,), seed + 3, device, 1.0, 0.02)
+    wk, wkb = _gpu_bits((kwid,), seed + 4, device, 1.0, 0.02)
+    kw_host = dict(q_norm_w=wqb, k_norm_w=wkb)
+    kw_dev = dict(q_norm_w=wq, k_norm_w=wk)
+    if qtab or ktab:
+        vt = L.rotaries(121, 768, 1280, audio_tokens=tokens["a"])
+    if qtab:
+        kw_host.update(q_cos=vt[qtab][0], q_sin=vt[qtab][1])
+        kw_dev["rotary"] = L.Rotary(dev(vt[qtab][0], device), dev(vt[qtab][1], device))
+    if ktab:
+        kw_host.update(k_cos=vt[ktab][0], k_sin=vt[ktab][1])
+        kw_dev["key_rotary"] = L.Rotary(dev(vt[ktab][0], device), dev(vt[ktab][1], device))
+    if vl:
+        kw_host["valid_len"] = vl
+        kw_dev["k_valid_len"] = vl
+    _full_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, f"c5 {label}")
+    torch.cuda.synchronize()
+
+
+def test_text_cross_unmasked_as_the_dit_calls_it(device):
+    """The DiT's attn2 / audio_attn2 attend over every text token with no mask
+    (DiTForward.swift:38-42 passes no mask; DiTAttention.swift:374-376 runs mask: .none):
+    the block driver's text_cross with no valid lengths over 1024 modulated connector
+    tokens, B = 2, against the oracle's unmasked attention over all 1024 keys."""
+    import torch
+
+    B, Tv, Ta, Tt, H = 2, 3120, 126, 1024, 32
+    _say(f"text cross, unmasked: {Tv} video / {Ta} audio queries over {Tt} text keys")
+    seed = 0x5EED + 300
+    wv, wvb = _gpu_bits((4096,), seed, device, 1.0, 0.02)
+    wa, wab = _gpu_bits((2048,), seed + 1, device, 1.0, 0.02)
+    wkv, wkvb = _gpu_bits((4096,), seed + 2, device, 1.0, 0.02)
+    wka, wkab = _gpu_bits((2048,), seed + 3, device, 1.0, 0.02)
     streams = {}
-    for name, T, inner, seed in (("v", Tv, 4096, 50), ("a", Ta, 2048, 60),
-                                 ("t4096", Tt, 4096, 70), ("t2048", Tt, 2048, 80),
-                                 ("v2048", Tv, 2048, 90)):
-        streams[name] = _gpu_bits((2, T, inner), 0x5EED + seed, device)
-    w = {n: _gpu_bits((i,), 0x5EED + s, device, 1.0, 0.02)
-         for n, i, s in (("w4096", 4096, 100), ("w2048", 2048, 101))}
-    valid = [94, 94]
-    cases = [
-        # label, q stream, kv stream, D, norm, q table, k table, valid
-        ("attn1", "v", "v", 128, "w4096", "videoSelf", None, None),
-        ("audio_attn1", "a", "a", 64, "w2048", "audioSelf", None, None),
-        ("attn2", "v", "t4096", 128, "w4096", None, None, valid),
-        ("audio_attn2", "a", "t2048", 64, "w2048", None, None, valid),
-        ("audio_to_video", "v2048", "a", 64, "w2048", "videoCross", "audioCross", None),
-        ("video_to_audio", "a", "v2048", 64, "w2048", "audioCross", "videoCross", None),
-    ]
-    for label, qs, ks, D, wn, qtab, ktab, vl in cases:
-        _say(f"c5 {label}")
-        tq, qb = streams[qs]
-        tk, kb = streams[ks]
-        tv, vb = streams[ks]
-        kw_host = dict(q_norm_w=w[wn][1], k_norm_w=w[wn][1])
-        kw_dev = dict(q_norm_w=w[wn][0], k_norm_w=w[wn][0])
-        if qtab:
-            kw_host.update(q_cos=vt[qtab][0], q_sin=vt[qtab][1])
-            kw_dev["rotary"] = L.Rotary(*tabs[qtab])
-        if ktab:
-            kw_host.update(k_cos=vt[ktab][0], k_sin=vt[ktab][1])
-            kw_dev["key_rotary"] = L.Rotary(*tabs[ktab])
-        if vl:
-            kw_host["valid_len"] = vl
-            kw_dev["k_valid_len"] = vl
-        Lq = tq.shape[1]
-        ranges = [(0, min(64, Lq))] if Lq <= 256 else [(0, 64), (Lq - 64, Lq)]
-        _sample_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, ranges, [5],
-                      f"c5 {label}")
-        torch.cuda.synchronize()
+    for name, (T, inner, s) in {"vq": (Tv, 4096, 4), "tk4": (Tt, 4096, 5), "tv4": (Tt, 4096, 6),
+                                "aq": (Ta, 2048, 7), "tk2": (Tt, 2048, 8),
+                                "tv2": (Tt, 2048, 9)}.items():
+        streams[name] = _gpu_bits((B, T, inner), seed + s, device)
+    norms = {v.value: (wv, wkv) if v in (L.Variant.videoSelf, L.Variant.videoCross)
+             else (wa, wka) for v in L.Variant}
+    blk = L.DiTBlockAttention(norms)
+    vo = torch.empty_like(streams["vq"][0])
+    ao = torch.empty_like(streams["aq"][0])
+    blk.text_cross((streams["vq"][0], streams["tk4"][0], streams["tv4"][0], vo),
+                   (streams["aq"][0], streams["tk2"][0], streams["tv2"][0], ao))
+    torch.cuda.synchronize()
+    for label, out, (q, k, v), (w1, w2) in (("attn2", vo, ("vq", "tk4", "tv4"), (wvb, wkvb)),
+                                            ("audio_attn2", ao, ("aq", "tk2", "tv2"),
+                                             (wab, wkab))):
+        bits = tuple(streams[n][1] for n in (q, k, v))
+        kw = dict(q_norm_w=w1, k_norm_w=w2)
+        truth = O.c_attention(*bits, H, mode="exact", **kw)
+        refm = O.round_bf16(O.c_attention(*bits, H, mode="reference", **kw))
+        check_heads(host_f32(out).reshape(truth.shape), truth, refm, f"unmasked {label}")
 
 
 def test_block_driver_matches_single_calls(device):

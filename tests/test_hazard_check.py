@@ -88,3 +88,17 @@ def test_scratch_spill_is_caught(tmp_path):
     assert H.main(str(f)) == 1
     f.write_text(text.replace("316", "0"))
     assert H.main(str(f)) == 0
+
+
+def test_allowed_spill_is_bounded_by_its_size(tmp_path):
+    """--allow-spill SUBSTRING:BYTES admits one reviewed spill at its size, and nothing more:
+    a larger spill of that kernel or any spill of another kernel still fails."""
+    f = tmp_path / "k.s"
+    f.write_text("_Zknown:\n\ts_endpgm\n\t.set _Zknown.private_seg_size, 28\n"
+                 "_Zother:\n\ts_endpgm\n\t.set _Zother.private_seg_size, 0\n")
+    assert H.main(str(f)) == 1
+    assert H.main(str(f), [("known", 28)]) == 0
+    f.write_text("_Zknown:\n\ts_endpgm\n\t.set _Zknown.private_seg_size, 32\n")
+    assert H.main(str(f), [("known", 28)]) == 1
+    f.write_text("_Zother:\n\ts_endpgm\n\t.set _Zother.private_seg_size, 4\n")
+    assert H.main(str(f), [("known", 28)]) == 1

@@ -594,3 +594,65 @@ def test_gemma_attention_invariants():
     # shared K/V: V is the weightless norm of the raw K projection, not of the finished K
     sh = O.gemma_attention(q, k, k, Hq, Hkv, wq, wk, cos, sin)
     assert not np.allclose(sh, O.gemma_attention(q, k, v, Hq, Hkv, wq, wk, cos, sin))
+
+
+# ---------------------------------------------------------------------------------------
+# The comparison metric and the reference bench's operand stream (Sources/ltx/Bench.swift)
+# ---------------------------------------------------------------------------------------
+
+def test_compare_hand_computed_cases():
+    """BenchComparison (Bench.swift:508-536): relRMS = sqrt(sum (a-b)^2 / sum b^2) over the
+    reference b, maxAbs, and the fraction of equal bf16 patterns -- on cases worked by hand,
+    so a dropped square root (0.5), a denominator over the candidate (sqrt(1/5)) or a mean in
+    place of a maximum fails."""
+    c = O.compare([1.0, 2.0], [1.0, 1.0])
+    assert c["rel_rms"] == math.sqrt(0.5)
+    assert c["max_abs"] == 1.0
+    assert c["bit_identical"] == 0.5
+    assert c["elements"] == 2
+    # the reference is the denominator: swapping the operands changes the figure
+    assert O.compare([1.0, 1.0], [1.0, 2.0])["rel_rms"] == math.sqrt(1.0 / 5.0)
+    # a uniform 1% error is exactly 1e-2, maxAbs is the largest single difference
+    c = O.compare([1.01, -2.02, 0.0], [1.0, -2.0, 0.0])
+    assert abs(c["rel_rms"] - 1e-2) < 1e-12 and abs(c["max_abs"] - 0.02) < 1e-12
+    # sum b^2 == 0 (Bench.swift:532-534): 0 when the candidate is 0 too, else infinity
+    assert O.compare([0.0, 0.0], [0.0, 0.0])["rel_rms"] == 0.0
+    assert O.compare([0.0, 1e-3], [0.0, 0.0])["rel_rms"] == math.inf
+    # "bit identical" is on the bf16 patterns: values rounding to one bf16 are identical
+    c = O.compare([1.0 + 2.0 ** -10, 1.0 + 2.0 ** -6], [1.0, 1.0])
+    assert c["bit_identical"] == 0.5
+
+
+# The standard splitmix64 generator seeded with 0 (Vigna's published sequence, the one the
+# xoshiro family seeds from): its first six outputs.
+SPLITMIX64_SEED0 = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F,
+                    0xF88BB8A8724C81EC, 0x1B39896A51A8749B, 0x53CB9F0C747EA2EA]
+
+
+def test_splitmix64_stream_matches_published_values():
+    """Bench.swift:479-490 advances its state before mixing from a state that already holds
+    seed + gamma: its word i is the standard output i + 1. Seeding it with -gamma therefore
+    gives the standard sequence of seed 0 from its first word."""
+    mask = (1 << 64) - 1
+    got = O.splitmix64(6, (-O.SPLITMIX_GAMMA) & mask)
+    assert [int(x) for x in got] == SPLITMIX64_SEED0
+    got = O.splitmix64(5, 0)
+    assert [int(x) for x in got] == SPLITMIX64_SEED0[1:]
+
+
+def test_splitmix_bf16_operands():
+    """Words -> [-1, 1) -> bf16 (Bench.swift:488-491): the top 24 bits m give exactly
+    (m - 2^23) / 2^23. Worked by hand for the first standard word: m = 0xE220A8 = 14819496,
+    value 6430888 / 8388608 = 0.76662..., whose nearest bf16 (step 2^-8 in [0.5, 1)) is
+    196 / 256 = 0.765625 = 0x3F44. The whole stream stays in [-1, 1) and is within half a
+    bf16 step of its exact value."""
+    mask = (1 << 64) - 1
+    bits = O.splitmix_bf16_bits(6, (-O.SPLITMIX_GAMMA) & mask)
+    assert int(bits[0]) == 0x3F44
+    bits = O.splitmix_bf16_bits(4096, 0x5EED)
+    vals = O.bf16_bits_to_f32(bits).astype(np.float64)
+    exact = (O.splitmix64(4096, 0x5EED) >> np.uint64(40)).astype(np.float64) / 2.0 ** 23 - 1.0
+    assert np.all(vals >= -1.0) and np.all(vals <= 1.0)
+    half_step = np.exp2(np.floor(np.log2(np.maximum(np.abs(exact), 2.0 ** -126))) - 8)
+    assert np.all(np.abs(vals - exact) <= half_step)
+    assert abs(vals.mean()) < 0.05 and 0.5 < vals.std() < 0.65   # uniform: std 1/sqrt(3)
