@@ -656,8 +656,8 @@ ltx_attn_status ltx_device_query(int32_t ordinal, ltx_device_info *out) {
     out->memory_bytes = (int64_t)prop.totalGlobalMem;
     out->clock_khz = prop.clockRate;
     out->lds_bytes_per_cu = (int32_t)prop.maxSharedMemoryPerMultiProcessor;
-    snprintf(out->name, sizeof out->name, "%s", prop.name);
-    snprintf(out->arch, sizeof out->arch, "%s", prop.gcnArchName);
+    snprintf(out->name, sizeof out->name, "%.127s", prop.name);
+    snprintf(out->arch, sizeof out->arch, "%.63s", prop.gcnArchName);
     out->supported = strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
                      (prop.gcnArchName[6] == 0 || prop.gcnArchName[6] == ':');
     return LTX_ATTN_OK;
