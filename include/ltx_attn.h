@@ -152,6 +152,21 @@ ltx_attn_status ltx_attn_validate(const ltx_attn_args *a);
  * and, with gate_logits, the gate multiply of :395-399. */
 ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream);
 
+/* Bytes of the device scratch ltx_attn_fwd_static holds (128 MiB per device). */
+#define LTX_ATTN_STATIC_SCRATCH_BYTES ((size_t)128 << 20)
+
+/* ltx_attn_fwd for callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc. No counterpart in the
+ * reference (whose MLX arrays are allocated by MLX). The caller passes inputs and outputs;
+ * `workspace` / `workspace_bytes` are ignored: the call's scratch (statistics, prepared K,
+ * split-KV partials) is a file-scope device array of LTX_ATTN_STATIC_SCRATCH_BYTES per
+ * device, looked up on the first call on each device and held until the process ends. Same
+ * plan, kernels and results as ltx_attn_fwd. Calls needing more scratch than that (see
+ * ltx_attn_workspace_bytes) return LTX_ATTN_EUNSUPPORTED before anything is launched. The
+ * array is shared by every call on a device: calls that overlap on one device race, so the
+ * caller serialises them. Allocates nothing. */
+ltx_attn_status ltx_attn_fwd_static(const ltx_attn_args *a, void *stream);
+
 /* Static text for a status code. */
 const char *ltx_attn_status_string(ltx_attn_status s);
 

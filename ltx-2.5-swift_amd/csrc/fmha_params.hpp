@@ -2,6 +2,7 @@
 // (ltx_attn_abi.cpp). Plain data only: no HIP or torch types.
 #pragma once
 
+#include <stdarg.h>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -145,6 +146,10 @@ struct GemmaAttnParams {
     int32_t window;                  // 0: causal only
     int32_t first_valid[kMaxBatch];  // keys below are left padding
 };
+
+// Host side: set the calling thread's error detail (ltx_attn_last_error) from a printf
+// format and its va_list, and return `s`. Defined in ltx_attn_abi.cpp, not exported.
+__attribute__((visibility("hidden"))) int set_error_detail(int s, const char *fmt, va_list ap);
 
 // Launchers (fmha_fwd.hip). Return the hipError_t of the launch as int.
 // Attention kernels:

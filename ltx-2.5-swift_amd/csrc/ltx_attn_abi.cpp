@@ -387,6 +387,13 @@ ltx_attn_status gemma_plan(const ltx_gemma_attn_args *a, GemmaPlan *pl) {
 
 }  // namespace
 
+namespace ltx {
+int set_error_detail(int s, const char *fmt, va_list ap) {
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    return s;
+}
+}  // namespace ltx
+
 extern "C" {
 
 void ltx_attn_args_init(ltx_attn_args *a) {

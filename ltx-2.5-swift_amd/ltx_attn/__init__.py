@@ -120,7 +120,11 @@ EXPORTED_SYMBOLS = (
     "ltx_rope_audio_positions", "ltx_rope_tables", "ltx_rope_tables_device",
     "ltx_linear", "ltx_linear_sumsq_blocks", "ltx_gemma_attn_workspace_bytes",
     "ltx_gemma_attn_fwd", "ltx_gemma_rope_tables", "ltx_device_count", "ltx_device_query",
+    "ltx_attn_fwd_static",
 )
+
+# ltx_attn_fwd_static's per-device scratch (LTX_ATTN_STATIC_SCRATCH_BYTES)
+STATIC_SCRATCH_BYTES = 128 << 20
 
 
 class DeviceInfo(ctypes.Structure):
@@ -197,6 +201,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                           ctypes.c_double, ctypes.c_int32, ctypes.c_void_p,
                                           ctypes.c_void_p]
     lib.ltx_gemma_rope_tables.restype = ctypes.c_int32
+    lib.ltx_attn_fwd_static.argtypes = [P, ctypes.c_void_p]
+    lib.ltx_attn_fwd_static.restype = ctypes.c_int
     lib.ltx_device_count.argtypes = []
     lib.ltx_device_count.restype = ctypes.c_int32
     lib.ltx_device_query.argtypes = [ctypes.c_int32, ctypes.POINTER(DeviceInfo)]
@@ -307,7 +313,7 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
                   k_valid_len: Optional[Sequence[int]] = None, scale: Optional[float] = None,
                   out=None, kprep: int = KPREP_AUTO, num_splits: int = 0, stream=None,
                   workspace=None, events=None, gate_logits=None, all_perturbed: bool = False,
-                  q_sumsq=None, k_sumsq=None):
+                  q_sumsq=None, k_sumsq=None, no_alloc: bool = False):
     """One call of ``ltx_attn_fwd``. Tensors are torch bf16 on the current HIP device.
 
     ``layout="merged"``: q ``[B, Lq, H*D]``, k/v ``[B, Lk, H*D]``, out ``[B, Lq, H*D]``.
@@ -320,6 +326,9 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
     ``[B*L, blocks]`` views with a unit column stride, as ``linear(..., sumsq=True)`` returns
     them, column-sliced to the q / k range of a fused projection); the norm then takes its
     statistic from them. Both must have the same number of blocks.
+    ``no_alloc``: call ``ltx_attn_fwd_static`` instead, whose scratch is the library's own
+    per-device array (no workspace is made or passed; calls needing more than
+    ``STATIC_SCRATCH_BYTES`` raise ``Failure``).
     Returns ``out``.
     """
     import torch
@@ -401,6 +410,11 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
         setattr(a, name + "_rs", t.stride(0))
     if blocks is not None:
         a.sumsq_blocks = blocks
+    if stream is None:
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+    if no_alloc:
+        _check(lib.ltx_attn_fwd_static(ctypes.byref(a), ctypes.c_void_p(stream)))
+        return out
     need = lib.ltx_attn_workspace_bytes(ctypes.byref(a))
     st = lib.ltx_attn_validate(ctypes.byref(a))
     if st not in (OK, EWORKSPACE):
@@ -411,8 +425,6 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
         base = workspace.data_ptr()
         a.workspace = ctypes.c_void_p((base + 255) // 256 * 256)
         a.workspace_bytes = need
-    if stream is None:
-        stream = torch.cuda.current_stream(q.device).cuda_stream
     _check(lib.ltx_attn_fwd(ctypes.byref(a), ctypes.c_void_p(stream)))
     # keep the workspace alive until the stream has consumed it
     if need:
