@@ -34,6 +34,21 @@ METRIC = "attention TFLOP/s + % bf16 MFMA peak at 3120/12480 tokens; ms per DiT-
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_attn_c4.json")
+# The sources the dominant kernel is built from: a traffic figure counted on another version
+# of them is stale and not reported.
+KERNEL_SOURCES = [os.path.join(ROOT, "ltx-2.5-swift_amd", "csrc", f) for f in
+                  ("fmha_dma.hip", "fmha_device.hpp", "lds_copy.hpp", "fmha_params.hpp",
+                   "ltx_attn_abi.cpp")]
+
+
+def kernel_source_sha256():
+    import hashlib
+
+    h = hashlib.sha256()
+    for path in KERNEL_SOURCES:
+        with open(path, "rb") as fh:
+            h.update(os.path.basename(path).encode() + b"\0" + fh.read())
+    return h.hexdigest()
 
 
 class HipEvents:
@@ -124,6 +139,38 @@ def time_steps(call, steps, warmup, hip, events_per_step=True):
     return wall, kms
 
 
+def stats(samples_ms):
+    """Median, min, max and spread (max - min) / median of per-call times, the reference's
+    timing summary (Sources/ltx/Bench.swift:123-152)."""
+    xs = sorted(samples_ms)
+    n = len(xs)
+    med = xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2])
+    return {"median_ms": round(med, 4), "min_ms": round(xs[0], 4), "max_ms": round(xs[-1], 4),
+            "spread": round((xs[-1] - xs[0]) / med, 4) if med > 0 else None, "samples": n}
+
+
+def per_call_ms(call, steps, hip, stream=None):
+    """Each call's own time: HIP events recorded on the call's stream before and after it
+    (a separate run from the aggregate timing, which records nothing between calls)."""
+    import torch
+
+    st = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+    rt = hip.rt
+    rt.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    evs = [(hip.create(), hip.create()) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for a, b in evs:
+        rt.hipEventRecord(a, ctypes.c_void_p(st))
+        call(None)
+        rt.hipEventRecord(b, ctypes.c_void_p(st))
+    torch.cuda.synchronize()
+    ms = [hip.elapsed_ms(a, b) for a, b in evs]
+    for a, b in evs:
+        hip.destroy(a)
+        hip.destroy(b)
+    return ms
+
+
 def settle(call, seconds):
     """Run `call` untimed for `seconds` of wall time: on a fresh MI355X the kernel's duration
     falls by about a quarter over its first ~25 launches (the clock ramps up under load) and
@@ -161,11 +208,12 @@ def bench_c4(device, steps, warmup, hip, settle_s=0.0):
     settle(call, settle_s)
     wall, _ = time_steps(call, steps, warmup, hip, events_per_step=False)
     _, kms = time_steps(call, steps, 0, hip)
+    cms = per_call_ms(call, steps, hip)
     flops = 4.0 * T * T * H * D
     return x, {
         "flops": flops, "wall_s": wall, "ms_per_step": wall / steps * 1e3,
         "tflops": flops * steps / wall / 1e12,
-        "kernel_ms": sum(kms) / len(kms), "kernel_ms_min": min(kms), "kernel_ms_max": max(kms),
+        "kernel_ms": sum(kms) / len(kms), "kernel_stats": stats(kms), "call_stats": stats(cms),
         "kernel_tflops": flops / (sum(kms) / len(kms) * 1e-3) / 1e12,
         "bytes": 4.0 * T * H * D * 2,
     }
@@ -186,12 +234,15 @@ def bench_c1(device, steps, warmup, hip):
         L.attention_fwd(q, k, v, heads=H, out=out,
                         events=None if ev is None else (ev[0], ev[1]))
 
-    wall, kms = time_steps(call, steps, warmup, hip)
+    wall, _ = time_steps(call, steps, warmup, hip, events_per_step=False)
+    _, kms = time_steps(call, steps, 0, hip)
+    cms = per_call_ms(call, steps, hip)
     flops = 4.0 * T * T * H * D
     km = sum(kms) / len(kms)
     return {"tflops": flops * steps / wall / 1e12, "ms_per_call": wall / steps * 1e3,
             "kernel_ms": km, "kernel_tflops": flops / (km * 1e-3) / 1e12,
-            "pct_peak": 100.0 * flops / (km * 1e-3) / 1e12 / PEAK_BF16_TFLOPS}
+            "pct_peak": 100.0 * flops / (km * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+            "kernel_stats": stats(kms), "call_stats": stats(cms)}
 
 
 def bench_short_keys(device, steps, warmup, hip, block=True):
@@ -526,7 +577,13 @@ def cpu_baseline(x, budget_s):
     all 12480 keys, a contiguous block of queries, some heads."""
     import oracle as O
 
-    threads = min(16, os.cpu_count() or 1)
+    # Every core this process may run on, unless the host allots a smaller CPU share per GPU
+    # through OMP_NUM_THREADS (the GPU hosts here give each GPU 16 threads).
+    visible = len(os.sched_getaffinity(0))
+    threads = visible
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        threads = min(visible, int(omp))
     H, D, T = x["H"], x["D"], x["T"]
     qb, kb, vb = _host_bits(x["q"]), _host_bits(x["k"]), _host_bits(x["v"])
     wq, wk = _host_bits(x["wq"]), _host_bits(x["wk"])
@@ -558,8 +615,11 @@ def cpu_baseline(x, budget_s):
         pass
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": (f"{nh} head(s) x {nq} queries x {T} keys of the 12480-token workload "
-                       f"(norm + 3-D RoPE + explicit fp32 SDPA), {dt:.1f} s on {cpu}; "
-                       "substitute for the reference's MLX CPU path (mlx not installed)")}
+                       f"(norm + 3-D RoPE + explicit fp32 SDPA), {dt:.1f} s on {threads} "
+                       f"threads of {cpu}; substitute for the reference's MLX CPU path (mlx "
+                       "not installed)"),
+            "cpu_model": cpu, "host_cores_visible": visible, "isa": O.c_library_isa,
+            "seconds": round(dt, 2)}
 
 
 def main():
@@ -675,26 +735,37 @@ def main():
             "dit_block_attn_ms": round(c5["ms_per_block"], 4),
             "dit_block_attn_tflops": round(c5["tflops"], 2),
             "dit_block_attn_kernel_ms": c5["kernel_ms"],
-            "video_self_12480_kernel_ms_min_max": [round(c4["kernel_ms_min"], 4),
-                                                   round(c4["kernel_ms_max"], 4)],
+            "video_self_3120_kernel_time_stats": c1["kernel_stats"],
+            "video_self_3120_call_time_stats": c1["call_stats"],
             "rope_tables_12480_device_ms": round(rope["device_ms"], 4),
             "rope_tables_12480_host_build_upload_ms": round(rope["host_build_and_upload_ms"], 2),
             "projection": proj,
         }
 
-    traffic = None
+    traffic, traffic_note = None, "no counter pass recorded"
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as fh:
-            traffic = json.load(fh).get("hbm_bytes_per_launch")
+            rec = json.load(fh)
+        if rec.get("kernel_source_sha256") == kernel_source_sha256():
+            traffic = rec.get("hbm_bytes_per_launch")
+            traffic_note = (f"FETCH_SIZE x {rec.get('fetch_scale')} + WRITE_SIZE x "
+                            f"{rec.get('write_scale')} per dispatch, counted on these kernel "
+                            "sources (profiles/traffic_attn_video_self_12480.md)")
+        else:
+            traffic_note = "stale: the kernel sources changed since the last counter pass"
     achieved = c4["kernel_tflops"]
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                "traffic": traffic, "kernel": "fmha_dma_kernel<128>",
+                "traffic": traffic, "traffic_note": traffic_note,
+                "kernel": "fmha_dma_kernel<128>",
                 "kernel_avg_ms": round(c4["kernel_ms"], 4),
+                "kernel_time_stats": c4["kernel_stats"],
                 "flops_per_launch": c4["flops"]}
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(x, args.cpu_budget)
+        # GPU whole-call throughput over the CPU restatement's, same workload and FLOP count
+        cpu["speedup"] = round(c4["tflops"] / cpu["value"], 1)
 
     line = {
         "metric": METRIC,
@@ -705,6 +776,7 @@ def main():
         "warmup": args.warmup,
         "clock_settle_ms": args.settle_ms,
         "ms_per_step": round(c4["ms_per_step"], 4),
+        "step_time_stats": c4["call_stats"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

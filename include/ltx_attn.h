@@ -237,6 +237,38 @@ int32_t ltx_rope_video_positions(int32_t latent_frames, int32_t latent_height,
                                  int32_t spatial_scale, double frame_rate, float *out,
                                  int64_t cap);
 
+/* An in-context reference clip appended to the video stream (IC-LoRA references, the
+ * Multiple-Subject-Reference slots): DiTForward.Geometry.Reference (DiTForward.swift:220-252). */
+typedef struct ltx_rope_reference {
+    int32_t latent_frames, latent_height, latent_width;
+    int32_t downscale_factor;       /* target-over-reference spatial ratio (2: x2 upscaler)   */
+    int32_t temporal_scale_factor;  /* target-over-reference temporal ratio (1: spatial only) */
+    int32_t frame_offset;           /* time shift in PIXEL frames, added before the divide by */
+                                    /* the frame rate; MSR slot i of n: -(n - i); 0 otherwise */
+} ltx_rope_reference;
+
+/* referencePositions (DiTForward.swift:553-593): the reference's own patch grid built at frame
+ * rate 1 (time in pixel frames), + frame_offset, / float(frame_rate / temporal_scale_factor),
+ * then for temporal_scale_factor != 1 max(t - (factor - 1) * target_first_end, 0), and the
+ * spatial axes times downscale_factor. `target_first_end` is the target grid's first patch
+ * end ([0][0][1] of its positions). Writes bounds [3][tokens][2] with a token stride
+ * `row_tokens` >= tokens: (dim, token, side) at out[(dim*row_tokens + token)*2 + side].
+ * Returns tokens, or -1 (also when both frame_offset and temporal_scale_factor != 1 are set:
+ * the reference refuses that combination, :564-567). */
+int32_t ltx_rope_reference_positions(const ltx_rope_reference *ref, int32_t temporal_scale,
+                                     int32_t spatial_scale, double frame_rate,
+                                     float target_first_end, float *out, int64_t row_tokens);
+
+/* The video grid of a render with references (rotaries(geometry:dtype:), DiTForward.swift
+ * :698-711): the target's grid, then each reference's in order, every reference shifted
+ * against the target's own grid. [3][total][2], total = target tokens + all reference tokens
+ * (`videoTokensWithReference`); cap in floats. Returns total, or -1. */
+int32_t ltx_rope_video_positions_with_references(int32_t latent_frames, int32_t latent_height,
+                                                 int32_t latent_width, int32_t temporal_scale,
+                                                 int32_t spatial_scale, double frame_rate,
+                                                 const ltx_rope_reference *refs,
+                                                 int32_t n_refs, float *out, int64_t cap);
+
 /* audioPositions (DiTForward.swift:606-619): bounds [1][tokens][2] in seconds. */
 int32_t ltx_rope_audio_positions(int32_t tokens, int32_t hop_length, int32_t sample_rate,
                                  int32_t downsample, float *out, int64_t cap);

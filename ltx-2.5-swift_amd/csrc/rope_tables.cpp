@@ -80,6 +80,88 @@ int32_t ltx_rope_video_positions(int32_t latent_frames, int32_t latent_height,
     return (int32_t)tokens;
 }
 
+int32_t ltx_rope_reference_positions(const ltx_rope_reference *r, int32_t temporal_scale,
+                                     int32_t spatial_scale, double frame_rate,
+                                     float target_first_end, float *out, int64_t row_tokens) {
+    if (!r || !out || !(frame_rate > 0) || r->downscale_factor < 1 ||
+        r->temporal_scale_factor < 1)
+        return -1;
+    // An offset and a sparse-reference shift do not compose: the shift clamps time at zero
+    // and would erase the negative times the offset creates (DiTForward.swift:570-573).
+    if (r->frame_offset != 0 && r->temporal_scale_factor != 1) return -1;
+    const int64_t tokens = (int64_t)r->latent_frames * r->latent_height * r->latent_width;
+    if (r->latent_frames < 1 || r->latent_height < 1 || r->latent_width < 1 ||
+        tokens > INT32_MAX || row_tokens < tokens)
+        return -1;
+    // 1. the reference's own patch grid at frame rate 1: time stays in pixel frames (the
+    //    divide by 1.0f is exact, so the no-offset grid keeps its bits)
+    std::vector<float> grid((size_t)tokens * 6);
+    if (ltx_rope_video_positions(r->latent_frames, r->latent_height, r->latent_width,
+                                 temporal_scale, spatial_scale, 1.0, grid.data(),
+                                 (int64_t)grid.size()) != (int32_t)tokens)
+        return -1;
+    // 2.-3. the offset in pixel frames, then the reference's own time spacing
+    //       fps / temporalScaleFactor, the divisor rounded to float once
+    const float offset = (float)r->frame_offset;
+    const float spacing = (float)(frame_rate / (double)r->temporal_scale_factor);
+    // 4. a temporally sparse reference slides forward so its last patch ends where the
+    //    target's does: shift = (factor - 1) * the target's first patch end, clamped at 0
+    const float shift = (float)(r->temporal_scale_factor - 1) * target_first_end;
+    const float down = (float)r->downscale_factor;
+    for (int64_t tok = 0; tok < tokens; ++tok)
+        for (int side = 0; side < 2; ++side) {
+            float t = grid[(size_t)tok * 2 + side];
+            if (r->frame_offset != 0) t = t + offset;
+            t = t / spacing;
+            if (r->temporal_scale_factor != 1) {
+                t = t - shift;
+                if (t < 0.0f) t = 0.0f;                       // maximum(t, 0)
+            }
+            out[(0 * row_tokens + tok) * 2 + side] = t;
+            for (int dim = 1; dim < 3; ++dim) {
+                float x = grid[((size_t)dim * tokens + tok) * 2 + side];
+                // 5. the spatial axes scaled by the target-over-reference ratio
+                if (r->downscale_factor != 1) x = x * down;
+                out[(dim * row_tokens + tok) * 2 + side] = x;
+            }
+        }
+    return (int32_t)tokens;
+}
+
+int32_t ltx_rope_video_positions_with_references(int32_t latent_frames, int32_t latent_height,
+                                                 int32_t latent_width, int32_t temporal_scale,
+                                                 int32_t spatial_scale, double frame_rate,
+                                                 const ltx_rope_reference *refs,
+                                                 int32_t n_refs, float *out, int64_t cap) {
+    if (n_refs < 0 || (n_refs > 0 && !refs) || !out) return -1;
+    const int64_t target = (int64_t)latent_frames * latent_height * latent_width;
+    if (latent_frames < 1 || latent_height < 1 || latent_width < 1) return -1;
+    int64_t total = target;
+    for (int32_t i = 0; i < n_refs; ++i)
+        total += (int64_t)refs[i].latent_frames * refs[i].latent_height * refs[i].latent_width;
+    if (total > INT32_MAX || cap < 3 * total * 2) return -1;
+    std::vector<float> grid((size_t)target * 6);
+    if (ltx_rope_video_positions(latent_frames, latent_height, latent_width, temporal_scale,
+                                 spatial_scale, frame_rate, grid.data(),
+                                 (int64_t)grid.size()) != (int32_t)target)
+        return -1;
+    for (int dim = 0; dim < 3; ++dim)
+        memcpy(out + (size_t)dim * total * 2, grid.data() + (size_t)dim * target * 2,
+               sizeof(float) * target * 2);
+    // every reference reads the shift from the generated grid itself, never from the growing
+    // concatenation (DiTForward.swift:707-711): the target's first patch end, [0][0][1]
+    const float first_end = grid[1];
+    int64_t at = target;
+    for (int32_t i = 0; i < n_refs; ++i) {
+        const int32_t n = ltx_rope_reference_positions(&refs[i], temporal_scale, spatial_scale,
+                                                       frame_rate, first_end, out + at * 2,
+                                                       total);
+        if (n < 0) return -1;
+        at += n;
+    }
+    return (int32_t)total;
+}
+
 int32_t ltx_rope_audio_positions(int32_t tokens, int32_t hop_length, int32_t sample_rate,
                                  int32_t downsample, float *out, int64_t cap) {
     if (tokens < 1 || hop_length < 1 || sample_rate < 1 || downsample < 1 || !out ||

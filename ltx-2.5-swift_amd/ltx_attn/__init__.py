@@ -120,8 +120,33 @@ EXPORTED_SYMBOLS = (
     "ltx_rope_audio_positions", "ltx_rope_tables", "ltx_rope_tables_device",
     "ltx_linear", "ltx_linear_sumsq_blocks", "ltx_gemma_attn_workspace_bytes",
     "ltx_gemma_attn_fwd", "ltx_gemma_rope_tables", "ltx_device_count", "ltx_device_query",
-    "ltx_attn_fwd_static",
+    "ltx_attn_fwd_static", "ltx_rope_reference_positions",
+    "ltx_rope_video_positions_with_references",
 )
+
+
+class Reference(ctypes.Structure):
+    """``ltx_rope_reference``: an in-context reference clip appended to the video stream
+    (``DiTForward.Geometry.Reference``, DiTForward.swift:220-252)."""
+    _fields_ = [("latent_frames", ctypes.c_int32), ("latent_height", ctypes.c_int32),
+                ("latent_width", ctypes.c_int32), ("downscale_factor", ctypes.c_int32),
+                ("temporal_scale_factor", ctypes.c_int32), ("frame_offset", ctypes.c_int32)]
+
+    def __init__(self, latent_frames, latent_height, latent_width, downscale_factor=1,
+                 temporal_scale_factor=1, frame_offset=0):
+        super().__init__(latent_frames, latent_height, latent_width, downscale_factor,
+                         temporal_scale_factor, frame_offset)
+
+    @property
+    def tokens(self) -> int:
+        return self.latent_frames * self.latent_height * self.latent_width
+
+
+def msr_slots(count: int, latent_frames: int, latent_height: int, latent_width: int):
+    """Multiple-Subject-Reference slots: slot i of n sits at -(n - i) pixel frames, the first
+    furthest back in time (DiTForward.swift:229-242)."""
+    return [Reference(latent_frames, latent_height, latent_width, frame_offset=-(count - i))
+            for i in range(count)]
 
 # ltx_attn_fwd_static's per-device scratch (LTX_ATTN_STATIC_SCRATCH_BYTES)
 STATIC_SCRATCH_BYTES = 128 << 20
@@ -180,6 +205,15 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ltx_rope_audio_positions.argtypes = [ctypes.c_int32] * 4 + [ctypes.c_void_p,
                                                                      ctypes.c_int64]
     lib.ltx_rope_audio_positions.restype = ctypes.c_int32
+    lib.ltx_rope_reference_positions.argtypes = [ctypes.POINTER(Reference), ctypes.c_int32,
+                                                 ctypes.c_int32, ctypes.c_double,
+                                                 ctypes.c_float, ctypes.c_void_p,
+                                                 ctypes.c_int64]
+    lib.ltx_rope_reference_positions.restype = ctypes.c_int32
+    lib.ltx_rope_video_positions_with_references.argtypes = [ctypes.c_int32] * 5 + [
+        ctypes.c_double, ctypes.POINTER(Reference), ctypes.c_int32, ctypes.c_void_p,
+        ctypes.c_int64]
+    lib.ltx_rope_video_positions_with_references.restype = ctypes.c_int32
     lib.ltx_rope_tables.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                     ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
                                     ctypes.c_double, ctypes.c_void_p, ctypes.c_void_p]
@@ -662,6 +696,38 @@ def rope_video_positions(latent_frames, latent_height, latent_width, temporal_sc
     return out
 
 
+def rope_reference_positions(ref: "Reference", target_first_end: float, frame_rate=24.0,
+                             temporal_scale=8, spatial_scale=32) -> np.ndarray:
+    """referencePositions (DiTForward.swift:553-593): ``[3, tokens, 2]`` bounds of one
+    reference in the target's frame; ``target_first_end`` is the target grid's first patch
+    end (``positions[0, 0, 1]``)."""
+    lib = load_library()
+    out = np.zeros((3, ref.tokens, 2), dtype=np.float32)
+    n = lib.ltx_rope_reference_positions(ctypes.byref(ref), temporal_scale, spatial_scale,
+                                         frame_rate, target_first_end, out.ctypes.data,
+                                         ref.tokens)
+    if n < 0:
+        raise Failure(EINVAL, "bad reference-position arguments")
+    return out
+
+
+def rope_video_positions_with_references(latent_frames, latent_height, latent_width,
+                                         references, temporal_scale=8, spatial_scale=32,
+                                         frame_rate=24.0) -> np.ndarray:
+    """The video grid of a render with references (DiTForward.swift:698-711): ``[3, total,
+    2]`` with the target's tokens first, then every reference's in order."""
+    lib = load_library()
+    refs = (Reference * max(1, len(references)))(*references)
+    total = latent_frames * latent_height * latent_width + sum(r.tokens for r in references)
+    out = np.zeros((3, total, 2), dtype=np.float32)
+    n = lib.ltx_rope_video_positions_with_references(
+        latent_frames, latent_height, latent_width, temporal_scale, spatial_scale, frame_rate,
+        refs, len(references), out.ctypes.data, out.size)
+    if n != total:
+        raise Failure(EINVAL, "bad video/reference-position arguments")
+    return out
+
+
 def rope_audio_positions(tokens, hop_length=160, sample_rate=16000, downsample=4) -> np.ndarray:
     lib = load_library()
     out = np.zeros((1, tokens, 2), dtype=np.float32)
@@ -744,12 +810,14 @@ def rope_tables_device(positions, inner: int, max_pos, heads: int = 32,
 
 def rotaries_device(frames: int, height: int, width: int, frame_rate: float = 24.0,
                     video_width: int = 4096, audio_width: int = 2048, heads: int = 32,
-                    theta: float = 10000.0, audio_tokens: Optional[int] = None):
+                    theta: float = 10000.0, audio_tokens: Optional[int] = None,
+                    references=()):
     """``rotaries`` with the tables built on the GPU: the positions (a few floats per token)
     are built on the host and copied; the tables are written in device memory. Returns
     ``Rotary`` pairs of bf16 device tensors keyed like ``rotaries``."""
     lf = 1 if frames <= 1 else (frames - 1) // 8 + 1
-    video = rope_video_positions(lf, height // 32, width // 32, 8, 32, frame_rate)
+    video = rope_video_positions_with_references(lf, height // 32, width // 32,
+                                                 list(references), 8, 32, frame_rate)
     if audio_tokens is None:
         audio_tokens = int(round(frames / frame_rate * 25.0))
     audio = rope_audio_positions(audio_tokens)
@@ -764,12 +832,14 @@ def rotaries_device(frames: int, height: int, width: int, frame_rate: float = 24
 
 def rotaries(frames: int, height: int, width: int, frame_rate: float = 24.0,
              video_width: int = 4096, audio_width: int = 2048, heads: int = 32,
-             theta: float = 10000.0, audio_tokens: Optional[int] = None):
+             theta: float = 10000.0, audio_tokens: Optional[int] = None, references=()):
     """The four tables of ``DiTForward.rotaries(geometry:dtype:)`` (DiTForward.swift:698-738)
     as numpy bf16 bit patterns, keyed ``videoSelf``, ``audioSelf``, ``videoCross``,
-    ``audioCross``."""
+    ``audioCross``. ``references``: ``Reference`` clips appended to the video stream (the
+    video tables then cover ``videoTokensWithReference`` tokens, :707-711)."""
     lf = 1 if frames <= 1 else (frames - 1) // 8 + 1
-    video = rope_video_positions(lf, height // 32, width // 32, 8, 32, frame_rate)
+    video = rope_video_positions_with_references(lf, height // 32, width // 32,
+                                                 list(references), 8, 32, frame_rate)
     if audio_tokens is None:
         audio_tokens = int(round(frames / frame_rate * 25.0))
     audio = rope_audio_positions(audio_tokens)

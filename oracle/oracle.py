@@ -28,7 +28,9 @@ This is a numpy restatement of the reference's arithmetic:
 * ``attention_module`` -- ``DiTAttention.callAsFunction`` (``:315-405``): projections, the
                         replaced unit, the gate from ``x`` and ``to_out``.
 * RoPE tables        -- ``Sources/LTXModules/DiTForward.swift:455-466`` (``frequencyGrid``),
-                        ``:486-520`` (``videoPositions``), ``:606-619`` (``audioPositions``),
+                        ``:486-520`` (``videoPositions``), ``:553-593``
+                        (``referencePositions``, IC-LoRA / MSR reference clips),
+                        ``:606-619`` (``audioPositions``),
                         ``:641-678`` (``rotary``), ``:698-738`` (``rotaries``).
 
 Gemma-4 text-encoder attention (``Sources/LTXModules/GemmaTextEncoder.swift``):
@@ -76,7 +78,8 @@ __all__ = [
     "f32_to_bf16_bits", "bf16_bits_to_f32", "round_bf16", "randn_bf16_bits",
     "splitmix64", "splitmix_bf16_bits", "rms_norm", "split_rope", "sdpa", "head_gate", "attention",
     "linear", "sumsq_partials", "attention_module",
-    "frequency_grid", "video_positions", "audio_positions", "rotary_tables",
+    "frequency_grid", "video_positions", "reference_positions",
+    "video_positions_with_references", "audio_positions", "rotary_tables",
     "rotaries", "compare",
 ]
 
@@ -123,16 +126,14 @@ def splitmix64(count: int, seed: int) -> np.ndarray:
     mixed, so word ``i`` is the standard splitmix64 output ``i + 1`` of a generator seeded
     with ``seed`` (the first output of the standard generator is skipped).
     """
-    mask = (1 << 64) - 1
-    state = (seed + SPLITMIX_GAMMA) & mask
-    out = np.empty(count, dtype=np.uint64)
-    for i in range(count):
-        state = (state + SPLITMIX_GAMMA) & mask
-        z = state
-        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
-        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
-        out[i] = z ^ (z >> 31)
-    return out
+    # state before mixing word i: seed + (i + 2) * gamma, modulo 2^64 (uint64 arithmetic
+    # wraps exactly that way)
+    with np.errstate(over="ignore"):
+        z = (np.uint64(seed % (1 << 64)) + np.uint64(SPLITMIX_GAMMA) *
+             (np.arange(count, dtype=np.uint64) + np.uint64(2)))
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
 
 
 def splitmix_bf16_bits(count: int, seed: int) -> np.ndarray:
@@ -419,6 +420,48 @@ def video_positions(latent_frames: int, latent_height: int, latent_width: int,
     return out
 
 
+def reference_positions(latent_frames: int, latent_height: int, latent_width: int, *,
+                        frame_rate: float = 24.0, downscale_factor: int = 1,
+                        temporal_scale_factor: int = 1, frame_offset: int = 0,
+                        target=None, temporal_scale: int = 8,
+                        spatial_scale: int = 32) -> np.ndarray:
+    """An in-context reference's bounds ``[1, 3, tokens, 2]`` in the target's frame
+    (``DiTForward.swift:553-593``): its own grid at frame rate 1 (pixel frames), the offset
+    added in pixel frames, then divided by ``float(fps / temporalScaleFactor)``; a temporally
+    sparse reference is slid by ``(factor - 1) * target[0, 0, 0, 1]`` and clamped at 0; the
+    spatial axes are multiplied by the downscale factor. All in fp32, step by step."""
+    if frame_offset != 0 and temporal_scale_factor != 1:
+        raise ValueError("a reference cannot carry both a frame offset and a temporal scale")
+    grid = video_positions(latent_frames, latent_height, latent_width, temporal_scale,
+                           spatial_scale, 1.0)
+    time = grid[:, 0:1].copy()
+    space = grid[:, 1:3].copy()
+    if frame_offset != 0:
+        time = (time + np.float32(frame_offset)).astype(np.float32)
+    time = (time / np.float32(frame_rate / float(temporal_scale_factor))).astype(np.float32)
+    if temporal_scale_factor != 1:
+        t_target = np.float32(np.asarray(target, dtype=np.float32)[0, 0, 0, 1])
+        shift = np.float32(np.float32(temporal_scale_factor - 1) * t_target)
+        time = np.maximum((time - shift).astype(np.float32), np.float32(0.0))
+    if downscale_factor != 1:
+        space = (space * np.float32(downscale_factor)).astype(np.float32)
+    return np.concatenate([time, space], axis=1)
+
+
+def video_positions_with_references(latent_frames: int, latent_height: int, latent_width: int,
+                                    references, frame_rate: float = 24.0) -> np.ndarray:
+    """``rotaries``' video grid with references (``DiTForward.swift:698-711``): the target's
+    grid, then every reference's (dicts of ``reference_positions`` keywords plus
+    ``latent_frames/height/width``), each shifted against the target's own grid."""
+    target = video_positions(latent_frames, latent_height, latent_width, 8, 32, frame_rate)
+    blocks = [target]
+    for ref in references:
+        kw = dict(ref)
+        dims = (kw.pop("latent_frames"), kw.pop("latent_height"), kw.pop("latent_width"))
+        blocks.append(reference_positions(*dims, frame_rate=frame_rate, target=target, **kw))
+    return np.concatenate(blocks, axis=2)
+
+
 def audio_positions(tokens: int, hop_length: int = 160, sample_rate: int = 16000,
                     downsample: int = 4) -> np.ndarray:
     """Audio bounds ``[1, 1, tokens, 2]`` in seconds (``DiTForward.swift:606-619``)."""
@@ -622,8 +665,23 @@ def compare(candidate, reference) -> dict:
 import ctypes as _ct
 import os as _os
 
-_C_LIB_PATH = _os.path.join(_os.path.dirname(_os.path.abspath(__file__)), "lib", "liboracle.so")
+_C_LIB_DIR = _os.path.join(_os.path.dirname(_os.path.abspath(__file__)), "lib")
+_C_LIB_PATH = _os.path.join(_C_LIB_DIR, "liboracle.so")
+_C_LIB_V4_PATH = _os.path.join(_C_LIB_DIR, "liboracle_v4.so")
 _c_lib = None
+c_library_isa = None
+
+
+def _cpu_has_avx512() -> bool:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    return {"avx512f", "avx512bw", "avx512dq", "avx512vl"} <= flags
+    except OSError:
+        pass
+    return False
 
 
 class _OracleArgs(_ct.Structure):
@@ -642,11 +700,15 @@ class _OracleArgs(_ct.Structure):
 
 
 def c_library():
-    global _c_lib
+    """The C restatement: the AVX-512 build where the CPU has AVX-512, else the AVX2 one."""
+    global _c_lib, c_library_isa
     if _c_lib is None:
-        if not _os.path.exists(_C_LIB_PATH):
-            raise RuntimeError(f"{_C_LIB_PATH} missing; run `make -C oracle`")
-        lib = _ct.CDLL(_C_LIB_PATH)
+        path, c_library_isa = _C_LIB_PATH, "x86-64-v3 (AVX2)"
+        if _cpu_has_avx512() and _os.path.exists(_C_LIB_V4_PATH):
+            path, c_library_isa = _C_LIB_V4_PATH, "x86-64-v4 (AVX-512)"
+        if not _os.path.exists(path):
+            raise RuntimeError(f"{path} missing; run `make -C oracle`")
+        lib = _ct.CDLL(path)
         lib.oracle_attention.argtypes = [_ct.POINTER(_OracleArgs)]
         lib.oracle_attention.restype = _ct.c_int
         lib.oracle_max_threads.restype = _ct.c_int

@@ -80,3 +80,51 @@ def test_attention_with_device_tables(device):
     b = L.attention_fwd(q, k, v, heads=H, rotary=L.Rotary(up[0], up[1]))
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def test_attention_over_a_reference_lengthened_stream(device):
+    """The stage-2 upscaler's stream with an IC-LoRA reference (VideoUpscaler.swift:808-812;
+    positions DiTForward.swift:553-593, :707-711) and two Multiple-Subject-Reference slots:
+    3120 target tokens (13 x 12 x 20), a half-resolution reference of 13 x 6 x 10 (downscale 2)
+    and two one-frame slots at -2 and -1 pixel frames: 4380 tokens. The device builder's video
+    tables equal the oracle's (its own positions, its own table recipe), and the self-attention
+    with norm + 3-D RoPE over the lengthened stream matches the C oracle over every head and
+    row, to the stated tolerance. The device tables equal the host builder's bit for bit; the
+    host positions equal the oracle's bit for bit (its tables may differ from the host's by a
+    rare bf16 step: its cos/sin are numpy's float32 ones)."""
+    import torch
+
+    from test_gpu_parity import _gpu_bits, check_heads
+
+    H, D = 32, 128
+    refs = [L.Reference(13, 6, 10, downscale_factor=2)] + L.msr_slots(2, 1, 12, 20)
+    tabs = L.rotaries_device(97, 384, 640, references=refs)
+    torch.cuda.synchronize()
+    pos = O.video_positions_with_references(
+        13, 12, 20, [dict(latent_frames=13, latent_height=6, latent_width=10,
+                          downscale_factor=2)] +
+        [dict(latent_frames=1, latent_height=12, latent_width=20, frame_offset=-(2 - i))
+         for i in range(2)], 24.0)
+    host_pos = L.rope_video_positions_with_references(13, 12, 20, refs)
+    assert np.array_equal(host_pos.view(np.uint32), pos[0].view(np.uint32))
+    host_cos, host_sin = L.rope_tables(host_pos, H * D, [20, 2048, 2048], H)
+    assert np.array_equal(_bits(tabs["videoSelf"].cos), host_cos)
+    assert np.array_equal(_bits(tabs["videoSelf"].sin), host_sin)
+    cos, sin = O.rotary_tables(pos, H * D, [20, 2048, 2048], H)
+    T = cos.shape[1]
+    print(f"reference-lengthened stream: {T} video tokens", flush=True)
+    assert T == 3120 + 780 + 2 * 240
+    seed = 0x5EED + 600
+    tq, qb = _gpu_bits((1, T, H * D), seed, device)
+    tk, kb = _gpu_bits((1, T, H * D), seed + 1, device)
+    tv, vb = _gpu_bits((1, T, H * D), seed + 2, device)
+    wq, wqb = _gpu_bits((H * D,), seed + 3, device, 1.0, 0.02)
+    wk, wkb = _gpu_bits((H * D,), seed + 4, device, 1.0, 0.02)
+    out = L.attention_fwd(tq, tk, tv, heads=H, q_norm_w=wq, k_norm_w=wk,
+                          rotary=tabs["videoSelf"])
+    torch.cuda.synchronize()
+    kw = dict(q_norm_w=wqb, k_norm_w=wkb, q_cos=cos, q_sin=sin)
+    truth = O.c_attention(qb, kb, vb, H, mode="exact", **kw)
+    refm = O.round_bf16(O.c_attention(qb, kb, vb, H, mode="reference", **kw))
+    got = O.bf16_bits_to_f32(_bits(out)).reshape(truth.shape)
+    check_heads(got, truth, refm, "reference-lengthened self-attention")
