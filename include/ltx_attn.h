@@ -21,9 +21,10 @@
  * Contract of ltx_attn_fwd (all of it checked on the host before anything is launched):
  *   - no allocation: scratch memory is the caller's `workspace`, sized by
  *     ltx_attn_workspace_bytes() for the same arguments;
- *   - no hidden global mutable state beyond a per-device cache of the CU count the work
- *     split is planned over (written once per device, idempotent); reentrant across streams
- *     and threads (the detail string of the last failure is thread-local, like dlerror);
+ *   - no hidden global mutable state; reentrant across streams and threads (the detail
+ *     string of the last failure is thread-local, like dlerror);
+ *   - sizing and validation (ltx_attn_workspace_bytes, ltx_attn_validate) are pure host
+ *     functions that do not touch the HIP runtime;
  *   - asynchronous on `stream`; inputs must stay valid until the stream reaches the call.
  */
 #ifndef LTX_ATTN_H
@@ -345,8 +346,8 @@ int32_t ltx_gemma_rope_tables(int32_t tokens, int32_t head_dim, double theta,
  * -------------------------------------------------------------------------------------- */
 typedef struct ltx_device_info {
     int32_t ordinal;
-    int32_t compute_units;        /* CUs (256 on an MI355X); the attention kernels run one     */
-                                  /* workgroup per CU and plan their tail splits over them     */
+    int32_t compute_units;        /* CUs (256 on an MI355X, the count the work split of the   */
+                                  /* attention kernels is planned for: one workgroup per CU)  */
     int64_t memory_bytes;         /* device memory (HBM) capacity                              */
     int32_t clock_khz;            /* peak shader clock                                         */
     int32_t lds_bytes_per_cu;     /* LDS per CU (160 KiB on gfx950)                            */

@@ -161,6 +161,7 @@ enum KernelKind { kRegPlain = 0, kRegFused = 1, kDma = 2 };
 int launch_fmha(const FmhaParams &p, int D, int kind, void *stream);
 int launch_fmha_dma(const FmhaParams &p, int D, void *stream);   // fmha_dma.hip
 int launch_fmha_short(const FmhaParams &p, int D, void *stream); // fmha_short.hip
+int launch_fmha_splitk(const FmhaParams &p, int D, void *stream);  // fmha_splitk.hip
 int launch_prep(const PrepParams &p, int D, void *stream);
 int launch_combine(const CombineParams &p, int D, void *stream);
 int launch_passthrough(const PassParams &p, int D, void *stream);

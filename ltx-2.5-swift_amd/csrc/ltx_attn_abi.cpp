@@ -13,7 +13,6 @@
 #include <string.h>
 
 #include <algorithm>
-#include <atomic>
 #include <utility>
 
 #include "../../include/ltx_attn.h"
@@ -35,32 +34,10 @@ bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// Attention workgroups resident at once: one per CU of the device current at the call (each
-// workgroup holds most of a CU's LDS). Queried once per device; an MI355X's 256 CUs when no
-// device is visible (pure host use of the planner, e.g. sizing a workspace ahead of time).
-constexpr int64_t kDefaultConcurrentGroups = 256;
-std::atomic<int32_t> g_device_cus[64];
-
-int64_t concurrent_groups() {
-    int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
-        (void)hipGetLastError();
-        return kDefaultConcurrentGroups;
-    }
-    if (dev >= 64) return kDefaultConcurrentGroups;
-    int32_t cus = g_device_cus[dev].load(std::memory_order_relaxed);
-    if (cus <= 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            n <= 0) {
-            (void)hipGetLastError();
-            return kDefaultConcurrentGroups;
-        }
-        cus = n;
-        g_device_cus[dev].store(cus, std::memory_order_relaxed);
-    }
-    return cus;
-}
+// Attention workgroups resident at once: one per CU (each holds most of a CU's LDS) of a
+// gfx950 part, 256 CUs. The planner is a pure host function (workspace sizing and validation
+// run without touching the HIP runtime), so the count is a constant, not a device query.
+constexpr int64_t kConcurrentGroups = 256;
 // Charge per extra split of a tail item, in rounds: its fp32 partial O is written and read
 // back by the combine kernel.
 constexpr double kSplitCharge = 0.02;
@@ -73,6 +50,8 @@ struct Plan {
     bool passthrough = false;  // STG passthrough: out = V (x gate), no attention
     bool dma = false;          // LDS-DMA kernel (K prologue when K needs work)
     bool shortk = false;       // short-key kernel: the head's keys resident in LDS
+    bool splitk = false;       // split-key kernel: one query block over key ranges, K
+                               // normalised/rotated in LDS
     bool k_prologue = false;   // K normalised/rotated by a separate pass into the workspace
     bool k_fused = false;      // K normalised/rotated while staging into LDS
     int nqblk = 0;
@@ -220,7 +199,6 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
     // 32-bit byte offsets up to the key length padded to whole tiles; calls past that take
     // the register-staged kernel.
     const bool k_work = pl->k_norm || pl->k_rope;
-    const int64_t kConcurrentGroups = concurrent_groups();
     // Short key ranges (text cross-attention over its valid keys, video queries over the
     // audio keys) take the short-key kernel: the head's K (prepared by the prologue, only
     // its valid rows, when it needs norm/RoPE) and V stay in LDS while the queries stream
@@ -264,22 +242,46 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
     else if (a->kprep == LTX_ATTN_KPREP_AUTO) pl->dma = dma_fits && pl->nqblk >= 2;
     if (pl->dma) pl->k_prologue = k_work;
     else pl->k_fused = k_work;
+    // One query block per (batch, head) over a key stream read once, at head dim 64 (the
+    // audio queries over the video keys): the split-key kernel streams K (raw), its statistic
+    // and table rows, and V through LDS by LDS DMA, three tiles ahead, over key ranges spread
+    // across the whole GPU. Its copies address a head's raw K and V rows with 32-bit byte
+    // offsets.
+    const int64_t raw_k_bytes = lk_pad * a->k_rs * 2;
+    if (a->kprep == LTX_ATTN_KPREP_AUTO && !pl->dma && pl->nqblk == 1 && D == 64 &&
+        B <= ltx::kMaxBatch &&
+        raw_k_bytes < 0x7fffffff && lk_pad * a->v_rs * 2 < 0x7fffffff)
+        pl->splitk = true;
 
-    // Work decomposition. 256 workgroups run at once (one per CU). The whole rounds of
-    // items run unsplit; the items of the last, partial round are split into key ranges so
-    // that they finish in a fraction of a round (split-KV, merged by the combine kernel).
+    // Work decomposition. One workgroup per CU runs at once. The whole rounds of items run
+    // unsplit; the items of a last round that would leave most CUs idle are split into key
+    // ranges so that they finish in a fraction of a round (split-KV, merged by the combine
+    // kernel).
     // A split count S costs ceil(rem*S/256)/S rounds for the rem tail items plus a small
     // per-split charge for the partial results. A caller-fixed num_splits splits every item.
     // Calls beyond one argument table of batches (B > kMaxBatch, sliced launches) run whole.
     const int64_t N = (int64_t)B * H * pl->nqblk;
     int64_t n_full = N;
     int splits = 1;
-    if (a->num_splits > 0) {
+    if (pl->splitk) {
+        // about one key range per CU (measured best for 32 heads over 3120 keys and 2 x 32
+        // over 15360: more ranges add start-ups and partials faster than they add overlap),
+        // none shorter than two tiles
+        splits = a->num_splits > 0
+                     ? a->num_splits
+                     : (int)std::min<int64_t>(ltx::kMaxSplits,
+                                              (kConcurrentGroups + N - 1) / N);
+        splits = std::max(1, std::min(splits, (pl->ntiles_max + 1) / 2));
+        n_full = 0;
+    } else if (a->num_splits > 0) {
         splits = a->num_splits;
         n_full = 0;
     } else if (B <= ltx::kMaxBatch) {
         const int64_t rounds = N / kConcurrentGroups, rem = N - rounds * kConcurrentGroups;
-        if (rem > 0) {
+        // A last round on at most half the CUs is split; a fuller one is not: with fewer
+        // workgroups resident each runs its tiles faster (measured at 3120 tokens: the 160
+        // tail items unsplit finish as fast as split three ways, without the combine).
+        if (rem > 0 && 2 * rem <= kConcurrentGroups) {
             double best = 1.0;
             for (int sp = 2; sp <= ltx::kMaxSplits && sp <= pl->ntiles_max; ++sp) {
                 const double c =
@@ -494,6 +496,7 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     }
 
     const int kind = pl.dma ? ltx::kDma : pl.k_fused ? ltx::kRegFused : ltx::kRegPlain;
+    (void)kind;
 
     // 2. attention
     ltx::FmhaParams fp{};
@@ -556,8 +559,9 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     if (a->ev_attn_start)
         if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_start, (hipStream_t)stream))
             return fail(LTX_ATTN_EHIP, "event record: %s", hipGetErrorString(e));
-    if (int e = pl.shortk ? ltx::launch_fmha_short(fp, D, stream)
-                          : ltx::launch_fmha(fp, D, kind, stream))
+    if (int e = pl.shortk   ? ltx::launch_fmha_short(fp, D, stream)
+                : pl.splitk ? ltx::launch_fmha_splitk(fp, D, stream)
+                            : ltx::launch_fmha(fp, D, kind, stream))
         return fail(LTX_ATTN_EHIP, "attention launch: %s", hipGetErrorString((hipError_t)e));
     if (a->ev_attn_stop)
         if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_stop, (hipStream_t)stream))

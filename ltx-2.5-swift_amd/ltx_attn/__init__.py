@@ -169,6 +169,14 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     global _lib
     if _lib is not None:
         return _lib
+    # torch (when installed) ships its own HIP and HSA runtimes under the same sonames as the
+    # system's. Loaded first, they are the ones this library binds to: one runtime in the
+    # process. Loaded after the library, torch would bring a second HSA runtime, and the two
+    # would contend for the device.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     if not os.path.exists(path):
         raise RuntimeError(f"libltx_attn.so not found at {path}; build it with "
                            "`python -c 'import __graft_entry__ as g; g.build()'` or "

@@ -86,10 +86,15 @@ def test_valid_arguments_pass():
     # blocks = 256): no workspace
     st, msg = _validate(_args(Lq=2048, kprep=L.KPREP_FUSED, ws=False))
     assert st == L.OK, msg
-    # LDS-DMA kernel over 13 query blocks: the tail split's partials must be provided
+    # LDS-DMA kernel over 13 query blocks per head (416 items): the last round of 160 would
+    # fill most CUs, so it is not split and needs no workspace
     st, msg = _validate(_args(ws=False))
+    assert st == L.OK, msg
+    # 9 query blocks over 2 x 32 heads (576 items): the last round's 64 items are split,
+    # whose partials must be provided
+    st, msg = _validate(_args(B=2, Lq=2100, Lk=3000, ws=False))
     assert st == L.EWORKSPACE, msg
-    st, msg = _validate(_args())
+    st, msg = _validate(_args(B=2, Lq=2100, Lk=3000))
     assert st == L.OK, msg
 
 
@@ -184,15 +189,20 @@ def test_key_padding_rules():
 def test_workspace_sizing_and_check():
     lib = L.load_library()
     # plain attention over 13 query blocks (LDS-DMA kernel, which reads K and V in place):
-    # the tail split only, 416 items = one whole round of 256 + 160 items split into 3 key
-    # ranges of 17 tiles, each partial row 128 fp32 + (max, sum)
-    rows = 3 * 160 * 256
-    tail3120 = rows * 128 * 4 + rows * 2 * 4
+    # 416 items = one whole round of 256 + 160, a last round more than half full: no split,
+    # nothing to hold
     a = _args(ws=False)
-    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == tail3120
-    # the register-staged kernel: the same tail split
+    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == 0
     a = _args(kprep=L.KPREP_FUSED, ws=False)
-    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == tail3120
+    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == 0
+    # 2 x 32 heads x 9 query blocks = 576 items: the last 64 are split (the tail round at a
+    # quarter of the CUs) into 4 key ranges of 12 tiles, each partial row 128 fp32 + (max, sum)
+    rows = 4 * 64 * 256
+    tail = rows * 128 * 4 + rows * 2 * 4
+    a = _args(B=2, Lq=2100, Lk=3000, ws=False)
+    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == tail
+    a = _args(B=2, Lq=2100, Lk=3000, kprep=L.KPREP_FUSED, ws=False)
+    assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == tail
     # whole rounds only (256 items): nothing
     a = _args(Lq=2048, kprep=L.KPREP_FUSED, ws=False)
     assert lib.ltx_attn_workspace_bytes(ctypes.byref(a)) == 0

@@ -99,13 +99,13 @@ def test_static_entry_matches_the_workspace_entry(device):
     def bits(t):
         return t.view(torch.int16).cpu().numpy().view(np.uint16)
 
-    # 1: 3120 tokens, 32 heads of 128, norm + RoPE: the K prologue's prepared K and the
-    #    split-KV partials of the tail items fill most of the scratch
-    big = (1, 32, 3120, 128)
+    # 1: 2 x 2100 tokens, 32 heads of 128, norm + RoPE: the statistics, the K prologue's
+    #    prepared K and the split-KV partials of the last round's 64 items fill most of it
+    big = (2, 32, 2100, 128)
     q, k, v, wq, wk, rot, _ = _inputs(device, *big, 0x5EED + 700)
     lib = L.load_library()
     need = lib.ltx_attn_workspace_bytes(
-        ctypes.byref(_fake_args(1, 32, 3120, 3120, 128, norm=True, rope=True)))
+        ctypes.byref(_fake_args(2, 32, 2100, 2100, 128, norm=True, rope=True)))
     _say(f"no-alloc call 1: B,H,T,D = {big}, scratch {need} of {L.STATIC_SCRATCH_BYTES} bytes")
     assert need > L.STATIC_SCRATCH_BYTES // 2
     want1 = _call(device, q, k, v, 32, wq, wk, rot, False)
