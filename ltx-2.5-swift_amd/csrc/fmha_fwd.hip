@@ -559,10 +559,10 @@ void fmha_fwd_kernel(const FmhaParams p) {
 constexpr int kPrepRows = NT / 64;             // token rows per workgroup
 
 template <int D, int UPL>
-__global__ __launch_bounds__(NT) void qk_prep_kernel(const PrepParams p) {
+__device__ __forceinline__ void qk_prep_rows(const PrepParams &p, int blk) {
     constexpr int PPH = D / 16;               // pair units per head
     const int lane = threadIdx.x & 63;
-    const int rid = blockIdx.x * kPrepRows + (threadIdx.x >> 6);   // output row b*L + lrow
+    const int rid = blk * kPrepRows + (threadIdx.x >> 6);   // output row b*L + lrow
     if (rid >= p.B * p.L) return;
     const int b = rid / p.L;
     const int lrow = rid % p.L;
@@ -648,6 +648,15 @@ __global__ __launch_bounds__(NT) void qk_prep_kernel(const PrepParams p) {
         *(u32x4 *)(dst + hh * D + 8 * c) = pack8(a);
         *(u32x4 *)(dst + hh * D + D / 2 + 8 * c) = pack8(c2);
     }
+}
+
+// One launch for one row set, or for two (the Q statistic and the K prologue of one call):
+// the first blocks_a workgroups take set a, the rest set b.
+template <int D, int UPL>
+__global__ __launch_bounds__(NT) void qk_prep_kernel(const PrepParams a, const PrepParams b,
+                                                     const int blocks_a) {
+    if ((int)blockIdx.x < blocks_a) qk_prep_rows<D, UPL>(a, blockIdx.x);
+    else qk_prep_rows<D, UPL>(b, blockIdx.x - blocks_a);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -763,21 +772,33 @@ int launch_rstd(const RstdParams &p, void *stream) {
 }
 
 template <int D>
-static void launch_prep_d(const PrepParams &p, dim3 grid, hipStream_t st) {
-    const int upl = (p.H * (D / 16) + 63) / 64;   // pair units per lane (inner <= 16384)
-    if (upl <= 1) hipLaunchKernelGGL((qk_prep_kernel<D, 1>), grid, dim3(NT), 0, st, p);
-    else if (upl <= 2) hipLaunchKernelGGL((qk_prep_kernel<D, 2>), grid, dim3(NT), 0, st, p);
-    else if (upl <= 4) hipLaunchKernelGGL((qk_prep_kernel<D, 4>), grid, dim3(NT), 0, st, p);
-    else if (upl <= 8) hipLaunchKernelGGL((qk_prep_kernel<D, 8>), grid, dim3(NT), 0, st, p);
-    else hipLaunchKernelGGL((qk_prep_kernel<D, 16>), grid, dim3(NT), 0, st, p);
+static void launch_prep_d(const PrepParams &a, const PrepParams &b, int blocks_a, dim3 grid,
+                          hipStream_t st) {
+    const int upl = (a.H * (D / 16) + 63) / 64;   // pair units per lane (inner <= 16384)
+    if (upl <= 1) hipLaunchKernelGGL((qk_prep_kernel<D, 1>), grid, dim3(NT), 0, st, a, b, blocks_a);
+    else if (upl <= 2) hipLaunchKernelGGL((qk_prep_kernel<D, 2>), grid, dim3(NT), 0, st, a, b, blocks_a);
+    else if (upl <= 4) hipLaunchKernelGGL((qk_prep_kernel<D, 4>), grid, dim3(NT), 0, st, a, b, blocks_a);
+    else if (upl <= 8) hipLaunchKernelGGL((qk_prep_kernel<D, 8>), grid, dim3(NT), 0, st, a, b, blocks_a);
+    else hipLaunchKernelGGL((qk_prep_kernel<D, 16>), grid, dim3(NT), 0, st, a, b, blocks_a);
+}
+
+static int prep_blocks(const PrepParams &p) {
+    return (int)(((int64_t)p.B * p.L + kPrepRows - 1) / kPrepRows);
 }
 
 int launch_prep(const PrepParams &p, int D, void *stream) {
-    const int64_t rows = (int64_t)p.B * p.L;
-    const dim3 grid((unsigned)((rows + kPrepRows - 1) / kPrepRows));
+    const int blocks = prep_blocks(p);
     hipStream_t st = (hipStream_t)stream;
-    if (D == 128) launch_prep_d<128>(p, grid, st);
-    else launch_prep_d<64>(p, grid, st);
+    if (D == 128) launch_prep_d<128>(p, p, blocks, dim3(blocks), st);
+    else launch_prep_d<64>(p, p, blocks, dim3(blocks), st);
+    return (int)hipGetLastError();
+}
+
+int launch_prep2(const PrepParams &a, const PrepParams &b, int D, void *stream) {
+    const int blocks_a = prep_blocks(a), blocks = blocks_a + prep_blocks(b);
+    hipStream_t st = (hipStream_t)stream;
+    if (D == 128) launch_prep_d<128>(a, b, blocks_a, dim3(blocks), st);
+    else launch_prep_d<64>(a, b, blocks_a, dim3(blocks), st);
     return (int)hipGetLastError();
 }
 

@@ -163,6 +163,8 @@ int launch_fmha_dma(const FmhaParams &p, int D, void *stream);   // fmha_dma.hip
 int launch_fmha_short(const FmhaParams &p, int D, void *stream); // fmha_short.hip
 int launch_fmha_splitk(const FmhaParams &p, int D, void *stream);  // fmha_splitk.hip
 int launch_prep(const PrepParams &p, int D, void *stream);
+// Two row sets in one launch (a call's Q statistic and its K prologue); same H * D.
+int launch_prep2(const PrepParams &a, const PrepParams &b, int D, void *stream);
 int launch_combine(const CombineParams &p, int D, void *stream);
 int launch_passthrough(const PassParams &p, int D, void *stream);
 int launch_rstd(const RstdParams &p, void *stream);

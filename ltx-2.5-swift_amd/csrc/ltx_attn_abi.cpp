@@ -446,7 +446,10 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
         return LTX_ATTN_OK;
     }
 
-    // 1. prologue passes: statistic (and, for the K prologue, the prepared K)
+    // 1. prologue passes: statistics (and, for the K prologue, the prepared K). A call that
+    // takes both its Q statistic and its K pass from the inputs runs them as one launch.
+    ltx::PrepParams qpp{}, kpp{};
+    bool q_pass = false, k_pass = false;
     if (pl.q_stat) {
         ltx::RstdParams rp{};
         rp.sumsq = a->q_sumsq; rp.rs = a->q_sumsq_rs;
@@ -455,13 +458,11 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
         if (int e = ltx::launch_rstd(rp, stream))
             return fail(LTX_ATTN_EHIP, "q statistic launch: %s", hipGetErrorString((hipError_t)e));
     } else if (pl.q_norm) {
-        ltx::PrepParams pp{};
-        pp.x = a->q; pp.bs = a->q_bs; pp.rs = a->q_rs; pp.hs = a->q_hs;
-        pp.B = B; pp.L = a->Lq; pp.H = H;
-        pp.w = a->q_norm_w; pp.eps = a->norm_eps;
-        pp.rstd = (float *)(ws + pl.off_qrstd);
-        if (int e = ltx::launch_prep(pp, D, stream))
-            return fail(LTX_ATTN_EHIP, "q prologue launch: %s", hipGetErrorString((hipError_t)e));
+        qpp.x = a->q; qpp.bs = a->q_bs; qpp.rs = a->q_rs; qpp.hs = a->q_hs;
+        qpp.B = B; qpp.L = a->Lq; qpp.H = H;
+        qpp.w = a->q_norm_w; qpp.eps = a->norm_eps;
+        qpp.rstd = (float *)(ws + pl.off_qrstd);
+        q_pass = true;
     }
     const void *kptr = a->k;
     int64_t k_bs = a->k_bs, k_rs = a->k_rs, k_hs = a->k_hs;
@@ -473,26 +474,30 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
         if (int e = ltx::launch_rstd(rp, stream))
             return fail(LTX_ATTN_EHIP, "k statistic launch: %s", hipGetErrorString((hipError_t)e));
     } else if (pl.k_prologue || (pl.k_fused && pl.k_norm)) {
-        ltx::PrepParams pp{};
-        pp.x = a->k; pp.bs = a->k_bs; pp.rs = a->k_rs; pp.hs = a->k_hs;
-        pp.B = B; pp.L = pl.k_prologue ? pl.kprep_rows : a->Lk; pp.L_full = a->Lk; pp.H = H;
-        pp.w = a->k_norm_w; pp.eps = a->norm_eps;
+        kpp.x = a->k; kpp.bs = a->k_bs; kpp.rs = a->k_rs; kpp.hs = a->k_hs;
+        kpp.B = B; kpp.L = pl.k_prologue ? pl.kprep_rows : a->Lk; kpp.L_full = a->Lk; kpp.H = H;
+        kpp.w = a->k_norm_w; kpp.eps = a->norm_eps;
         if (pl.k_stat) {
-            pp.sumsq = a->k_sumsq; pp.ss_rs = a->k_sumsq_rs; pp.ss_blocks = a->sumsq_blocks;
+            kpp.sumsq = a->k_sumsq; kpp.ss_rs = a->k_sumsq_rs; kpp.ss_blocks = a->sumsq_blocks;
         }
         if (pl.k_prologue) {
-            pp.out = ws + pl.off_kprep;
-            pp.cos = a->k_cos ? a->k_cos : a->q_cos;
-            pp.sin = a->k_sin ? a->k_sin : a->q_sin;
-        } else {
-            pp.rstd = (float *)(ws + pl.off_krstd);
-        }
-        if (int e = ltx::launch_prep(pp, D, stream))
-            return fail(LTX_ATTN_EHIP, "k prologue launch: %s", hipGetErrorString((hipError_t)e));
-        if (pl.k_prologue) {
+            kpp.out = ws + pl.off_kprep;
+            kpp.cos = a->k_cos ? a->k_cos : a->q_cos;
+            kpp.sin = a->k_sin ? a->k_sin : a->q_sin;
             kptr = ws + pl.off_kprep;
             k_bs = (int64_t)pl.kprep_rows * H * D; k_rs = (int64_t)H * D; k_hs = D;
+        } else {
+            kpp.rstd = (float *)(ws + pl.off_krstd);
         }
+        k_pass = true;
+    }
+    if (q_pass && k_pass) {
+        if (int e = ltx::launch_prep2(qpp, kpp, D, stream))
+            return fail(LTX_ATTN_EHIP, "q/k prologue launch: %s", hipGetErrorString((hipError_t)e));
+    } else if (q_pass || k_pass) {
+        if (int e = ltx::launch_prep(q_pass ? qpp : kpp, D, stream))
+            return fail(LTX_ATTN_EHIP, "%s prologue launch: %s", q_pass ? "q" : "k",
+                        hipGetErrorString((hipError_t)e));
     }
 
     const int kind = pl.dma ? ltx::kDma : pl.k_fused ? ltx::kRegFused : ltx::kRegPlain;

@@ -736,6 +736,19 @@ def rope_video_positions_with_references(latent_frames, latent_height, latent_wi
     return out
 
 
+def audio_latent_count(frames: int, frame_rate: float = 24.0,
+                       latents_per_second: float = 25.0) -> int:
+    """Audio tokens of a clip: ``round(frames / frame_rate * latents_per_second)`` with halves
+    rounded away from zero, as Swift's ``rounded()`` does, not to even
+    (LatentGeometry.audioLatentCount, Sources/LTXFoundation/LatentGeometry.swift:128-132):
+    97 frames at 24 fps are 101 tokens, 121 frames 126, 12 frames 13."""
+    if frames <= 0 or not frame_rate > 0:
+        raise Failure(EINVAL, "frames and frame_rate must be positive")
+    x = float(frames) / float(frame_rate) * float(latents_per_second)
+    whole = math.floor(x)
+    return int(whole) + (1 if x - whole >= 0.5 else 0)   # x - whole is exact
+
+
 def rope_audio_positions(tokens, hop_length=160, sample_rate=16000, downsample=4) -> np.ndarray:
     lib = load_library()
     out = np.zeros((1, tokens, 2), dtype=np.float32)
@@ -827,7 +840,7 @@ def rotaries_device(frames: int, height: int, width: int, frame_rate: float = 24
     video = rope_video_positions_with_references(lf, height // 32, width // 32,
                                                  list(references), 8, 32, frame_rate)
     if audio_tokens is None:
-        audio_tokens = int(round(frames / frame_rate * 25.0))
+        audio_tokens = audio_latent_count(frames, frame_rate)
     audio = rope_audio_positions(audio_tokens)
     out = {
         "videoSelf": rope_tables_device(video, video_width, [20, 2048, 2048], heads, theta),
@@ -849,7 +862,7 @@ def rotaries(frames: int, height: int, width: int, frame_rate: float = 24.0,
     video = rope_video_positions_with_references(lf, height // 32, width // 32,
                                                  list(references), 8, 32, frame_rate)
     if audio_tokens is None:
-        audio_tokens = int(round(frames / frame_rate * 25.0))
+        audio_tokens = audio_latent_count(frames, frame_rate)
     audio = rope_audio_positions(audio_tokens)
     return {
         "videoSelf": rope_tables(video, video_width, [20, 2048, 2048], heads, theta),

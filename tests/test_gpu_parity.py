@@ -567,6 +567,46 @@ def test_c4_stage2_self_12480_norm_rope(device, kprep):
     _full_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, "c4", kprep=kprep)
 
 
+AUDIO_101_CASES = [
+    # label, (query tokens, width), (key tokens, width), q table, k table
+    ("audio_attn1", ("a", 2048), ("a", 2048), "audioSelf", None),
+    ("audio_attn2", ("a", 2048), ("t", 2048), None, None),
+    ("audio_to_video", ("v", 2048), ("a", 2048), "videoCross", "audioCross"),
+    ("video_to_audio", ("a", 2048), ("v", 2048), "audioCross", "videoCross"),
+]
+
+
+@pytest.mark.parametrize("case", AUDIO_101_CASES, ids=[c[0] for c in AUDIO_101_CASES])
+def test_audio_stream_at_formula_token_count(device, case):
+    """The audio stream's attentions at the token count the geometry formula gives for 97
+    frames at 24 fps (LatentGeometry.swift:128-132: round(97 / 24 * 25) = 101, against the 126
+    of 121 frames) beside 3120 video tokens (640x384) and 1024 unmasked text tokens, with the
+    tables rotaries builds for that clip and separate q / k norm weights."""
+    label, (qs, qw), (ks, kwid), qtab, ktab = case
+    H, D = 32, 64
+    Ta = L.audio_latent_count(97, 24.0)
+    assert Ta == 101
+    tokens = {"v": 3120, "a": Ta, "t": 1024}
+    seed = 0x5EED + 400 + 10 * AUDIO_101_CASES.index(case)
+    _say(f"audio stream at 101 tokens, {label}: Lq {tokens[qs]} Lk {tokens[ks]}")
+    tq, qb = _gpu_bits((1, tokens[qs], qw), seed, device)
+    tk, kb = _gpu_bits((1, tokens[ks], kwid), seed + 1, device)
+    tv, vb = _gpu_bits((1, tokens[ks], kwid), seed + 2, device)
+    wq, wqb = _gpu_bits((qw,), seed + 3, device, 1.0, 0.02)
+    wk, wkb = _gpu_bits((kwid,), seed + 4, device, 1.0, 0.02)
+    kw_host = dict(q_norm_w=wqb, k_norm_w=wkb)
+    kw_dev = dict(q_norm_w=wq, k_norm_w=wk)
+    tabs = L.rotaries(97, 384, 640)
+    assert tabs["audioSelf"][0].shape[1] == Ta and tabs["videoCross"][0].shape[1] == 3120
+    for name, host_keys, dev_key in ((qtab, ("q_cos", "q_sin"), "rotary"),
+                                     (ktab, ("k_cos", "k_sin"), "key_rotary")):
+        if name:
+            kw_host.update({host_keys[0]: tabs[name][0], host_keys[1]: tabs[name][1]})
+            kw_dev[dev_key] = L.Rotary(dev(tabs[name][0], device), dev(tabs[name][1], device))
+    assert H * D == qw
+    _full_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, f"audio101 {label}")
+
+
 C5_CASES = [
     # label, query stream (tokens, width), key stream, D, q table, k table, text keys valid
     ("attn1", ("v", 4096), ("v", 4096), 128, "videoSelf", None, None),

@@ -142,3 +142,23 @@ def test_rotaries_with_references_extend_the_video_tables():
     cos, sin = L.rope_tables(grid[:, T:], 4096, [20, 2048, 2048], 32)
     assert np.array_equal(withr["videoSelf"][0][:, T:], cos)
     assert np.array_equal(withr["videoSelf"][1][:, T:], sin)
+
+
+@pytest.mark.parametrize("frames,fps,tokens", [
+    (97, 24.0, 101), (121, 24.0, 126), (25, 24.0, 26), (12, 24.0, 13), (1, 24.0, 1),
+    (121, 30.0, 101), (36, 24.0, 38),
+])
+def test_audio_latent_count_rounds_half_away_from_zero(frames, fps, tokens):
+    """LatentGeometry.audioLatentCount (LatentGeometry.swift:128-132): round, not ceil, and
+    Swift's rounded() takes 12.5 (12 frames at 24 fps) to 13 where Python's round gives 12;
+    36 frames are 37.5 -> 38 (even would also give 38), 121 at 30 fps 100.83 -> 101."""
+    assert L.audio_latent_count(frames, fps) == tokens
+    assert L.rotaries(frames, 64, 64)["audioSelf"][0].shape[1] == \
+        L.audio_latent_count(frames, 24.0)
+
+
+def test_audio_latent_count_refuses_empty_clips():
+    with pytest.raises(L.Failure):
+        L.audio_latent_count(0, 24.0)
+    with pytest.raises(L.Failure):
+        L.audio_latent_count(97, 0.0)
