@@ -641,6 +641,12 @@ def main():
                     help="only run the short-key calls (text cross-attention, the cross-modal "
                          "pair, the block set's video->text and video->audio-keys calls), "
                          "--steps times each (for counter passes)")
+    ap.add_argument("--c1-only", action="store_true",
+                    help="only run the 3120-token self-attention, --steps timed calls (for "
+                         "counter passes)")
+    ap.add_argument("--block-only", action="store_true",
+                    help="only run one DiT block's six attentions at 1280x768x121, B=2, "
+                         "--steps times (for counter passes)")
     ap.add_argument("--gemma-only", action="store_true",
                     help="only run the Gemma-4 encoder attention (sliding and full layer at "
                          "1024 tokens), --steps timed calls each")
@@ -684,6 +690,16 @@ def main():
             L.linear(xin, w, out=y, sumsq=True)
         torch.cuda.synchronize()
         print(json.dumps({"projection": [12480, 4096, 4096], "launches": args.steps}), flush=True)
+        return
+
+    if args.c1_only:
+        res = bench_c1(device, args.steps, args.warmup, hip)
+        print(json.dumps({"video_self_3120": {k: v for k, v in res.items()}}), flush=True)
+        return
+
+    if args.block_only:
+        res = bench_c5(device, args.steps, args.warmup, hip)
+        print(json.dumps({"dit_block_attn": res}), flush=True)
         return
 
     if args.gemma_only:
