@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define LTX_ATTN_ABI_VERSION 6
+#define LTX_ATTN_ABI_VERSION 7
 
 /* Status codes. The reference throws `DiTAttention.Failure` for structural errors
  * (DiTAttention.swift:107-121); a Swift wrapper maps these onto thrown errors. */
@@ -208,10 +208,22 @@ typedef struct ltx_linear_args {
      * fused projection) have their own partials. */
     float *sumsq;
     int64_t sumsq_rs;
+    /* Device scratch for the fp32 partial tiles of a split tail (see
+     * ltx_linear_workspace_bytes), 256-byte aligned, or NULL. With less than that the tail
+     * tiles run whole: same result up to fp32 summation order, slower. */
+    void *workspace;
+    size_t workspace_bytes;
 } ltx_linear_args;
 
 /* ceil(N / LTX_LINEAR_SUMSQ_COLS): partial sums per row of y. */
 int32_t ltx_linear_sumsq_blocks(int32_t N);
+
+/* Bytes of workspace that let ltx_linear split its tail: the 256 x 256 tiles past the last
+ * whole round of 256 (one per CU) are cut along K into as many ranges as fill the CUs, and a
+ * fixup launch sums each tile's ranges (256 KiB of fp32 per range; 0 when the tiles fill
+ * whole rounds or the tail is more than half a round). Pure host function; 0 for invalid
+ * arguments. No counterpart in the reference, whose matmul (MLX) manages its own scratch. */
+size_t ltx_linear_workspace_bytes(const ltx_linear_args *a);
 
 /* Run the projection asynchronously on `stream` (a hipStream_t or NULL). The fp32
  * accumulator is rounded to bf16, then the bias is added in fp32 and rounded again, as the

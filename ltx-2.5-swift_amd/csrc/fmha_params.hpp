@@ -113,6 +113,12 @@ struct LinearParams {
     int64_t ss_rs;
     int32_t M, N, K;
     int32_t tiles_m, tiles_n;
+    // Tail split: tiles [n_full, tiles_m * tiles_n) of the tile order are cut into `splits`
+    // ranges of `steps_per_split` 64-wide k steps; each range writes its fp32 accumulators to
+    // part (256 KiB per range, tile-major) and linear_fixup_kernel sums them. splits == 1:
+    // every tile whole (n_full = tiles_m * tiles_n).
+    float *part;
+    int32_t n_full, splits, steps_per_split;
 };
 
 // RMS statistic from partial sums of squares: rstd[row] = 1/sqrt(sum_j parts[row][j] / n + eps)
@@ -169,6 +175,7 @@ int launch_combine(const CombineParams &p, int D, void *stream);
 int launch_passthrough(const PassParams &p, int D, void *stream);
 int launch_rstd(const RstdParams &p, void *stream);
 int launch_linear(const LinearParams &p, void *stream);           // linear_gemm.hip
+int64_t linear_part_bytes(int64_t tail_tiles, int splits);          // one range: 256 KiB
 int launch_gemma_prep(const GemmaPrepParams &p, int D, void *stream);   // gemma_attn.hip
 int launch_gemma_attn(const GemmaAttnParams &p, int D, void *stream);
 

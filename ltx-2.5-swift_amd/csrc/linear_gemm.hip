@@ -28,6 +28,13 @@
 //
 // Rounding follows the reference's two operations: the fp32 accumulator is rounded to bf16
 // (the matmul's output), then the bias is added in fp32 and the sum rounded to bf16 again.
+//
+// Tail split: one workgroup runs per CU, so a tile count just past a multiple of 256 costs a
+// whole extra round (12480 x 4096: 784 tiles = 3 rounds + 16 tiles). The host cuts the tiles
+// past the last whole round into k ranges, as many per tile as fill the CUs (16 tiles -> 16
+// ranges of 4 k steps each); a range stores its fp32 accumulators, in register order, to the
+// workspace, and linear_fixup_kernel sums a tile's ranges in order and runs the same epilogue
+// (eight workgroups per tile).
 #include <type_traits>
 
 #include "lds_copy.hpp"
@@ -55,165 +62,52 @@ __device__ __forceinline__ int lswz(int row, int u) {
     return U == 8 ? (u ^ ((row >> 1) & 7)) : (u ^ ((row >> 2) & 3));
 }
 
-template <int BK>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
-void linear_kernel(const LinearParams p) {
-    using T = LinTile<BK>;
-    constexpr int U = T::U, CPT = T::CPT, NCH = T::NCH, ELEMS = T::ELEMS;
-    __shared__ __attribute__((aligned(16))) bf16 sW[2 * ELEMS];
-    __shared__ __attribute__((aligned(16))) bf16 sX[2 * ELEMS];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
-    const int r = lane & 31, g = lane >> 5;
-
-    // Tile of this workgroup. Workgroups go to the 8 XCDs round-robin; each XCD gets a
-    // contiguous range of the tile order, which walks groups of 8 row tiles column tile by
-    // column tile, so the ~32 workgroups an XCD runs at once share 8 row tiles of x and 4
-    // column tiles of w in its L2.
-    const int total = p.tiles_m * p.tiles_n;
-    const int wg = blockIdx.x;
-    const int xcd = wg & 7, slot = wg >> 3;
-    const int q8 = total >> 3, r8 = total & 7;
-    const int t = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + slot;
+// Tile t of the tile order -> (row tile, column tile): groups of 8 row tiles, walked column
+// tile by column tile.
+__device__ __forceinline__ void tile_coords(const LinearParams &p, int t, int &tm, int &tn) {
     constexpr int GRP = 8;
     const int group = t / (GRP * p.tiles_n);
     const int first_m = group * GRP;
     const int rows_g = min(GRP, p.tiles_m - first_m);
     const int within = t - group * GRP * p.tiles_n;
-    const int tm = first_m + within % rows_g, tn = within / rows_g;
-    const int m0 = tm * LT, n0 = tn * LT;
+    tm = first_m + within % rows_g;
+    tn = within / rows_g;
+}
 
-    // ---- copies HBM -> LDS ----------------------------------------------------------
-    const int xrow = (int)(p.x_rs * 2), wrow = (int)(p.w_rs * 2);    // row bytes
-    const char *X0 = (const char *)p.x + (int64_t)m0 * xrow;
-    const char *W0 = (const char *)p.w + (int64_t)n0 * wrow;
-    const int64_t xbytes = (int64_t)min(LT, p.M - m0) * xrow;
-    const int64_t wbytes = (int64_t)min(LT, p.N - n0) * wrow;
-    // Copy j of this wave's share of a tile: LDS unit q = (wave*CPT + j)*64 + lane holds row
-    // q / U, logical unit lswz(row, q % U); its source offset is fixed for the whole tile, the
-    // k step moves the resource's base.
-    int xl[CPT], wl[CPT];
-#pragma unroll
-    for (int j = 0; j < CPT; ++j) {
-        const int q = (wave * CPT + j) * 64 + lane;
-        const int row = q / U, u = lswz<U>(row, q % U);
-        xl[j] = row * xrow + 16 * u;
-        wl[j] = row * wrow + 16 * u;
-    }
-    // Copy j (0 .. 2*CPT-1) of this wave's share of k step s into buffer st: even j of w, odd
-    // of x.
-    auto copy_one = [&](int s, int st, int j) __attribute__((always_inline)) {
-        const int kb = s * BK * 2;
-        if ((j & 1) == 0) {
-            copy_all(rsrc_words(W0 + kb, wbytes),
-                     (uint32_t)(uintptr_t)((lds_bf16 *)sW + st * ELEMS + (wave * CPT + j / 2) * 512),
-                     wl[j / 2]);
-        } else {
-            copy_all(rsrc_words(X0 + kb, xbytes),
-                     (uint32_t)(uintptr_t)((lds_bf16 *)sX + st * ELEMS + (wave * CPT + j / 2) * 512),
-                     xl[j / 2]);
-        }
-    };
-    // Operand of rows row0 + 0..31, reduction chunk c: lane (r, g) reads row row0 + r, unit 2c + g.
-    auto frag = [&](const lds_bf16 *S, int row0, int c) __attribute__((always_inline)) {
-        const int row = row0 + r;
-        return *(const __attribute__((address_space(3))) bf16x8 *)(S + row * BK + 8 * lswz<U>(row, 2 * c + g));
-    };
-
-    f32x16 acc[4][4];              // [n block][m block]
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = splat16(0.f);
-
-    const int nsteps = p.K / BK;
-    bf16x8 a[2][4], b[2][4];       // operands of the current and the next chunk
-    auto read_chunk = [&](int st, int c, int buf) __attribute__((always_inline)) {
-        const lds_bf16 *Ws = (const lds_bf16 *)sW + st * ELEMS;
-        const lds_bf16 *Xs = (const lds_bf16 *)sX + st * ELEMS;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            a[buf][i] = frag(Ws, wn * 128 + 32 * i, c);
-            b[buf][i] = frag(Xs, wm * 128 + 32 * i, c);
-        }
-    };
-    // Prologue: steps 0 and 1 into both buffers, then step 0's first operands.
-#pragma unroll
-    for (int j = 0; j < 2 * CPT; ++j) copy_one(0, 0, j);
-    if (nsteps > 1) {
-#pragma unroll
-        for (int j = 0; j < 2 * CPT; ++j) copy_one(1, 1, j);
-        wait_copies_but<2 * CPT>();
-    } else {
-        wait_copies();
-    }
-    __syncthreads();
-    read_chunk(0, 0, 0);
-
-    // One k step; COPY: issue the copies of step s + 2, NEXT: read step s + 1's first operands.
-    auto step = [&](int s, auto copy, auto next) __attribute__((always_inline)) {
-        const int st = s & 1;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const int cb = c & 1;          // NCH is even: chunk 0 of every step is in buffer 0
-            if (c < NCH - 1) {
-                read_chunk(st, c + 1, cb ^ 1);
-            } else {
-                // Step s+1's copies (issued one step ago) have landed for this wave; after the
-                // barrier they have for every wave, and every wave's reads of buffer st are done.
-                // The scheduling fences keep the earlier chunks' products ahead of the wait.
-                __builtin_amdgcn_sched_barrier(0);
-                wait_copies();
-                __syncthreads();
-                __builtin_amdgcn_sched_barrier(0);
-                if (decltype(next)::value) read_chunk(st ^ 1, 0, 0);
-            }
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-                for (int mb = 0; mb < 4; ++mb) {
-                    acc[nb][mb] = mfma32(a[cb][nb], b[cb][mb], acc[nb][mb]);
-                    if (decltype(copy)::value && c == NCH - 1) {
-                        copy_one(s + 2, st, 4 * nb + mb);      // one copy per product
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                }
-        }
-    };
-    using yes = std::true_type;
-    using no = std::false_type;
-    int s = 0;
-    for (; s + 2 < nsteps; ++s) step(s, yes{}, yes{});
-    if (s + 1 < nsteps) step(s++, no{}, yes{});
-    step(s, no{}, no{});
-
-    // ---- epilogue ---------------------------------------------------------------------
-    // Lane (r, g) of product (nb, mb) holds y[m][n + e] for m = m0 + wm*128 + 32*mb + r,
-    // n = n0 + wn*128 + 32*nb + 8*qd + 4*g (qd = 0..3), e = 0..3 in accumulator 4*qd + e.
+// Epilogue of NMB 32-row blocks of a wave: round to bf16, add the bias, store, and the rows'
+// sums of squares. Lane (r, g) of product (nb, mb) holds y[m][n + e] for
+// m = mrow + 32*mb + r, n = ncol + 32*nb + 8*qd + 4*g (qd = 0..3), e = 0..3 in accumulator
+// 4*qd + e; the wave covers columns [ncol, ncol + 128) of column tile tn, the workgroup's two
+// waves of one row range (wn = 0, 1) all 256. The workgroup's rows are the `rows` rows from
+// mrow - red_off, in which the wave's blocks start at red_off. Every thread calls it.
+template <int NMB>
+__device__ __forceinline__ void store_rows(const LinearParams &p, const f32x16 (&acc)[4][NMB],
+                                           int mrow, int ncol, int tn, int wn, int red_off,
+                                           int rows) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int r = lane & 31, g = lane >> 5;
     u32x2 bias[4][4];
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
-            const int n = n0 + wn * 128 + 32 * nb + 8 * qd + 4 * g;
+            const int n = ncol + 32 * nb + 8 * qd + 4 * g;
             bias[nb][qd] = (p.bias && n < p.N) ? *(const u32x2 *)((const bf16 *)p.bias + n)
                                                : u32x2{0u, 0u};
         }
     __shared__ float red[2][LT];
-    float ss[4];
+    float ss[NMB];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-        const int m = m0 + wm * 128 + 32 * mb + r;
+    for (int mb = 0; mb < NMB; ++mb) {
+        const int m = mrow + 32 * mb + r;
         bf16 *yrow = (bf16 *)p.y + (int64_t)m * p.y_rs;
         float sum = 0.f;
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
             for (int qd = 0; qd < 4; ++qd) {
-                const int n = n0 + wn * 128 + 32 * nb + 8 * qd + 4 * g;
+                const int n = ncol + 32 * nb + 8 * qd + 4 * g;
                 const f32x16 &c = acc[nb][mb];
                 u32x2 w;
                 w[0] = pack_bf2(c[4 * qd + 0], c[4 * qd + 1]);
@@ -237,18 +131,207 @@ void linear_kernel(const LinearParams p) {
     if (!p.sumsq) return;
     if (g == 0) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) red[wn][wm * 128 + 32 * mb + r] = ss[mb];
+        for (int mb = 0; mb < NMB; ++mb) red[wn][red_off + 32 * mb + r] = ss[mb];
     }
     __syncthreads();
-    const int m = m0 + tid;
-    if (m < p.M) p.sumsq[(int64_t)m * p.ss_rs + tn] = red[0][tid] + red[1][tid];
+    const int m = mrow - red_off + tid;
+    if (tid < rows && m < p.M) p.sumsq[(int64_t)m * p.ss_rs + tn] = red[0][tid] + red[1][tid];
+}
+
+template <int BK>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void linear_kernel(const LinearParams p) {
+    using T = LinTile<BK>;
+    constexpr int U = T::U, CPT = T::CPT, NCH = T::NCH, ELEMS = T::ELEMS;
+    __shared__ __attribute__((aligned(16))) bf16 sW[2 * ELEMS];
+    __shared__ __attribute__((aligned(16))) bf16 sX[2 * ELEMS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r = lane & 31, g = lane >> 5;
+
+    // Tile of this workgroup. Workgroups go to the 8 XCDs round-robin; in each region of the
+    // grid (whole tiles, then tail ranges) each XCD gets a contiguous range of the tile order,
+    // which walks groups of 8 row tiles column tile by column tile, so the ~32 workgroups an
+    // XCD runs at once share 8 row tiles of x and 4 column tiles of w in its L2, and the
+    // ranges of one tail tile share all of it.
+    const int bid = blockIdx.x;
+    const int nsteps = p.K / BK;
+    int t, k_begin = 0, k_end = nsteps, range = -1;
+    if (bid < p.n_full) {
+        t = xcd_major(bid, p.n_full);
+    } else {
+        const int n_tail = p.tiles_m * p.tiles_n - p.n_full;
+        range = xcd_major(bid - p.n_full, n_tail * p.splits);   // tile-major: (tile, split)
+        t = p.n_full + range / p.splits;
+        k_begin = (range % p.splits) * p.steps_per_split;
+        k_end = min(k_begin + p.steps_per_split, nsteps);
+    }
+    int tm, tn;
+    tile_coords(p, t, tm, tn);
+    const int m0 = tm * LT, n0 = tn * LT;
+
+    // Whole tiles and tail ranges run separate copies of what follows, so that neither's
+    // epilogue shares a register assignment with the other's (one shared copy spills).
+    auto body = [&](auto tail) __attribute__((always_inline)) {
+        // ---- copies HBM -> LDS ----------------------------------------------------------
+        const int xrow = (int)(p.x_rs * 2), wrow = (int)(p.w_rs * 2);    // row bytes
+        const char *X0 = (const char *)p.x + (int64_t)m0 * xrow;
+        const char *W0 = (const char *)p.w + (int64_t)n0 * wrow;
+        const int64_t xbytes = (int64_t)min(LT, p.M - m0) * xrow;
+        const int64_t wbytes = (int64_t)min(LT, p.N - n0) * wrow;
+        // Copy j of this wave's share of a tile: LDS unit q = (wave*CPT + j)*64 + lane holds row
+        // q / U, logical unit lswz(row, q % U); its source offset is fixed for the whole tile, the
+        // k step moves the resource's base.
+        int xl[CPT], wl[CPT];
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int q = (wave * CPT + j) * 64 + lane;
+            const int row = q / U, u = lswz<U>(row, q % U);
+            xl[j] = row * xrow + 16 * u;
+            wl[j] = row * wrow + 16 * u;
+        }
+        // Copy j (0 .. 2*CPT-1) of this wave's share of k step s into buffer st: even j of w, odd
+        // of x.
+        auto copy_one = [&](int s, int st, int j) __attribute__((always_inline)) {
+            const int kb = s * BK * 2;
+            if ((j & 1) == 0) {
+                copy_all(rsrc_words(W0 + kb, wbytes),
+                         (uint32_t)(uintptr_t)((lds_bf16 *)sW + st * ELEMS + (wave * CPT + j / 2) * 512),
+                         wl[j / 2]);
+            } else {
+                copy_all(rsrc_words(X0 + kb, xbytes),
+                         (uint32_t)(uintptr_t)((lds_bf16 *)sX + st * ELEMS + (wave * CPT + j / 2) * 512),
+                         xl[j / 2]);
+            }
+        };
+        // Operand of rows row0 + 0..31, reduction chunk c: lane (r, g) reads row row0 + r, unit 2c + g.
+        auto frag = [&](const lds_bf16 *S, int row0, int c) __attribute__((always_inline)) {
+            const int row = row0 + r;
+            return *(const __attribute__((address_space(3))) bf16x8 *)(S + row * BK + 8 * lswz<U>(row, 2 * c + g));
+        };
+
+        f32x16 acc[4][4];              // [n block][m block]
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = splat16(0.f);
+
+        bf16x8 a[2][4], b[2][4];       // operands of the current and the next chunk
+        auto read_chunk = [&](int st, int c, int buf) __attribute__((always_inline)) {
+            const lds_bf16 *Ws = (const lds_bf16 *)sW + st * ELEMS;
+            const lds_bf16 *Xs = (const lds_bf16 *)sX + st * ELEMS;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                a[buf][i] = frag(Ws, wn * 128 + 32 * i, c);
+                b[buf][i] = frag(Xs, wm * 128 + 32 * i, c);
+            }
+        };
+        // Prologue: the range's first two steps into both buffers, then the first operands.
+#pragma unroll
+        for (int j = 0; j < 2 * CPT; ++j) copy_one(k_begin, 0, j);
+        if (k_end - k_begin > 1) {
+#pragma unroll
+            for (int j = 0; j < 2 * CPT; ++j) copy_one(k_begin + 1, 1, j);
+            wait_copies_but<2 * CPT>();
+        } else {
+            wait_copies();
+        }
+        __syncthreads();
+        read_chunk(0, 0, 0);
+
+        // One k step; COPY: issue the copies of step s + 2, NEXT: read step s + 1's first operands.
+        auto step = [&](int s, auto copy, auto next) __attribute__((always_inline)) {
+            const int st = (s - k_begin) & 1;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int cb = c & 1;          // NCH is even: chunk 0 of every step is in buffer 0
+                if (c < NCH - 1) {
+                    read_chunk(st, c + 1, cb ^ 1);
+                } else {
+                    // Step s+1's copies (issued one step ago) have landed for this wave; after the
+                    // barrier they have for every wave, and every wave's reads of buffer st are done.
+                    // The scheduling fences keep the earlier chunks' products ahead of the wait.
+                    __builtin_amdgcn_sched_barrier(0);
+                    wait_copies();
+                    __syncthreads();
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (decltype(next)::value) read_chunk(st ^ 1, 0, 0);
+                }
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                    for (int mb = 0; mb < 4; ++mb) {
+                        acc[nb][mb] = mfma32(a[cb][nb], b[cb][mb], acc[nb][mb]);
+                        if (decltype(copy)::value && c == NCH - 1) {
+                            copy_one(s + 2, st, 4 * nb + mb);      // one copy per product
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
+            }
+        };
+        using yes = std::true_type;
+        using no = std::false_type;
+        int s = k_begin;
+        for (; s + 2 < k_end; ++s) step(s, yes{}, yes{});
+        if (s + 1 < k_end) step(s++, no{}, yes{});
+        step(s, no{}, no{});
+
+        if constexpr (decltype(tail)::value) {
+            // A tail range: its accumulators, in register order, for the fixup.
+            f32x16 *dst = (f32x16 *)(p.part + (int64_t)range * (LT * LT)) + wave * 16 * 64 + lane;
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb) dst[(4 * nb + mb) * 64] = acc[nb][mb];
+        } else {
+            store_rows<4>(p, acc, m0 + wm * 128, n0 + wn * 128, tn, wn, wm * 128, LT);
+        }
+    };
+    if (range >= 0) body(std::true_type{});
+    else body(std::false_type{});
+}
+
+// Tail tiles: the sum of a tile's k ranges, then the epilogue. Eight workgroups per tile, one
+// per 32-row block (wm, mb) of it, so the partials are read by as many CUs as a whole round
+// of the tail had; the workgroup's two waves are the block's column halves (wn).
+constexpr int kFixupThreads = 128;
+__global__ __attribute__((amdgpu_flat_work_group_size(kFixupThreads, kFixupThreads)))
+void linear_fixup_kernel(const LinearParams p) {
+    const int lane = threadIdx.x & 63, wn = threadIdx.x >> 6;
+    const int tt = blockIdx.x >> 3, wm = (blockIdx.x >> 2) & 1, mb = blockIdx.x & 3;
+    int tm, tn;
+    tile_coords(p, p.n_full + tt, tm, tn);
+    // the range's accumulators of wave (wm, wn), products (nb, mb), in register order
+    const f32x16 *src = (const f32x16 *)(p.part + (int64_t)tt * p.splits * (LT * LT)) +
+                        (2 * wm + wn) * 16 * 64 + mb * 64 + lane;
+    f32x16 acc[4][1];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) acc[nb][0] = src[nb * 4 * 64];
+    for (int sp = 1; sp < p.splits; ++sp) {
+        src += LT * LT / 16;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) acc[nb][0] += src[nb * 4 * 64];
+    }
+    store_rows<1>(p, acc, tm * LT + wm * 128 + 32 * mb, tn * LT + wn * 128, tn, wn, 0, 32);
 }
 
 }  // namespace
 
+int64_t linear_part_bytes(int64_t tail_tiles, int splits) {
+    return tail_tiles * splits * (int64_t)LT * LT * 4;
+}
+
 int launch_linear(const LinearParams &p, void *stream) {
-    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(256);
-    hipLaunchKernelGGL((linear_kernel<64>), grid, block, 0, (hipStream_t)stream, p);
+    const int n_tail = p.tiles_m * p.tiles_n - p.n_full;
+    const dim3 block(256);
+    hipLaunchKernelGGL((linear_kernel<64>), dim3((unsigned)(p.n_full + n_tail * p.splits)), block,
+                       0, (hipStream_t)stream, p);
+    if (n_tail > 0 && p.splits > 1)
+        hipLaunchKernelGGL(linear_fixup_kernel, dim3((unsigned)n_tail * 8), dim3(kFixupThreads),
+                           0, (hipStream_t)stream, p);
     return (int)hipGetLastError();
 }
 

@@ -683,6 +683,52 @@ int32_t ltx_linear_sumsq_blocks(int32_t N) {
     return N <= 0 ? 0 : (N + LTX_LINEAR_SUMSQ_COLS - 1) / LTX_LINEAR_SUMSQ_COLS;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Tail split of a projection: the tiles past the last whole round of kConcurrentGroups, when
+// they fill at most half a round, are cut into k ranges of at least two 64-wide steps, as many
+// per tile as keep every CU busy. Pure host arithmetic.
+struct LinearSplit {
+    int64_t tiles = 0, n_full = 0;
+    int32_t splits = 1, steps_per_split = 0;
+    size_t bytes = 0;
+};
+
+LinearSplit linear_split(int64_t M, int64_t N, int64_t K) {
+    LinearSplit ls;
+    const int64_t T = ((M + ltx::kLinearTile - 1) / ltx::kLinearTile) *
+                      ((N + ltx::kLinearTile - 1) / ltx::kLinearTile);
+    const int64_t nsteps = K / 64;
+    ls.tiles = ls.n_full = T;
+    ls.steps_per_split = (int32_t)nsteps;
+    const int64_t rem = T % kConcurrentGroups;
+    if (T == 0 || rem == 0 || 2 * rem > kConcurrentGroups || nsteps < 4) return ls;
+    int64_t s = std::min<int64_t>(kConcurrentGroups / rem, nsteps / 2);
+    const int64_t per = (nsteps + s - 1) / s;
+    s = (nsteps + per - 1) / per;          // no empty range
+    if (s < 2) return ls;
+    ls.n_full = T - rem;
+    ls.splits = (int32_t)s;
+    ls.steps_per_split = (int32_t)per;
+    ls.bytes = (size_t)ltx::linear_part_bytes(rem, (int)s);
+    return ls;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t ltx_linear_workspace_bytes(const ltx_linear_args *a) {
+    g_err[0] = 0;
+    if (!a || a->M < 0 || a->N < 8 || a->K < 64 || (a->K % 64)) {
+        fail(LTX_ATTN_EINVAL, "ltx_linear_workspace_bytes: invalid M, N or K");
+        return 0;
+    }
+    return linear_split(a->M, a->N, a->K).bytes;
+}
+
 ltx_attn_status ltx_linear(const ltx_linear_args *a, void *stream) {
     g_err[0] = 0;
     if (!a) return fail(LTX_ATTN_EINVAL, "args is NULL");
@@ -733,6 +779,26 @@ ltx_attn_status ltx_linear(const ltx_linear_args *a, void *stream) {
     p.sumsq = a->sumsq; p.ss_rs = a->sumsq_rs;
     p.M = a->M; p.N = a->N; p.K = a->K;
     p.tiles_m = (int32_t)tiles_m; p.tiles_n = (int32_t)tiles_n;
+    const LinearSplit ls = linear_split(a->M, a->N, a->K);
+    p.n_full = (int32_t)ls.tiles;
+    p.splits = 1;
+    p.steps_per_split = a->K / 64;
+    if (ls.splits > 1 && a->workspace && a->workspace_bytes >= ls.bytes) {
+        if ((uintptr_t)a->workspace & 255u)
+            return fail(LTX_ATTN_EINVAL, "linear workspace must be 256-byte aligned");
+        const uintptr_t wb = (uintptr_t)a->workspace, we = wb + ls.bytes;
+        auto overlaps = [&](std::pair<uintptr_t, uintptr_t> r) {
+            return wb < r.second && r.first < we;
+        };
+        if (overlaps(yb) || overlaps(span(a->x, a->M, a->x_rs, a->K, 2)) ||
+            overlaps(span(a->w, a->N, a->w_rs, a->K, 2)) ||
+            (a->sumsq && overlaps(span(a->sumsq, a->M, a->sumsq_rs, blocks, 4))))
+            return fail(LTX_ATTN_EINVAL, "linear workspace overlaps x, w, y or sumsq");
+        p.part = (float *)a->workspace;
+        p.n_full = (int32_t)ls.n_full;
+        p.splits = ls.splits;
+        p.steps_per_split = ls.steps_per_split;
+    }
     if (int e = ltx::launch_linear(p, stream))
         return fail(LTX_ATTN_EHIP, "linear launch: %s", hipGetErrorString((hipError_t)e));
     return LTX_ATTN_OK;

@@ -94,20 +94,24 @@ public:
         float *qs = reinterpret_cast<float *>(ws + L.qparts);
         float *ks = reinterpret_cast<float *>(ws + L.kparts);
         const int32_t Mq = batch * x.tokens, Mk = batch * kv.tokens;
-        project(w_.to_v, kv.data, kv.row_stride, Mk, v, n, nullptr, stream);
+        void *scratch = ws + L.attn;
+        const size_t sb = L.lin_bytes;
+        project(w_.to_v, kv.data, kv.row_stride, Mk, v, n, nullptr, scratch, sb, stream);
         if (!allPerturbed) {
-            project(w_.to_q, x.data, x.row_stride, Mq, q, n, qs, stream);
-            project(w_.to_k, kv.data, kv.row_stride, Mk, k, n, ks, stream);
+            project(w_.to_q, x.data, x.row_stride, Mq, q, n, qs, scratch, sb, stream);
+            project(w_.to_k, kv.data, kv.row_stride, Mk, k, n, ks, scratch, sb, stream);
         }
         const bool gated = w_.to_gate_logits.weight != nullptr;
-        if (gated) project(w_.to_gate_logits, x.data, x.row_stride, Mq, gate, heads, nullptr, stream);
+        if (gated)
+            project(w_.to_gate_logits, x.data, x.row_stride, Mq, gate, heads, nullptr, scratch,
+                    sb, stream);
         const DiTAttention::Stream sq{allPerturbed ? nullptr : q, (int64_t)x.tokens * n, n, x.tokens};
         const DiTAttention::Stream sk{allPerturbed ? nullptr : k, (int64_t)kv.tokens * n, n, kv.tokens};
         const DiTAttention::Stream sv{v, (int64_t)kv.tokens * n, n, kv.tokens};
         core_(batch, n, sq, sk, sv, merged, (int64_t)x.tokens * n, n, variant, rotary, keyRotary,
               ws + L.attn, L.attn_bytes, stream, k_valid_len, gated ? gate : nullptr,
               allPerturbed, allPerturbed ? nullptr : qs, allPerturbed ? nullptr : ks, blocks);
-        project(w_.to_out, merged, n, Mq, out, w_.to_out.out, nullptr, stream);
+        project(w_.to_out, merged, n, Mq, out, w_.to_out.out, nullptr, scratch, sb, stream);
     }
 
     size_t workspaceBytes(int32_t batch, const Input &x, const Input *context, Variant variant,
@@ -121,7 +125,7 @@ public:
 private:
     struct Layout {
         size_t v = 0, q = 0, k = 0, qparts = 0, kparts = 0, gate = 0, merged = 0, attn = 0;
-        size_t attn_bytes = 0, bytes = 0;
+        size_t attn_bytes = 0, lin_bytes = 0, bytes = 0;
     };
 
     static size_t up(size_t x) { return (x + 255) / 256 * 256; }
@@ -158,20 +162,33 @@ private:
             const char *why = ltx_attn_last_error();
             if (why && *why) throw Failure(LTX_ATTN_EINVAL, why);
         }
-        L.attn = take(L.attn_bytes);
+        // The projections' split-tail scratch shares that region: they run before and after
+        // the attention call on the same stream.
+        auto lin = [](const Linear &l, size_t M) {
+            ltx_linear_args a{};
+            a.M = (int32_t)M; a.N = l.out; a.K = l.in;
+            return l.weight ? ltx_linear_workspace_bytes(&a) : (size_t)0;
+        };
+        L.lin_bytes = std::max({lin(w_.to_v, Mk), lin(w_.to_q, Mq), lin(w_.to_k, Mk),
+                                lin(w_.to_gate_logits, Mq), lin(w_.to_out, Mq)});
+        L.attn = take(std::max(L.attn_bytes, L.lin_bytes));
         L.bytes = off;
         return L;
     }
 
-    // y [M, out] = x [M, in] . w^T (+ b), rows of x `x_rs` apart; `sumsq` optional partials.
+    // y [M, out] = x [M, in] . w^T (+ b), rows of x `x_rs` apart; `sumsq` optional partials;
+    // `scratch` the split tail's partial tiles.
     static void project(const Linear &l, const void *x, int64_t x_rs, int32_t M, void *y,
-                        int32_t y_rs, float *sumsq, void *stream) {
+                        int32_t y_rs, float *sumsq, void *scratch, size_t scratch_bytes,
+                        void *stream) {
         ltx_linear_args a{};
         a.M = M; a.N = l.out; a.K = l.in;
         a.x = x; a.w = l.weight; a.bias = l.bias; a.y = y;
         a.x_rs = x_rs; a.w_rs = l.in; a.y_rs = y_rs;
         a.sumsq = sumsq;
         a.sumsq_rs = ltx_linear_sumsq_blocks(l.out);
+        a.workspace = scratch;
+        a.workspace_bytes = scratch_bytes;
         DiTAttention::check(ltx_linear(&a, stream));
     }
 

@@ -77,6 +77,7 @@ class LinearArgs(ctypes.Structure):
         ("y", ctypes.c_void_p),
         ("x_rs", ctypes.c_int64), ("w_rs", ctypes.c_int64), ("y_rs", ctypes.c_int64),
         ("sumsq", ctypes.c_void_p), ("sumsq_rs", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -118,7 +119,7 @@ EXPORTED_SYMBOLS = (
     "ltx_attn_status_string", "ltx_attn_last_error", "ltx_attn_provenance",
     "ltx_attn_abi_version", "ltx_attn_args_size", "ltx_rope_frequency_grid", "ltx_rope_video_positions",
     "ltx_rope_audio_positions", "ltx_rope_tables", "ltx_rope_tables_device",
-    "ltx_linear", "ltx_linear_sumsq_blocks", "ltx_gemma_attn_workspace_bytes",
+    "ltx_linear", "ltx_linear_sumsq_blocks", "ltx_linear_workspace_bytes", "ltx_gemma_attn_workspace_bytes",
     "ltx_gemma_attn_fwd", "ltx_gemma_rope_tables", "ltx_device_count", "ltx_device_query",
     "ltx_attn_fwd_static", "ltx_rope_reference_positions",
     "ltx_rope_video_positions_with_references",
@@ -233,6 +234,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ltx_rope_tables_device.restype = ctypes.c_int
     lib.ltx_linear.argtypes = [ctypes.POINTER(LinearArgs), ctypes.c_void_p]
     lib.ltx_linear.restype = ctypes.c_int
+    lib.ltx_linear_workspace_bytes.argtypes = [ctypes.POINTER(LinearArgs)]
+    lib.ltx_linear_workspace_bytes.restype = ctypes.c_size_t
     lib.ltx_linear_sumsq_blocks.argtypes = [ctypes.c_int32]
     lib.ltx_linear_sumsq_blocks.restype = ctypes.c_int32
     lib.ltx_gemma_attn_workspace_bytes.argtypes = [ctypes.POINTER(GemmaArgs)]
@@ -479,7 +482,15 @@ def linear_sumsq_blocks(n: int) -> int:
     return load_library().ltx_linear_sumsq_blocks(n)
 
 
-def linear(x, weight, bias=None, *, out=None, sumsq=False, stream=None):
+def linear_workspace_bytes(M: int, N: int, K: int) -> int:
+    """Device scratch ``ltx_linear`` uses to split the tiles past its last whole round along K
+    (0 when it would not split them)."""
+    a = LinearArgs()
+    a.M, a.N, a.K = M, N, K
+    return load_library().ltx_linear_workspace_bytes(ctypes.byref(a))
+
+
+def linear(x, weight, bias=None, *, out=None, sumsq=False, stream=None, workspace=None):
     """``linear(_:_:)`` of ``DiTAttention.swift:178-188`` through ``ltx_linear``:
     ``y = x . weight^T (+ bias)``, bf16 in and out, fp32 accumulation.
 
@@ -488,7 +499,9 @@ def linear(x, weight, bias=None, *, out=None, sumsq=False, stream=None):
     ``bias``: bf16 ``[N]`` or None. ``out``: optional bf16 ``[..., N]`` view to write (unit
     last stride; e.g. a column slice of a fused buffer). ``sumsq=True`` also returns the
     statistic partials: fp32 ``[rows, ceil(N/256)]``, partial j of a row being the sum of
-    squares of its bf16 outputs over columns ``[256 j, 256 j + 256)``.
+    squares of its bf16 outputs over columns ``[256 j, 256 j + 256)``. ``workspace``: a
+    device tensor of at least ``linear_workspace_bytes(M, N, K)`` bytes for the split tail;
+    None allocates one when the shape splits, ``False`` runs every tile whole.
     Returns ``y`` or ``(y, partials)``.
     """
     import torch
@@ -523,6 +536,12 @@ def linear(x, weight, bias=None, *, out=None, sumsq=False, stream=None):
         nb = lib.ltx_linear_sumsq_blocks(N)
         parts = torch.empty((M, nb), dtype=torch.float32, device=x.device)
         a.sumsq, a.sumsq_rs = _ptr(parts), nb
+    need = lib.ltx_linear_workspace_bytes(ctypes.byref(a)) if M > 0 else 0
+    if workspace is None and need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    if workspace is not None and workspace is not False:
+        nbytes = workspace.numel() * workspace.element_size()
+        a.workspace, a.workspace_bytes = _ptr(workspace), nbytes
     if stream is None:
         stream = torch.cuda.current_stream(x.device).cuda_stream
     _check(lib.ltx_linear(ctypes.byref(a), ctypes.c_void_p(stream)))
@@ -606,28 +625,34 @@ class DiTAttentionModule:
             raise Failure(EINVAL, f"to_q.weight {tuple(q.shape)} is not [k * {heads}, queryDim]")
         self.core = DiTAttentionCore(weights["q_norm.weight"], weights["k_norm.weight"], heads)
 
-    def _lin(self, t, name, sumsq=False):
-        return linear(t, self.w[name + ".weight"], self.w.get(name + ".bias"), sumsq=sumsq)
+    def _lin(self, t, name, sumsq=False, workspace=None):
+        w = self.w[name + ".weight"]
+        # the call's workspace doubles as the projection's split-tail scratch when it is
+        # large enough (the projections and the attention run in stream order)
+        need = linear_workspace_bytes(t.numel() // t.shape[-1], w.shape[0], w.shape[1])
+        if workspace is not None and workspace.numel() * workspace.element_size() < need:
+            workspace = None
+        return linear(t, w, self.w.get(name + ".bias"), sumsq=sumsq, workspace=workspace)
 
     def __call__(self, x, context=None, *, variant: Variant, rotary: Optional[Rotary] = None,
                  key_rotary: Optional[Rotary] = None, k_valid_len=None,
                  all_perturbed: bool = False, workspace=None):
         kv = x if context is None else context                       # :327
         B, Lq, Lk = x.shape[0], x.shape[1], kv.shape[1]
-        v = self._lin(kv, "to_v")                                     # :341
+        v = self._lin(kv, "to_v", workspace=workspace)                # :341
         gate = None
         if "to_gate_logits.weight" in self.w:                          # :387-391
-            gate = self._lin(x, "to_gate_logits")
+            gate = self._lin(x, "to_gate_logits", workspace=workspace)
         if all_perturbed:                                              # :351-356
             o = self.core(None, None, v, variant=variant, gate_logits=gate, all_perturbed=True,
                           workspace=workspace)
         else:
-            q, qs = self._lin(x, "to_q", sumsq=True)                   # :358-359
-            k, ks = self._lin(kv, "to_k", sumsq=True)
+            q, qs = self._lin(x, "to_q", sumsq=True, workspace=workspace)     # :358-359
+            k, ks = self._lin(kv, "to_k", sumsq=True, workspace=workspace)
             o = self.core(q, k, v, variant=variant, rotary=rotary, key_rotary=key_rotary,
                           k_valid_len=k_valid_len, gate_logits=gate, workspace=workspace,
                           q_sumsq=qs.view(B * Lq, -1), k_sumsq=ks.view(B * Lk, -1))
-        return self._lin(o, "to_out.0")                               # :402-404
+        return self._lin(o, "to_out.0", workspace=workspace)          # :402-404
 
 
 class DiTBlockAttention:

@@ -153,18 +153,29 @@ public enum HIPAttention {
     /// `linear(_:_:)` (`DiTAttention.swift:178-188`) without LoRA: y [M, N] = x [M, K] .
     /// w [N, K]^T (+ bias), bf16; with `sumsq`, the fp32 [M, ceil(N/256)] partial sums of
     /// squares of y's rows that `Call` can take in place of the norm's own statistic pass.
+    /// `workspace` (at least `linearWorkspaceBytes` bytes, or nil) lets the tail tiles split.
     public static func linear(rows: Int32, outFeatures: Int32, inFeatures: Int32,
                               x: UnsafeRawPointer, xRowStride: Int64,
                               weight: UnsafeRawPointer, bias: UnsafeRawPointer?,
                               y: UnsafeMutableRawPointer, yRowStride: Int64,
                               sumsq: UnsafeMutablePointer<Float>?,
+                              workspace: UnsafeMutableRawPointer? = nil, workspaceBytes: Int = 0,
                               stream: UnsafeMutableRawPointer?) throws {
         var a = ltx_linear_args()
         a.M = rows; a.N = outFeatures; a.K = inFeatures
         a.x = x; a.w = weight; a.bias = bias; a.y = y
         a.x_rs = xRowStride; a.w_rs = Int64(inFeatures); a.y_rs = yRowStride
         a.sumsq = sumsq; a.sumsq_rs = Int64(ltx_linear_sumsq_blocks(outFeatures))
+        a.workspace = workspace; a.workspace_bytes = workspaceBytes
         try check(ltx_linear(&a, stream))
+    }
+
+    /// Scratch bytes that let `linear` split its tail tiles along K (0: none needed).
+    public static func linearWorkspaceBytes(rows: Int32, outFeatures: Int32,
+                                            inFeatures: Int32) -> Int {
+        var a = ltx_linear_args()
+        a.M = rows; a.N = outFeatures; a.K = inFeatures
+        return ltx_linear_workspace_bytes(&a)
     }
 }
 

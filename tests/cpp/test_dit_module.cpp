@@ -55,8 +55,13 @@ int main() {
                         up(2ull * T * 4096);
     EXPECT(need > proj, "workspace holds the projections and the attention's own");
     const size_t need_p = m.workspaceBytes(B, x, nullptr, V::videoSelf, &pe, nullptr, nullptr, true);
-    EXPECT(need_p == up(2ull * T * 4096) + up(2ull * T * 32) + up(2ull * T * 4096),
-           "perturbed: v, gate logits and the merged output only");
+    // the projections' split-tail scratch: to_v / to_out at 12480 x 4096 x 4096 is the largest
+    ltx_linear_args la{};
+    la.M = T; la.N = 4096; la.K = 4096;
+    const size_t scratch = ltx_linear_workspace_bytes(&la);
+    EXPECT(scratch == 16ull * 16 * 256 * 256 * 4, "linear scratch: 16 tail tiles x 16 k ranges");
+    EXPECT(need_p == up(2ull * T * 4096) + up(2ull * T * 32) + up(2ull * T * 4096) + up(scratch),
+           "perturbed: v, gate logits, the merged output and the projections' scratch only");
 
     // failures before any launch
     try {

@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layout_and_version():
     lib = L.load_library()
     assert lib.ltx_attn_args_size() == ctypes.sizeof(L.Args)
-    assert lib.ltx_attn_abi_version() == 6
+    assert lib.ltx_attn_abi_version() == 7
     assert "gfx950" in L.provenance()
     for s in range(5):
         assert lib.ltx_attn_status_string(s)
@@ -312,6 +312,41 @@ def test_linear_statistic_layout():
     a = _linear_args(sumsq=FAKE + (3 << 32), sumsq_rs=15)
     assert lib.ltx_linear(ctypes.byref(a), None) == L.EINVAL
     assert lib.ltx_linear(ctypes.byref(_linear_args(M=0)), None) == L.OK
+
+
+@pytest.mark.parametrize("M,N,K,tail_tiles,ranges", [
+    (12480, 4096, 4096, 16, 16),   # 784 tiles: 3 rounds + 16 tiles, 16 ranges of 4 steps
+    (12480, 12288, 4096, 48, 5),   # fused q/k/v: 2352 = 9 rounds + 48 tiles, 5 ranges of 13
+    (12480, 32, 4096, 49, 5),      # gate logits: 49 tiles in one round
+    (1000, 4096, 2048, 64, 4),     # 64 tiles, 4 ranges of 8 steps
+    (77, 32, 4096, 1, 32),         # one tile: 32 ranges of 2 steps
+    (3120, 4096, 4096, 0, 0),      # 208 tiles: a tail of more than half a round runs whole
+    (4096, 4096, 4096, 0, 0),      # 256 tiles: one whole round
+    (300, 520, 192, 0, 0),         # 3 k steps: too few to split
+])
+def test_linear_tail_split_workspace(M, N, K, tail_tiles, ranges):
+    """ltx_linear_workspace_bytes: 256 KiB of fp32 partials per k range of each tile past the
+    last whole round of 256; a host-only query."""
+    assert L.linear_workspace_bytes(M, N, K) == tail_tiles * ranges * 256 * 256 * 4
+    lib = L.load_library()
+    bad = _linear_args(K=96)
+    assert lib.ltx_linear_workspace_bytes(ctypes.byref(bad)) == 0
+    assert lib.ltx_attn_last_error().decode()
+
+
+def test_linear_workspace_is_checked():
+    """A workspace large enough to split is checked for alignment and overlap before a
+    launch; a smaller one (or none) means whole tiles, not an error."""
+    lib = L.load_library()
+    need = L.linear_workspace_bytes(12480, 4096, 4096)
+    base = FAKE + (8 << 32)
+    a = _linear_args(M=12480, N=4096, K=4096, x=base, w=base + (1 << 30),
+                     y=base + (2 << 30), x_rs=4096, w_rs=4096, y_rs=4096)
+    a.workspace, a.workspace_bytes = base + (3 << 30) + 128, need
+    assert lib.ltx_linear(ctypes.byref(a), None) == L.EINVAL          # not 256-byte aligned
+    a.workspace = base + (2 << 30)                                    # on top of y
+    assert lib.ltx_linear(ctypes.byref(a), None) == L.EINVAL
+    assert "overlaps" in lib.ltx_attn_last_error().decode()
 
 
 def test_zero_work_needs_no_gpu():

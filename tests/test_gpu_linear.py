@@ -113,24 +113,35 @@ def test_linear_strided_views_and_zero_rows(device):
 
 
 def test_fused_projection_equals_separate_ones(device):
-    """One GEMM over [to_q; to_k; to_v] weights writes the same bits, and the same statistic
-    partials for the q and k column ranges (which start at multiples of 256), as three
-    separate projections: each 256 x 256 tile depends only on its own rows of x and w."""
+    """With every tile whole (no tail split), one GEMM over [to_q; to_k; to_v] weights writes
+    the same bits, and the same statistic partials for the q and k column ranges (which start
+    at multiples of 256), as three separate projections: each 256 x 256 tile depends only on
+    its own rows of x and w. With the tail split (36 and 12 tiles: 7 and 16 k ranges) the
+    summation order differs, so the two agree within the fp32 bound of check_linear."""
     import torch
 
     M, inner, K = 700, 1024, 2048
-    x = dev(O.randn_bf16_bits((M, K), 41), device)
-    ws = [dev(O.randn_bf16_bits((inner, K), 42 + i, std=K ** -0.5), device) for i in range(3)]
-    bs = [dev(O.randn_bf16_bits((inner,), 45 + i, std=0.3), device) for i in range(3)]
+    xb = O.randn_bf16_bits((M, K), 41)
+    x = dev(xb, device)
+    wb = [O.randn_bf16_bits((inner, K), 42 + i, std=K ** -0.5) for i in range(3)]
+    bb = [O.randn_bf16_bits((inner,), 45 + i, std=0.3) for i in range(3)]
+    ws = [dev(w, device) for w in wb]
+    bs = [dev(b, device) for b in bb]
     fused_w = torch.cat(ws, dim=0).contiguous()
     fused_b = torch.cat(bs, dim=0).contiguous()
-    y, parts = L.linear(x, fused_w, fused_b, sumsq=True)
-    sep = [L.linear(x, ws[i], bs[i], sumsq=True) for i in range(3)]
+    y, parts = L.linear(x, fused_w, fused_b, sumsq=True, workspace=False)
+    sep = [L.linear(x, ws[i], bs[i], sumsq=True, workspace=False) for i in range(3)]
+    ys, ps = L.linear(x, fused_w, fused_b, sumsq=True)
+    sep_s = [L.linear(x, ws[i], bs[i], sumsq=True) for i in range(3)]
     torch.cuda.synchronize()
     nb = inner // 256
     for i, (yi, pi) in enumerate(sep):
         assert torch.equal(y[:, i * inner:(i + 1) * inner], yi), i
         assert torch.equal(parts[:, i * nb:(i + 1) * nb], pi), i
+    check_linear(host_bits(ys), xb, np.concatenate(wb), np.concatenate(bb), "fused, split")
+    for i, (yi, pi) in enumerate(sep_s):
+        check_linear(host_bits(yi), xb, wb[i], bb[i], f"separate {i}, split")
+        check_partials(pi.cpu().numpy(), host_bits(yi), f"separate {i}, split")
 
 
 def test_projection_rows_of_the_video_stage2_call(device):
@@ -199,3 +210,42 @@ def test_attention_takes_the_projection_statistic(device, Lq, Lk):
     c = O.compare(host_f32(given), host_f32(computed))
     _say(f"  given vs computed statistic: relRMS {c['rel_rms']:.2e} maxAbs {c['max_abs']:.2e}")
     assert c["rel_rms"] <= 1e-3 and c["max_abs"] <= MAX_ABS
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (12480, 4096, 4096),    # to_q at 12480 tokens: 784 tiles = 3 rounds + 16 tiles in 16 ranges
+    (12480, 32, 4096),      # to_gate_logits: 49 tiles in 5 ranges each
+])
+def test_tail_split_matches_whole_tiles(device, M, N, K):
+    """The tiles past the last whole round of 256, cut along K into ranges whose fp32 partials
+    the fixup kernel sums, against the same call with every tile whole (workspace=False):
+    each element within twice the fp32 summation bound plus one bf16 step; rows of a whole
+    tile and of the split tile row against the oracle; the statistic partials of every row."""
+    import torch
+
+    need = L.linear_workspace_bytes(M, N, K)
+    assert need > 0
+    x = O.randn_bf16_bits((M, K), 500 + N)
+    w = O.randn_bf16_bits((N, K), 600 + N, std=K ** -0.5)
+    b = O.randn_bf16_bits((N,), 700 + N, std=0.5)
+    xt, wt, bt = dev(x, device), dev(w, device), dev(b, device)
+    _say(f"linear tail split M={M} N={N} K={K}: {need >> 20} MiB of partials")
+    ws = torch.empty(need, dtype=torch.uint8, device=device)
+    y_split, p_split = L.linear(xt, wt, bt, sumsq=True, workspace=ws)
+    y_whole, _ = L.linear(xt, wt, bt, sumsq=True, workspace=False)
+    torch.cuda.synchronize()
+    ys, yw = host_f32(y_split).astype(np.float64), host_f32(y_whole).astype(np.float64)
+    xa = np.abs(O.bf16_bits_to_f32(x)).astype(np.float32)
+    wa = np.abs(O.bf16_bits_to_f32(w)).astype(np.float32)
+    gamma = K * U32 / (1 - K * U32)
+    acc = 2 * gamma * (xa @ wa.T).astype(np.float64) * 1.01
+    mm = np.abs(yw) + acc
+    bound = acc + _ulp_bf16(np.maximum(np.abs(ys), np.abs(yw))) + _ulp_bf16(mm)
+    diff = np.abs(ys - yw)
+    _say(f"  split vs whole: {np.count_nonzero(diff) / diff.size:.2e} of elements differ, "
+         f"max diff/bound {float(np.max(diff / bound)):.3f}")
+    assert np.all(diff <= bound)
+    ysb = host_bits(y_split)
+    rows = np.r_[0:64, M - 64:M]                  # a whole tile's rows, the split tile row's
+    check_linear(ysb[rows], np.ascontiguousarray(x[rows]), w, b, f"{M}x{N}x{K} split rows")
+    check_partials(p_split.cpu().numpy(), ysb, f"{M}x{N}x{K} split")
