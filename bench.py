@@ -390,7 +390,7 @@ def bench_gemma(device, steps, warmup):
         cos, sin = (torch.from_numpy(t).to(device) for t in
                     L.gemma_rope_tables(T, D, spec["theta"], spec["partial"], spec["proportional"]))
         out = torch.empty((1, T, Hq * D), dtype=torch.float32, device=device)
-        ws = torch.empty(64 << 20, dtype=torch.uint8, device=device)
+        ws = torch.empty(256 << 20, dtype=torch.uint8, device=device)   # q', k', v', partials
         ms = _time_ms(lambda: L.gemma_attention_fwd(
             q, k, v, q_heads=Hq, kv_heads=Hkv, q_norm_w=wq, k_norm_w=wk, cos=cos, sin=sin,
             window=spec["window"], out=out, workspace=ws), steps, warmup)

@@ -144,6 +144,8 @@ struct GemmaPrepParams {
     const float *cos, *sin;          // fp32 [T][D/2]
     void *qp, *qp_lo, *kp, *vt;      // bf16 outputs (workspace); q' as hi + lo parts
 };
+constexpr int kGemmaMaxChunks = 8;  // key ranges per Gemma query block, at most
+
 struct GemmaAttnParams {
     const void *qp, *qp_lo, *kp, *vt;
     float *out;                      // fp32 [B][T][Hq*D], element strides below
@@ -151,6 +153,13 @@ struct GemmaAttnParams {
     int32_t B, T, Hq, Hkv;
     int32_t window;                  // 0: causal only
     int32_t first_valid[kMaxBatch];  // keys below are left padding
+    // Key split: a query block's key blocks (32 keys each) run in ranges of `chunk` blocks,
+    // at most `nch_max` per query block; with more than one, each range writes fp32 partials
+    // (unnormalised O, then the row's max and sum) that gemma_combine_kernel merges. The grid
+    // is nch_max layers of B * Hq * query blocks.
+    int32_t chunk, nch_max;          // nch_max <= kGemmaMaxChunks
+    float *part_o;                   // [B * Hq * query blocks][nch_max][queries][D]
+    float *part_ml;                  // [B * Hq * query blocks][nch_max][queries][2]
 };
 
 // Host side: set the calling thread's error detail (ltx_attn_last_error) from a printf
@@ -178,5 +187,6 @@ int launch_linear(const LinearParams &p, void *stream);           // linear_gemm
 int64_t linear_part_bytes(int64_t tail_tiles, int splits);          // one range: 256 KiB
 int launch_gemma_prep(const GemmaPrepParams &p, int D, void *stream);   // gemma_attn.hip
 int launch_gemma_attn(const GemmaAttnParams &p, int D, void *stream);
+int gemma_queries_per_workgroup(int D);                              // 128 (D 256), 64 (D 512)
 
 }  // namespace ltx

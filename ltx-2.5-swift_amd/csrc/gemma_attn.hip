@@ -37,12 +37,13 @@
 // The key range of a query block is cut to the causal / window / padding bounds; query rows
 // inside the left padding (no allowed key) attend to every key unmasked, the reference's
 // rule for fully-masked rows.
-#include "fmha_device.hpp"
+#include <type_traits>
+
+#include "lds_copy.hpp"
+#include "mfma_s.hpp"
 
 namespace ltx {
 namespace {
-
-constexpr int kGemmaQB = 32;       // queries per workgroup
 
 // ---- prologue ------------------------------------------------------------------------------
 template <int D>
@@ -184,184 +185,282 @@ __global__ __launch_bounds__(256) void gemma_vt_kernel(const GemmaPrepParams p) 
 }
 
 // ---- attention -----------------------------------------------------------------------------
+// Geometry: a wave owns 32 queries over 256 channels of the head (D = 256: the whole head; D =
+// 512: one half, its partner wave the other). Four waves per workgroup: 128 queries at D =
+// 256, 64 at D = 512. A key block is 32 keys; its K' and V'^T operand units (D/16 and 2 * D/32
+// units of 1 KB, contiguous per block in the prologue's layout) are copied HBM -> LDS by the
+// buffer-load-to-LDS path into a ring of NS stages.
 template <int D>
-__global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p) {
-    constexpr int DS = D / 4;                       // channels per wave
-    constexpr int NCS = DS / 16;                    // 16-channel chunks of the wave's S slice
-    constexpr int NDS = DS / 32;                    // 32-channel blocks of the wave's O slice
-    // partial S per wave, double-buffered; 20-float lane rows keep the 16-byte accesses of
-    // 16 lanes on distinct banks
-    __shared__ __attribute__((aligned(16))) float sS[2][4][64][20];
+struct GemmaTile {
+    static constexpr int SPLIT = D / 256;            // waves per query group
+    static constexpr int QWG = 128 / SPLIT;          // queries per workgroup
+    static constexpr int NCW = 256 / 16;             // Q'/K' 16-channel chunks per wave
+    static constexpr int NDW = 256 / 32;             // V'^T / O 32-channel blocks per wave
+    static constexpr int KBYTES = D * 32 * 2;        // K' (or V'^T) of one key block
+    static constexpr int BLOCK = 2 * KBYTES;
+    static constexpr int NS = D == 256 ? 4 : 2;      // key blocks resident (copies in flight)
+    static constexpr int COPIES = BLOCK / 1024 / 4;  // 1 KB copies per wave per key block
+    static constexpr int XBYTES = SPLIT > 1 ? 4 * 64 * 16 * 4 : 0;   // S partial exchange
+};
 
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r = lane & 31, g = lane >> 5;
-    const int nqb = (p.T + kGemmaQB - 1) / kGemmaQB;
-    // heaviest (latest) query blocks first
-    const int qblk = nqb - 1 - (int)(blockIdx.x % nqb);
-    const int bh = (int)(blockIdx.x / nqb);
-    const int h = bh % p.Hq, b = bh / p.Hq;
-    const int kvh = h / (p.Hq / p.Hkv);
-    const int q0 = qblk * kGemmaQB;
-    const int fv = p.first_valid[b];
-    const int T = p.T;
-
-    // Q' slice of this wave: query q0 + r, channels wave*DS + 16c + 8g .. +7
-    const bf16 *Qh = (const bf16 *)p.qp + ((int64_t)b * p.Hq + h) * T * D + wave * DS;
-    const int qr = min(q0 + r, T - 1);
-    const bf16 *Ql = (const bf16 *)p.qp_lo + ((int64_t)b * p.Hq + h) * T * D + wave * DS;
-    bf16x8 qf[NCS], ql[NCS];
-#pragma unroll
-    for (int c = 0; c < NCS; ++c) {
-        qf[c] = __builtin_bit_cast(bf16x8, ldg16(Qh + (int64_t)qr * D + 16 * c + 8 * g));
-        ql[c] = __builtin_bit_cast(bf16x8, ldg16(Ql + (int64_t)qr * D + 16 * c + 8 * g));
-    }
-    // K' and V'^T of this KV head in operand order: per 32-key block, one 1 KB unit (64 lanes x
-    // 16 bytes) per operand, so each operand is one coalesced 16-byte load per lane.
-    const int nkb_all = (T + 31) / 32;
-    const bf16 *Kt = (const bf16 *)p.kp + ((int64_t)b * p.Hkv + kvh) * nkb_all * (D * 32) +
-                     (wave * NCS) * 512 + lane * 8;
-    const bf16 *Vt = (const bf16 *)p.vt + ((int64_t)b * p.Hkv + kvh) * nkb_all * (D * 32) +
-                     (wave * NDS) * 512 + lane * 8;
-
-    // Key blocks: causal / window / padding bounds; a block with rows inside the left padding
-    // (their rows have no allowed key) runs over all keys, those rows unmasked.
-    const int nkb = (T + 31) / 32;
-    const bool has_free_rows = q0 < fv;
-    int kb_lo = 0, kb_hi = nkb - 1;
-    if (!has_free_rows) {
-        kb_hi = min(q0 + kGemmaQB - 1, T - 1) / 32;
+// Key blocks of the query block [q0, q0 + nq): causal / window / padding bounds; a block with
+// rows inside the left padding (their rows have no allowed key) runs over all keys, those rows
+// unmasked.
+struct KeyBlocks {
+    int lo, hi;
+};
+__device__ __forceinline__ KeyBlocks gemma_key_blocks(const GemmaAttnParams &p, int q0, int nq,
+                                                      int fv) {
+    const int nkb = (p.T + 31) / 32;
+    KeyBlocks r{0, nkb - 1};
+    if (q0 >= fv) {
+        r.hi = min(q0 + nq - 1, p.T - 1) / 32;
         int lo = fv;
         if (p.window > 0) lo = max(lo, q0 - p.window + 1);
-        kb_lo = max(0, lo) / 32;
+        r.lo = max(0, lo) / 32;
     }
-    const int q = q0 + r;                           // this lane's query row
-    const bool free_row = q < fv;
+    return r;
+}
+
+// The fast pass keeps each row's max from its first block with an allowed key; a later block
+// whose weights would pass 2^kGemmaBound (log2 units over that max) sends the workgroup to
+// the exact pass, which rescales O and l whenever a row's max grows.
+constexpr float kGemmaBound = 64.0f;
+
+template <int D>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void gemma_attn_kernel(const GemmaAttnParams p) {
+    using G = GemmaTile<D>;
+    constexpr int SPLIT = G::SPLIT, QWG = G::QWG, NCW = G::NCW, NDW = G::NDW, NS = G::NS;
+    __shared__ __attribute__((aligned(16))) char smem[NS * G::BLOCK + G::XBYTES];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 31, g = lane >> 5;
+    const int grp = wave / SPLIT, half = wave % SPLIT;   // query group, channel half
+    const int T = p.T;
+    const int nqb = (T + QWG - 1) / QWG;
+    // grid layer `chunk` holds every query block's chunk-th key range; within a layer the
+    // heaviest (latest) query blocks come first, each across all (batch row, head) pairs, so
+    // the workgroups that the dispatcher deals to the 8 XCDs in turn carry equal work
+    const int nbh = p.B * p.Hq;
+    const int per_layer = nbh * nqb;
+    const int chunk = (int)blockIdx.x / per_layer;
+    const int rem = (int)blockIdx.x - chunk * per_layer;
+    const int qblk = nqb - 1 - rem / nbh;
+    const int bh = rem % nbh;
+    const int h = bh % p.Hq, b = bh / p.Hq;
+    const int kvh = h / (p.Hq / p.Hkv);
+    const int q0 = qblk * QWG;
+    const int fv = p.first_valid[b];
+    const KeyBlocks kr = gemma_key_blocks(p, q0, QWG, fv);
+    const int nch = (kr.hi - kr.lo + p.chunk) / p.chunk;
+    if (chunk >= nch) return;                        // this block has fewer key ranges
+    const int kb_lo = kr.lo + chunk * p.chunk;
+    const int kb_hi = min(kb_lo + p.chunk - 1, kr.hi);
+    const int nblk = kb_hi - kb_lo + 1;
+
+    // ---- copies of key blocks into the ring ---------------------------------------------
+    const int nkb_all = (T + 31) / 32;
+    const int64_t head_off = ((int64_t)b * p.Hkv + kvh) * nkb_all * (D * 32);   // elements
+    const u32x4 rk = rsrc_words((const bf16 *)p.kp + head_off, (int64_t)nkb_all * G::KBYTES);
+    const u32x4 rv = rsrc_words((const bf16 *)p.vt + head_off, (int64_t)nkb_all * G::KBYTES);
+    auto copy_block = [&](int i) __attribute__((always_inline)) {   // i-th block of the range
+        const int kb = kb_lo + i;
+        char *dst = smem + (i % NS) * G::BLOCK;
+#pragma unroll
+        for (int j = 0; j < G::COPIES; ++j) {
+            const int u = wave * G::COPIES + j;          // 1 KB unit of the block: K' then V'^T
+            const bool isk = u < G::KBYTES / 1024;
+            const int uu = isk ? u : u - G::KBYTES / 1024;
+            copy_all(isk ? rk : rv, (uint32_t)(uintptr_t)(lds_void *)(dst + u * 1024),
+                     kb * G::KBYTES + uu * 1024 + lane * 16);
+        }
+    };
+    // The first blocks' copies go out before the Q loads, so the two latencies overlap.
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i)
+        if (i < nblk) copy_block(i);
+
+    // ---- Q' of this wave: query q0 + 32 grp + r, channels 256 half + 16 c + 8 g .. +7 ---
+    const int q = q0 + 32 * grp + r;                 // this lane's query row
+    const int qr = min(q, T - 1);
+    const int64_t qoff = (((int64_t)b * p.Hq + h) * T + qr) * D + 256 * half + 8 * g;
+    bf16x8 qh[NCW], ql[NCW];
+#pragma unroll
+    for (int c = 0; c < NCW; ++c) {
+        qh[c] = __builtin_bit_cast(bf16x8, ldg16((const bf16 *)p.qp + qoff + 16 * c));
+        ql[c] = __builtin_bit_cast(bf16x8, ldg16((const bf16 *)p.qp_lo + qoff + 16 * c));
+    }
+    // Q' is only an MFMA operand: home it in AGPRs, leaving the VGPRs to S, P and operands
+#pragma unroll
+    for (int c = 0; c < NCW; ++c) asm volatile("" : "+a"(qh[c]), "+a"(ql[c]));
     // The row's allowed keys as one range [k_lo, k_hi]: all keys for a row inside the left
     // padding, else causal (k <= q), past the padding (k >= fv) and inside the window
     // (q - k < window); k_hi <= T - 1 also masks the keys past T of the last block.
+    const bool free_row = q < fv;
     const int k_lo = free_row ? 0 : max(fv, p.window > 0 ? q - p.window + 1 : 0);
     const int k_hi = free_row ? T - 1 : min(q, T - 1);
 
-    f32x16 o[NDS];
+    f32x16 o[NDW];
+    float m, l;
+    const f32x16 zero = splat16(0.f);               // the S chains' first SrcC
+    float *xs = (float *)(smem + NS * G::BLOCK);     // [4 waves][64 lanes][16] partial S
+    bool overflow = false;                           // some row's weights passed the bound
+
+    // One pass over the range's key blocks. SAFE: the exact online softmax (O and l rescaled
+    // when a row's max grows); otherwise each row's max is fixed at its first block with an
+    // allowed key. `first`: the ring's first blocks are already on their way.
+    auto run = [&](auto safe, bool first) __attribute__((always_inline)) {
+        constexpr bool SAFE = decltype(safe)::value;
 #pragma unroll
-    for (int db = 0; db < NDS; ++db) o[db] = splat16(0.f);
-    float m = -INFINITY, l = 0.f;
-    // Operands in flight: the block's K' rows are fetched one block ahead, its V'^T rows at
-    // the top of the block, so their latency overlaps the products, the exchange and the
-    // softmax instead of stalling each step.
-    auto load_k = [&](int kb, u32x4 (&kx)[NCS]) __attribute__((always_inline)) {
+        for (int db = 0; db < NDW; ++db) o[db] = splat16(0.f);
+        m = -INFINITY;
+        l = 0.f;
+        if (!first) {
 #pragma unroll
-        for (int c = 0; c < NCS; ++c) kx[c] = ldg16(Kt + ((int64_t)kb * (D / 16) + c) * 512);
-    };
-    // V'^T operand units of a block: channel block wave*NDS + db, key half hf
-    auto load_v = [&](int kb, u32x4 (&vx)[2][NDS]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-            for (int db = 0; db < NDS; ++db)
-                vx[hf][db] = ldg16(Vt + (((int64_t)kb * 2 + hf) * (D / 32) + db) * 512);
-    };
-    // D = 256 has the registers to hold the next block's V'^T as well (one block ahead, like
-    // K', in two buffers that alternate by block parity); D = 512 loads it at the top of its
-    // block.
-    constexpr bool kVAhead = D <= 256;
-    u32x4 kx[NCS];
-    u32x4 va[2][NDS], vb[2][NDS];
-    load_k(kb_lo, kx);
-    if constexpr (kVAhead) load_v(kb_lo, va);
-    // One 32-key block; `buf` selects the LDS exchange buffer, vc holds this block's V'^T
-    // (when loaded ahead) and vn receives the next block's.
-    auto block = [&](int kb, auto bufc, u32x4 (&vc)[2][NDS], u32x4 (&vn)[2][NDS])
-        __attribute__((always_inline)) {
-        constexpr int buf = decltype(bufc)::value;
-        u32x4 vl[2][NDS];
-        if constexpr (!kVAhead) load_v(kb, vl);
-        u32x4 (&vx)[2][NDS] = kVAhead ? vc : vl;
-        // partial S^T over this wave's channels: the hi and lo parts of q' in two chains
-        f32x16 sh = splat16(0.f), sl = splat16(0.f);
-#pragma unroll
-        for (int c = 0; c < NCS; ++c) {
-            const bf16x8 a = __builtin_bit_cast(bf16x8, kx[c]);
-            sh = mfma32(a, qf[c], sh);
-            sl = mfma32(a, ql[c], sl);
+            for (int i = 0; i < NS - 1; ++i)
+                if (i < nblk) copy_block(i);
         }
-        if (kb < kb_hi) {
-            load_k(kb + 1, kx);
-            if constexpr (kVAhead) load_v(kb + 1, vn);
-        }
+        for (int i = 0; i < nblk; ++i) {
+            // block i's copies have landed for this wave (later blocks' may still be in
+            // flight); after the barrier for every wave, and the stage of block i - 1 is free
+            if (i + NS - 2 < nblk) wait_copies_but<(NS - 2) * G::COPIES>();
+            else wait_copies();
+            __syncthreads();
+            if (i + NS - 1 < nblk) copy_block(i + NS - 1);
+            const char *Ks = smem + (i % NS) * G::BLOCK;
+            const char *Vs = Ks + G::KBYTES;
+            const int kb = kb_lo + i;
+            // S^T over this wave's channels: the hi and lo parts of q' in two interleaved
+            // chains, so consecutive products are independent and the matrix cores never wait
+            // for a result (inline products with S in VGPRs and Q' in AGPRs, mfma_s.hpp)
+            f32x16 sh, sl;
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4)
-            *(f32x4 *)&sS[buf][wave][lane][4 * i4] =
-                f32x4{sh[4 * i4] + sl[4 * i4], sh[4 * i4 + 1] + sl[4 * i4 + 1],
-                      sh[4 * i4 + 2] + sl[4 * i4 + 2], sh[4 * i4 + 3] + sl[4 * i4 + 3]};
-        __syncthreads();
-        f32x16 s;
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-            const f32x4 p0 = *(const f32x4 *)&sS[buf][0][lane][4 * i4];
-            const f32x4 p1 = *(const f32x4 *)&sS[buf][1][lane][4 * i4];
-            const f32x4 p2 = *(const f32x4 *)&sS[buf][2][lane][4 * i4];
-            const f32x4 p3 = *(const f32x4 *)&sS[buf][3][lane][4 * i4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) s[4 * i4 + e] = ((p0[e] + p1[e]) + p2[e]) + p3[e];
-        }
-        // mask: key k = 32kb + 8(i>>2) + 4g + (i&3) for query q
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int k = 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
-            s[i] = ((k >= k_lo) & (k <= k_hi)) ? s[i] : -INFINITY;
-            mx = fmaxf(mx, s[i]);
-        }
-        mx = fmaxf(mx, xlane32(mx));
-        const float mn = fmaxf(m, mx);
-        // fp32 weights, their fp32 row sums, and P as two bf16 parts for P.V (the reference's
-        // explicit path multiplies fp32 weights)
-        float alpha = 1.f, ts = 0.f;
-        u32x4 wh[2], wl[2];
-        if (mn == -INFINITY) {                      // nothing allowed yet in this row
-            wh[0] = wh[1] = wl[0] = wl[1] = u32x4{0, 0, 0, 0};
-        } else {
-            alpha = __builtin_amdgcn_exp2f(m - mn); // 0 when m is -inf
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float x0 = __builtin_amdgcn_exp2f(s[8 * hf + 2 * e] - mn);
-                    const float x1 = __builtin_amdgcn_exp2f(s[8 * hf + 2 * e + 1] - mn);
-                    ts += x0 + x1;
-                    const uint32_t hi = pack_bf2_opaque(x0, x1);
-                    wh[hf][e] = hi;
-                    wl[hf][e] = pack_bf2(x0 - bf_lo(hi), x1 - bf_hi(hi));
+            for (int c = 0; c < NCW; ++c) {
+                const bf16x8 a = *(const __attribute__((address_space(3))) bf16x8 *)(
+                    (lds_void *)(Ks + (half * NCW + c) * 1024 + lane * 16));
+                if (c == 0) {
+                    sh = mfma_s_first(a, qh[0], zero);
+                    sl = mfma_s_first(a, ql[0], zero);
+                } else {
+                    mfma_s_next(sh, a, qh[c]);
+                    mfma_s_next(sl, a, ql[c]);
                 }
-        }
-        m = mn;
-        l = l * alpha + ts;
-#pragma unroll
-        for (int db = 0; db < NDS; ++db) o[db] *= splat16(alpha);
-        // O^T += V^T.P^T
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-            for (int db = 0; db < NDS; ++db) {
-                const bf16x8 a = __builtin_bit_cast(bf16x8, vx[hf][db]);
-                o[db] = mfma32(a, __builtin_bit_cast(bf16x8, wh[hf]), o[db]);
-                o[db] = mfma32(a, __builtin_bit_cast(bf16x8, wl[hf]), o[db]);
             }
+            s_ready(sh, sl, zero, zero);
+            f32x16 s = sh + sl;
+            if constexpr (SPLIT > 1) {
+                // the partner wave holds the other half of the channels: exchange the partial
+                // sums and add them in a fixed order, so both waves hold the same S
+                float *mine = xs + (wave * 64 + lane) * 16;
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4)
+                    *(f32x4 *)(mine + 4 * i4) =
+                        f32x4{s[4 * i4], s[4 * i4 + 1], s[4 * i4 + 2], s[4 * i4 + 3]};
+                __syncthreads();
+                const float *lo_ = xs + ((2 * grp) * 64 + lane) * 16;
+                const float *hi_ = xs + ((2 * grp + 1) * 64 + lane) * 16;
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const f32x4 a0 = *(const f32x4 *)(lo_ + 4 * i4);
+                    const f32x4 a1 = *(const f32x4 *)(hi_ + 4 * i4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) s[4 * i4 + e] = a0[e] + a1[e];
+                }
+            }
+            // mask: key k = 32 kb + 8 (i >> 2) + 4 g + (i & 3) for query q
+            float mx = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int k = 32 * kb + 8 * (e >> 2) + 4 * g + (e & 3);
+                s[e] = ((k >= k_lo) & (k <= k_hi)) ? s[e] : -INFINITY;
+                mx = fmaxf(mx, s[e]);
+            }
+            mx = fmaxf(mx, xlane32(mx));
+            if constexpr (SAFE) {
+                if (__builtin_amdgcn_ballot_w64(mx > m) != 0) {
+                    const float mn = fmaxf(m, mx);
+                    const float alpha = mn > m ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;  // 0 from -inf
+#pragma unroll
+                    for (int db = 0; db < NDW; ++db) o[db] *= splat16(alpha);
+                    l *= alpha;
+                    m = mn;
+                }
+            } else {
+                if (m == -INFINITY) m = mx;              // the row's first allowed keys
+                overflow |= mx > m + kGemmaBound;
+            }
+            // fp32 weights, their fp32 row sums, and P as two bf16 parts for P.V (the
+            // reference's explicit path multiplies fp32 weights); a row with no allowed key
+            // so far has none
+            u32x4 wh[2], wl[2];
+            float ts = 0.f;
+            if (m == -INFINITY) {
+                wh[0] = wh[1] = wl[0] = wl[1] = u32x4{0, 0, 0, 0};
+            } else {
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x0 = __builtin_amdgcn_exp2f(s[8 * hf + 2 * e] - m);
+                        const float x1 = __builtin_amdgcn_exp2f(s[8 * hf + 2 * e + 1] - m);
+                        ts += x0 + x1;
+                        const uint32_t hi = pack_bf2_opaque(x0, x1);
+                        wh[hf][e] = hi;
+                        wl[hf][e] = pack_bf2(x0 - bf_lo(hi), x1 - bf_hi(hi));
+                    }
+            }
+            l += ts;
+            // O^T += V^T.P^T for this wave's channels; consecutive products update different
+            // accumulators (the hi parts of a key half over all channel blocks, then the lo)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                bf16x8 va[NDW];
+#pragma unroll
+                for (int db = 0; db < NDW; ++db)
+                    va[db] = *(const __attribute__((address_space(3))) bf16x8 *)(
+                        (lds_void *)(Vs + (hf * (D / 32) + half * NDW + db) * 1024 + lane * 16));
+#pragma unroll
+                for (int db = 0; db < NDW; ++db)
+                    o[db] = mfma32(va[db], __builtin_bit_cast(bf16x8, wh[hf]), o[db]);
+#pragma unroll
+                for (int db = 0; db < NDW; ++db)
+                    o[db] = mfma32(va[db], __builtin_bit_cast(bf16x8, wl[hf]), o[db]);
+            }
+        }
     };
-    for (int kb = kb_lo; kb <= kb_hi; kb += 2) {
-        block(kb, std::integral_constant<int, 0>{}, va, vb);
-        if (kb + 1 <= kb_hi) block(kb + 1, std::integral_constant<int, 1>{}, vb, va);
-    }
+    run(std::false_type{}, true);
+    // the exact pass, for the whole workgroup, when any row outgrew its fixed max
+    if (__syncthreads_or(overflow)) run(std::true_type{}, false);
 
     // ---- epilogue: O / l in fp32 (the reference's dtype here), this wave's channels ------
     const float lt = l + xlane32(l);
+    if (nch > 1) {
+        // one key range of several: unnormalised O, then (max, sum) per row, for the combine
+        const int64_t row = ((int64_t)(bh * nqb + qblk) * p.nch_max + chunk) * QWG + 32 * grp + r;
+        float *po = p.part_o + row * D + 256 * half;
+#pragma unroll
+        for (int db = 0; db < NDW; ++db)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                f32x4 w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = o[db][4 * i4 + e];
+                *(f32x4 *)(po + 32 * db + 8 * i4 + 4 * g) = w;
+            }
+        if (half == 0 && g == 0) {
+            p.part_ml[row * 2] = m;
+            p.part_ml[row * 2 + 1] = lt;
+        }
+        return;
+    }
     if (q < T) {
         const float inv = 1.0f / lt;
-        float *Ob = p.out + (int64_t)b * p.o_bs + (int64_t)q * p.o_rs + (int64_t)h * D + wave * DS;
+        float *Ob = p.out + (int64_t)b * p.o_bs + (int64_t)q * p.o_rs + (int64_t)h * D + 256 * half;
 #pragma unroll
-        for (int db = 0; db < NDS; ++db)
+        for (int db = 0; db < NDW; ++db)
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
                 f32x4 w;
@@ -370,6 +469,61 @@ __global__ __launch_bounds__(256) void gemma_attn_kernel(const GemmaAttnParams p
                 *(f32x4 *)(Ob + 32 * db + 8 * i4 + 4 * g) = w;
             }
     }
+}
+
+// Merge of a query block's key ranges: O = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c over
+// its ranges c (M the largest max; a range in which a row allows no key has m = -inf and adds
+// nothing), written in fp32. A thread per 4 channels of a row, 256 / (D / 4) rows per
+// workgroup, all of one query block (blocks with one range wrote their output themselves).
+template <int D>
+__global__ __launch_bounds__(256) void gemma_combine_kernel(const GemmaAttnParams p) {
+    constexpr int QWG = GemmaTile<D>::QWG;
+    constexpr int U = D / 4;                        // threads per row
+    constexpr int RPW = 256 / U;                    // rows per workgroup
+    const int nqb = (p.T + QWG - 1) / QWG;
+    const int wg_per_qb = QWG / RPW;
+    const int blk = (int)blockIdx.x / wg_per_qb;    // (batch row, head, query block)
+    const int qblk = blk % nqb;
+    const int bh = blk / nqb;
+    const int h = bh % p.Hq, b = bh / p.Hq;
+    const int q0 = qblk * QWG;
+    const KeyBlocks kr = gemma_key_blocks(p, q0, QWG, p.first_valid[b]);
+    const int nch = (kr.hi - kr.lo + p.chunk) / p.chunk;
+    if (nch <= 1) return;
+    const int rr = ((int)blockIdx.x % wg_per_qb) * RPW + (int)threadIdx.x / U;
+    const int c4 = (int)threadIdx.x % U;
+    const int q = q0 + rr;
+    if (q >= p.T) return;
+    const int64_t row0 = ((int64_t)blk * p.nch_max) * QWG + rr;
+    float mc[kGemmaMaxChunks], lc[kGemmaMaxChunks];
+    f32x4 oc[kGemmaMaxChunks];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < kGemmaMaxChunks; ++c) {
+        if (c < nch) {
+            const int64_t row = row0 + (int64_t)c * QWG;
+            mc[c] = p.part_ml[row * 2];
+            lc[c] = p.part_ml[row * 2 + 1];
+            oc[c] = *(const f32x4 *)(p.part_o + row * D + 4 * c4);
+            mx = fmaxf(mx, mc[c]);
+        }
+    }
+    float lsum = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < kGemmaMaxChunks; ++c) {
+        if (c < nch) {
+            const float wgt = mc[c] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc[c] - mx);
+            lsum += wgt * lc[c];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] += wgt * oc[c][e];
+        }
+    }
+    const float inv = 1.0f / lsum;
+    f32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = acc[e] * inv;
+    *(f32x4 *)(p.out + (int64_t)b * p.o_bs + (int64_t)q * p.o_rs + (int64_t)h * D + 4 * c4) = w;
 }
 
 }  // namespace
@@ -392,12 +546,22 @@ int launch_gemma_prep(const GemmaPrepParams &p, int D, void *stream) {
 }
 
 int launch_gemma_attn(const GemmaAttnParams &p, int D, void *stream) {
-    const int nqb = (p.T + kGemmaQB - 1) / kGemmaQB;
-    const dim3 grid((unsigned)((int64_t)p.B * p.Hq * nqb)), block(256);
+    const int qwg = D == 512 ? GemmaTile<512>::QWG : GemmaTile<256>::QWG;
+    const int64_t per_layer = (int64_t)p.B * p.Hq * ((p.T + qwg - 1) / qwg);
+    const dim3 grid((unsigned)(per_layer * p.nch_max)), block(256);
     hipStream_t st = (hipStream_t)stream;
     if (D == 512) hipLaunchKernelGGL(gemma_attn_kernel<512>, grid, block, 0, st, p);
     else hipLaunchKernelGGL(gemma_attn_kernel<256>, grid, block, 0, st, p);
+    if (p.nch_max > 1) {
+        const dim3 cgrid((unsigned)(per_layer * qwg / (256 / (D / 4))));
+        if (D == 512) hipLaunchKernelGGL(gemma_combine_kernel<512>, cgrid, block, 0, st, p);
+        else hipLaunchKernelGGL(gemma_combine_kernel<256>, cgrid, block, 0, st, p);
+    }
     return (int)hipGetLastError();
+}
+
+int gemma_queries_per_workgroup(int D) {
+    return D == 512 ? GemmaTile<512>::QWG : GemmaTile<256>::QWG;
 }
 
 }  // namespace ltx

@@ -332,8 +332,21 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
 // Gemma-4 text-encoder attention: validation and workspace layout.
 
 struct GemmaPlan {
-    size_t off_q = 0, off_qlo = 0, off_k = 0, off_v = 0, bytes = 0;
+    size_t off_q = 0, off_qlo = 0, off_k = 0, off_v = 0, off_po = 0, off_pml = 0, bytes = 0;
+    int32_t chunk = 0, nch_max = 1;
 };
+
+// Key blocks (32 keys) per range of a Gemma query block. The latest query blocks of a causal
+// layer walk every key block while the earliest walk a few; ranges of at most 16 blocks spread
+// the long ones over several CUs at the price of fp32 partials and a merge. Measured at 1024
+// tokens (MI355X, attention + merge): ranges of 16 blocks 45 + 7 us (D 256, 128-query
+// workgroups) and 79 + 11 us (D 512, 64-query workgroups), of 8 blocks 53 + 10 and 99 + 17 us.
+// Longer prompts take longer ranges, so that a query block never has more than the merge's
+// kGemmaMaxChunks.
+int32_t gemma_chunk_blocks(int32_t T) {
+    const int nkb = (T + 31) / 32;
+    return std::max(std::min(nkb, 16), (nkb + ltx::kGemmaMaxChunks - 1) / ltx::kGemmaMaxChunks);
+}
 
 ltx_attn_status gemma_plan(const ltx_gemma_attn_args *a, GemmaPlan *pl) {
     g_err[0] = 0;
@@ -384,6 +397,16 @@ ltx_attn_status gemma_plan(const ltx_gemma_attn_args *a, GemmaPlan *pl) {
     pl->off_k = pl->off_qlo + align_up(qn, 256);
     pl->off_v = pl->off_k + align_up(kn, 256);
     pl->bytes = pl->off_v + align_up(kn, 256);
+    const int qwg = ltx::gemma_queries_per_workgroup(a->D);
+    const int nkb = (a->T + 31) / 32, nqb = (a->T + qwg - 1) / qwg;
+    pl->chunk = gemma_chunk_blocks(a->T);
+    pl->nch_max = (nkb + pl->chunk - 1) / pl->chunk;
+    if (pl->nch_max > 1) {
+        const size_t rows = (size_t)a->B * a->Hq * nqb * pl->nch_max * qwg;
+        pl->off_po = pl->bytes;
+        pl->off_pml = pl->off_po + align_up(rows * D * 4, 256);
+        pl->bytes = pl->off_pml + align_up(rows * 2 * 4, 256);
+    }
     return LTX_ATTN_OK;
 }
 
@@ -621,6 +644,10 @@ ltx_attn_status ltx_gemma_attn_fwd(const ltx_gemma_attn_args *a, void *stream) {
     ap.out = a->out; ap.o_bs = a->o_bs; ap.o_rs = a->o_rs;
     ap.B = a->B; ap.T = a->T; ap.Hq = a->Hq; ap.Hkv = a->Hkv; ap.window = a->window;
     for (int b = 0; b < a->B; ++b) ap.first_valid[b] = a->first_valid ? a->first_valid[b] : 0;
+    ap.chunk = pl.chunk;
+    ap.nch_max = pl.nch_max;
+    ap.part_o = (float *)(ws + pl.off_po);
+    ap.part_ml = (float *)(ws + pl.off_pml);
     if (int e = ltx::launch_gemma_attn(ap, a->D, stream))
         return fail(LTX_ATTN_EHIP, "gemma attention launch: %s", hipGetErrorString((hipError_t)e));
     return LTX_ATTN_OK;

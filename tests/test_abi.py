@@ -548,7 +548,10 @@ def test_gemma_attention_rejects_bad_arguments():
 
     a = args()
     need = lib.ltx_gemma_attn_workspace_bytes(ctypes.byref(a))
-    assert need == 2 * 1024 * 256 * (2 * 16 + 8 + 8)      # q' (hi, lo), k', v'^T
+    # q' (hi, lo), k', v'^T, then the key split's partials: 128-query workgroups, whose 4..32
+    # key blocks run in ranges of at most 16 (two per query block): fp32 O and (max, sum) rows
+    rows = 1 * 16 * 8 * 2 * 128
+    assert need == 2 * 1024 * 256 * (2 * 16 + 8 + 8) + rows * 256 * 4 + rows * 2 * 4
     assert status(a)[0] == L.EWORKSPACE
     assert status(args(D=128))[0] == L.EUNSUPPORTED
     assert status(args(Hkv=3))[0] == L.EINVAL

@@ -5,7 +5,7 @@ Tolerance (the target's): relative RMS error <= 5e-3 and max-abs <= 2e-2 on the 
 (fp32 here, the dtype of the reference's explicit path) against the float64 oracle of the same
 inputs; in addition the kernel may be at most 1.25x as far from the truth as the reference's
 own arithmetic (``mode="reference"``: bf16 norms, fp32 RoPE and softmax), with a 2.5e-3
-floor.
+floor. Stress cases with logits far beyond the checkpoint's take only the relative bound.
 """
 
 import numpy as np
@@ -41,7 +41,8 @@ def _run(device, case):
     v = k if spec["shares_kv"] else O.randn_bf16_bits((B, T, Hkv * D), seed + 2)
     # weights at the checkpoint's magnitudes: q_norm ~1.03, k_norm ~0.12 (D 256) / ~0.06 (D 512)
     wq = O.randn_bf16_bits((D,), seed + 3, mean=1.03, std=0.02)
-    wk = O.randn_bf16_bits((D,), seed + 4, mean=0.12 if D == 256 else 0.06, std=0.01)
+    wk = O.randn_bf16_bits((D,), seed + 4, mean=case.get("wk_mean", 0.12 if D == 256 else 0.06),
+                           std=0.01)
     cos, sin = L.gemma_rope_tables(T, D, spec["theta"], spec["partial"], spec["proportional"])
     tq, tk = _dev(q, device), _dev(k, device)
     tv = tk if spec["shares_kv"] else _dev(v, device)
@@ -80,6 +81,20 @@ CASES = {
     # 8 KV heads at a ragged length with a window and padding in the same prompt
     "sliding_window17_T76_pad5": dict(B=1, T=76, kind="sliding", fv=[5], window=17,
                                       seed=0x5EED + 500),
+    # prompts longer than 32 key blocks: the latest query blocks' keys run as up to four
+    # ranges of 16 blocks merged afterwards, with padding and (sliding) a window inside them
+    "sliding_window700_T1600_pad200": dict(B=1, T=1600, kind="sliding", fv=[200], window=700,
+                                           seed=0x5EED + 510),
+    "full_T1600_pad200": dict(B=1, T=1600, kind="full", fv=[200], seed=0x5EED + 520),
+    # k_norm weights 25x the checkpoint's: logits with a spread of ~70 (log2 units), so later
+    # key blocks pass a row's first-block max by more than 2^64 and the workgroups rerun their
+    # range with the exact online softmax. Logits that large amplify the inputs' bf16
+    # rounding (the reference's own arithmetic is ~2e-2 off), so only the bound relative to
+    # the reference's arithmetic applies.
+    "sliding_1024_large_logits": dict(B=1, T=1024, kind="sliding", fv=[0], wk_mean=3.0,
+                                      seed=0x5EED + 530, relative_only=True),
+    "full_1024_large_logits": dict(B=1, T=1024, kind="full", fv=[0], wk_mean=3.0,
+                                   seed=0x5EED + 540, relative_only=True),
 }
 
 
@@ -91,6 +106,7 @@ def test_gemma_attention(device, name):
     r = O.compare(ref, truth)
     _say(f"  relRMS {c['rel_rms']:.3e} maxAbs {c['max_abs']:.3e} "
          f"(reference arithmetic relRMS {r['rel_rms']:.3e})")
-    assert c["rel_rms"] <= 5e-3, c
-    assert c["max_abs"] <= 2e-2, c
+    if not CASES[name].get("relative_only"):
+        assert c["rel_rms"] <= 5e-3, c
+        assert c["max_abs"] <= 2e-2, c
     assert c["rel_rms"] <= max(r["rel_rms"], 2.5e-3) * 1.25, (c, r)
