@@ -2,7 +2,7 @@
 // :288-321) for gfx950: head dims 256 / 512, 16 query heads over 8 or 1 KV heads, causal +
 // sliding-window + left-padding mask, scale 1.0, 1024 tokens per prompt.
 //
-// Three launches:
+// Four launches:
 //   gemma_prep_kernel   one wave per (batch row, token, head) row of q or k: the per-head
 //                       RMS norm (fp32, pow(mean + eps, -0.5), times the weight), rotate_half
 //                       RoPE with the fp32 tables, q scaled by scale*log2(e). Rounding points:
@@ -23,20 +23,24 @@
 //                       one 32-key block into operand order: per key half hf and 32-channel
 //                       block cb one 1 KB unit, lane r + 32g holding channel 32cb + r at keys
 //                       16hf + 4g + {0..3, 8..11}. Keys past T are zeros in both layouts, and
-//                       every operand of the attention is one coalesced 16-byte load per lane.
-//   gemma_attn_kernel   one workgroup of four waves per (batch row, query head, 32 queries);
-//                       the waves split the head dim into four slices of D/4 channels. Per
-//                       32-key block each wave forms the partial S^T = K.Q'^T over its slice
-//                       (MFMA 32x32x16 over both parts of Q', K' and Q' straight from memory;
-//                       the reference keeps q in fp32 after its fp32 RoPE), the four partials are
-//                       added through LDS in a fixed order (every wave holds the same S), the
-//                       mask and an online softmax (running max, rescale) run in every wave,
-//                       and each wave accumulates O^T += V^T.P^T for its own channels with P
-//                       as two bf16 parts (the reference's weights are fp32); O
-//                       is written in fp32, the dtype the reference's explicit path returns.
-// The key range of a query block is cut to the causal / window / padding bounds; query rows
-// inside the left padding (no allowed key) attend to every key unmasked, the reference's
-// rule for fully-masked rows.
+//                       a key block's k' and v'^T are each one contiguous run of units.
+//   gemma_attn_kernel   a wave owns 32 queries over 256 channels (D = 256: the whole head;
+//                       D = 512: half of it, its partner wave the other half), four waves per
+//                       workgroup: 128 queries at D = 256, 64 at D = 512. The key blocks of
+//                       the workgroup's range are copied HBM -> LDS by the buffer-load-to-LDS
+//                       path into a ring (4 blocks at D = 256, 2 at D = 512) and read from LDS
+//                       by every wave. Per key block: S^T = K.Q'^T over the hi and lo parts of
+//                       q' (inline products with S in VGPRs and Q' in AGPRs; at D = 512 the two
+//                       halves' partial sums are exchanged through LDS and added in a fixed
+//                       order), the mask, exp2 with each row's max fixed at its first block with
+//                       an allowed key, and O^T += V^T.P^T with P as two bf16 parts (the
+//                       reference's weights are fp32). A block whose weights would pass 2^64
+//                       sends the workgroup to an exact pass (online max with rescaling) over
+//                       its range. O is written in fp32, the dtype the reference's explicit
+//                       path returns.
+//   gemma_combine_kernel  the long query blocks' keys run as ranges of at most 16 blocks on
+//                       separate workgroups, each writing unnormalised O and (max, sum); the
+//                       merge rescales and adds them.
 #include <type_traits>
 
 #include "lds_copy.hpp"
