@@ -37,8 +37,8 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_attn_c4.json")
 # The sources the dominant kernel is built from: a traffic figure counted on another version
 # of them is stale and not reported.
 KERNEL_SOURCES = [os.path.join(ROOT, "ltx-2.5-swift_amd", "csrc", f) for f in
-                  ("fmha_dma.hip", "fmha_device.hpp", "lds_copy.hpp", "fmha_params.hpp",
-                   "ltx_attn_abi.cpp")]
+                  ("fmha_dma.hip", "fmha_device.hpp", "lds_copy.hpp", "mfma_s.hpp",
+                   "fmha_params.hpp", "ltx_attn_abi.cpp")]
 
 
 def kernel_source_sha256():
