@@ -615,14 +615,22 @@ def cpu_baseline(x, budget_s):
     dt = timed(nh, nq)
     flops = 4.0 * nq * T * nh * D
     cpu = "unknown"
+    info = {}
     try:
         with open("/proc/cpuinfo") as fh:
             for line in fh:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
+                if not line.strip():
+                    break                              # the first processor's block
+                key, _, val = line.partition(":")
+                info[key.strip()] = val.strip()
     except OSError:
         pass
+    if "model name" in info:
+        cpu = info["model name"]
+        # a virtual machine may report only the vendor's family name: add family/model/stepping
+        if not any(ch.isdigit() for ch in cpu) and "cpu family" in info:
+            cpu += (f" (family {info['cpu family']}, model {info.get('model', '?')}, "
+                    f"stepping {info.get('stepping', '?')})")
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": (f"{nh} head(s) x {nq} queries x {T} keys of the 12480-token workload "
                        f"(norm + 3-D RoPE + explicit fp32 SDPA), {dt:.1f} s on {threads} "
