@@ -104,6 +104,8 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 // prologue's statistic and q_norm.weight (DiTAttention.swift:202-204), rotate (split-half
 // RoPE, :226-237), multiply by scale*log2(e) in fp32, round to bf16 once. Lane (r, g) holds
 // query 32*qb + r, channels 16c + 8g .. +7 in qf[qb][c]. Rows past Lq read as zero.
+// Every load (the rows, the statistic, the weight, the table rows) is issued before any of
+// the arithmetic, so an item start waits for one memory round trip, not one per kind.
 template <int D>
 __device__ __forceinline__ void load_q(const FmhaParams &p, int b, int h, int q0, bool active,
                                        int r, int g, bf16x8 (&qf)[2][D / 16]) {
@@ -112,36 +114,54 @@ __device__ __forceinline__ void load_q(const FmhaParams &p, int b, int h, int q0
     const int nq = max(0, min(QW, p.Lq - q0));   // valid queries of this wave
     const rsrc_t rq = make_rsrc(Qb + (int64_t)(active ? q0 : 0) * p.q_rs,
                                 (int64_t)nq * p.q_rs * 2);
-    float wq[NC][8];
-    if (p.q_rstd) {
+    const bool norm = p.q_rstd != nullptr, rope = p.q_cos != nullptr;
+    u32x4 xr[2][NC], wr[NC], cr[2][NC / 2], sr[2][NC / 2];
+    float rs[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            xr[qb][c] = bload16(rq, (uint32_t)((32 * qb + r) * p.q_rs * 2 + (16 * c + 8 * g) * 2));
+    if (norm) {
         const bf16 *w = (const bf16 *)p.q_w + h * D;
 #pragma unroll
-        for (int c = 0; c < NC; ++c) unpack8(ldg16(w + 16 * c + 8 * g), wq[c]);
+        for (int c = 0; c < NC; ++c) wr[c] = ldg16(w + 16 * c + 8 * g);
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+            rs[qb] = p.q_rstd[(int64_t)b * p.Lq + min(q0 + 32 * qb + r, p.Lq - 1)];
+    }
+    if (rope) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int qc = min(q0 + 32 * qb + r, p.Lq - 1);   // clamped index for side tables
+            const int64_t toff = ((int64_t)h * p.Lq + qc) * (D / 2);
+#pragma unroll
+            for (int c = 0; c < NC / 2; ++c) {
+                cr[qb][c] = ldg16((const bf16 *)p.q_cos + toff + 16 * c + 8 * g);
+                sr[qb][c] = ldg16((const bf16 *)p.q_sin + toff + 16 * c + 8 * g);
+            }
+        }
     }
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-        const int qi = 32 * qb + r;               // query within the wave
-        const int qc = min(q0 + qi, p.Lq - 1);     // clamped index for side tables
         float x[NC][8];
 #pragma unroll
-        for (int c = 0; c < NC; ++c)
-            unpack8(bload16(rq, (uint32_t)(qi * p.q_rs * 2 + (16 * c + 8 * g) * 2)), x[c]);
-        if (p.q_rstd) {
-            const float rs = p.q_rstd[(int64_t)b * p.Lq + qc];
+        for (int c = 0; c < NC; ++c) unpack8(xr[qb][c], x[c]);
+        if (norm) {
 #pragma unroll
-            for (int c = 0; c < NC; ++c)
+            for (int c = 0; c < NC; ++c) {
+                float wq[8];
+                unpack8(wr[c], wq);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) x[c][e] = (x[c][e] * rs) * wq[c][e];
+                for (int e = 0; e < 8; ++e) x[c][e] = (x[c][e] * rs[qb]) * wq[e];
+            }
         }
-        if (p.q_cos) {
-            const int64_t toff = ((int64_t)h * p.Lq + qc) * (D / 2);
-            const bf16 *cs = (const bf16 *)p.q_cos + toff;
-            const bf16 *sn = (const bf16 *)p.q_sin + toff;
+        if (rope) {
 #pragma unroll
             for (int c = 0; c < NC / 2; ++c) {
                 float fc[8], fs[8];
-                unpack8(ldg16(cs + 16 * c + 8 * g), fc);
-                unpack8(ldg16(sn + 16 * c + 8 * g), fs);
+                unpack8(cr[qb][c], fc);
+                unpack8(sr[qb][c], fs);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float x1 = x[c][e], x2 = x[c + NC / 2][e];
