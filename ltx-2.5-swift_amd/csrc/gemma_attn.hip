@@ -2,7 +2,7 @@
 // :288-321) for gfx950: head dims 256 / 512, 16 query heads over 8 or 1 KV heads, causal +
 // sliding-window + left-padding mask, scale 1.0, 1024 tokens per prompt.
 //
-// Four launches:
+// Three launches (the first is the whole prologue, its q/k rows and its v blocks side by side):
 //   gemma_prep_kernel   one wave per (batch row, token, head) row of q or k: the per-head
 //                       RMS norm (fp32, pow(mean + eps, -0.5), times the weight), rotate_half
 //                       RoPE with the fp32 tables, q scaled by scale*log2(e). Rounding points:
@@ -19,7 +19,7 @@
 //                       k' is stored in MFMA operand order: per (batch row, KV head, 32-key
 //                       block) D/16 units of 1 KB, lane r + 32g of unit c holding channels
 //                       16c + 8g .. +7 of key r.
-//   gemma_vt_kernel     v with the weightless per-head norm, transposed through an LDS tile of
+//   (same launch)       v with the weightless per-head norm, transposed through an LDS tile of
 //                       one 32-key block into operand order: per key half hf and 32-channel
 //                       block cb one 1 KB unit, lane r + 32g holding channel 32cb + r at keys
 //                       16hf + 4g + {0..3, 8..11}. Keys past T are zeros in both layouts, and
@@ -50,14 +50,15 @@ namespace ltx {
 namespace {
 
 // ---- prologue ------------------------------------------------------------------------------
+// q/k rows: workgroup wg of the rows' part of the launch.
 template <int D>
-__global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p) {
+__device__ __forceinline__ void gemma_prep_rows(const GemmaPrepParams &p, int wg) {
     // 8 channels per lane: a row of D = 512 takes a wave, a row of D = 256 half a wave
     constexpr int E = 8;
     constexpr int LPR = D / E;                      // lanes per row: 64 or 32
     constexpr int RPW = 64 / LPR;                   // rows per wave
     const int lane = threadIdx.x & (LPR - 1);       // lane within the row
-    const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW +
+    const int64_t row = ((int64_t)wg * 4 + (threadIdx.x >> 6)) * RPW +
                         ((threadIdx.x & 63) / LPR);
     const int heads = p.Hq + p.Hkv;                 // q heads, then k heads, per token
     if (row >= (int64_t)p.B * p.T * heads) return;
@@ -120,17 +121,18 @@ __global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p
 
 // v: the weightless per-head norm, stored transposed in operand order. One workgroup per
 // (batch row, KV head, 32-key block): each wave loads its 8 token rows at once, normalises
-// them into an LDS tile, then the tile leaves as the block's P.V operand units.
+// them into an LDS tile, then the tile leaves as the block's P.V operand units. Workgroup wg
+// of the v part of the launch.
 template <int D>
-__global__ __launch_bounds__(256) void gemma_vt_kernel(const GemmaPrepParams p) {
+__device__ __forceinline__ void gemma_vt_block(const GemmaPrepParams &p, int wg,
+                                               bf16 (&tile)[32][D + 8]) {
     constexpr int E = D / 64;
     constexpr int TT = 32;                          // tokens per workgroup: one key block
     constexpr int RW = TT / 4;                      // rows per wave
-    __shared__ __attribute__((aligned(16))) bf16 tile[TT][D + 8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nkb = (p.T + TT - 1) / TT;
-    const int kb = (int)(blockIdx.x % nkb), t0 = kb * TT;
-    const int bh = (int)(blockIdx.x / nkb);
+    const int kb = wg % nkb, t0 = kb * TT;
+    const int bh = wg / nkb;
     const int h = bh % p.Hkv, b = bh / p.Hkv;
     float x[RW][E];
 #pragma unroll
@@ -186,6 +188,16 @@ __global__ __launch_bounds__(256) void gemma_vt_kernel(const GemmaPrepParams p) 
             if (t0 + (l & 31) >= p.T) *(u32x4 *)(kbase + u * 8) = u32x4{0, 0, 0, 0};
         }
     }
+}
+
+// The prologue as one launch: the q/k rows' workgroups, then the v blocks' (they write
+// disjoint parts of k': rows below T, and the zeroed rows past T of the last block).
+template <int D>
+__global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p, int row_wgs) {
+    __shared__ __attribute__((aligned(16))) bf16 tile[32][D + 8];
+    const int wg = blockIdx.x;
+    if (wg < row_wgs) gemma_prep_rows<D>(p, wg);
+    else gemma_vt_block<D>(p, wg - row_wgs, tile);
 }
 
 // ---- attention -----------------------------------------------------------------------------
@@ -536,16 +548,13 @@ int launch_gemma_prep(const GemmaPrepParams &p, int D, void *stream) {
     // rows per workgroup: four waves of one (D = 512) or two (D = 256) rows
     const int64_t rows = (int64_t)p.B * p.T * (p.Hq + p.Hkv);
     const int64_t rows_wg = D == 512 ? 4 : 8;
-    const dim3 grid((unsigned)((rows + rows_wg - 1) / rows_wg)), block(256);
-    const dim3 vgrid((unsigned)((int64_t)p.B * p.Hkv * ((p.T + 31) / 32)));
+    const int64_t row_wgs = (rows + rows_wg - 1) / rows_wg;
+    const int64_t v_wgs = (int64_t)p.B * p.Hkv * ((p.T + 31) / 32);
+    if (row_wgs + v_wgs > 0x7fffffff) return (int)hipErrorInvalidValue;
+    const dim3 grid((unsigned)(row_wgs + v_wgs)), block(256);
     hipStream_t st = (hipStream_t)stream;
-    if (D == 512) {
-        hipLaunchKernelGGL(gemma_prep_kernel<512>, grid, block, 0, st, p);
-        hipLaunchKernelGGL(gemma_vt_kernel<512>, vgrid, block, 0, st, p);
-    } else {
-        hipLaunchKernelGGL(gemma_prep_kernel<256>, grid, block, 0, st, p);
-        hipLaunchKernelGGL(gemma_vt_kernel<256>, vgrid, block, 0, st, p);
-    }
+    if (D == 512) hipLaunchKernelGGL(gemma_prep_kernel<512>, grid, block, 0, st, p, (int)row_wgs);
+    else hipLaunchKernelGGL(gemma_prep_kernel<256>, grid, block, 0, st, p, (int)row_wgs);
     return (int)hipGetLastError();
 }
 
