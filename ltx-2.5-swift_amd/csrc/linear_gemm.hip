@@ -50,7 +50,7 @@ struct LinTile {
     static constexpr int ELEMS = LT * BK;         // one operand's tile of one k step
     static constexpr int CPT = LT * U / 64 / 4;   // copies per wave per operand tile
     static constexpr int NCH = BK / 16;           // MFMA reduction chunks per k step
-    static_assert(BK == 64, "k step: the copy schedule places 2*CPT = 16 copies in 16 products");
+    static_assert(BK == 64, "k step: the copy schedule places CPT = 8 copies in each of two chunks");
     static_assert(2 * 2 * ELEMS * 2 <= 160 * 1024, "LDS budget");
 };
 
@@ -195,17 +195,18 @@ void linear_kernel(const LinearParams p) {
         }
         // Copy j (0 .. 2*CPT-1) of this wave's share of k step s into buffer st: even j of w, odd
         // of x.
-        auto copy_one = [&](int s, int st, int j) __attribute__((always_inline)) {
-            const int kb = s * BK * 2;
+        auto copy_with = [&](const u32x4 &rw, const u32x4 &rx, int st, int j) __attribute__((always_inline)) {
             if ((j & 1) == 0) {
-                copy_all(rsrc_words(W0 + kb, wbytes),
-                         (uint32_t)(uintptr_t)((lds_bf16 *)sW + st * ELEMS + (wave * CPT + j / 2) * 512),
+                copy_all(rw, (uint32_t)(uintptr_t)((lds_bf16 *)sW + st * ELEMS + (wave * CPT + j / 2) * 512),
                          wl[j / 2]);
             } else {
-                copy_all(rsrc_words(X0 + kb, xbytes),
-                         (uint32_t)(uintptr_t)((lds_bf16 *)sX + st * ELEMS + (wave * CPT + j / 2) * 512),
+                copy_all(rx, (uint32_t)(uintptr_t)((lds_bf16 *)sX + st * ELEMS + (wave * CPT + j / 2) * 512),
                          xl[j / 2]);
             }
+        };
+        auto copy_one = [&](int s, int st, int j) __attribute__((always_inline)) {
+            const int kb = s * BK * 2;
+            copy_with(rsrc_words(W0 + kb, wbytes), rsrc_words(X0 + kb, xbytes), st, j);
         };
         // Operand of rows row0 + 0..31, reduction chunk c: lane (r, g) reads row row0 + r, unit 2c + g.
         auto frag = [&](const lds_bf16 *S, int row0, int c) __attribute__((always_inline)) {
@@ -229,22 +230,37 @@ void linear_kernel(const LinearParams p) {
                 b[buf][i] = frag(Xs, wm * 128 + 32 * i, c);
             }
         };
-        // Prologue: the range's first two steps into both buffers, then the first operands.
+        // Prologue: the range's first step, and the first half of its second (the first step
+        // issues the rest, as every step does for its successor), then the first operands.
 #pragma unroll
         for (int j = 0; j < 2 * CPT; ++j) copy_one(k_begin, 0, j);
         if (k_end - k_begin > 1) {
 #pragma unroll
-            for (int j = 0; j < 2 * CPT; ++j) copy_one(k_begin + 1, 1, j);
-            wait_copies_but<2 * CPT>();
+            for (int j = 0; j < CPT; ++j) copy_one(k_begin + 1, 1, j);
+            wait_copies_but<CPT>();
         } else {
             wait_copies();
         }
         __syncthreads();
         read_chunk(0, 0, 0);
 
-        // One k step; COPY: issue the copies of step s + 2, NEXT: read step s + 1's first operands.
-        auto step = [&](int s, auto copy, auto next) __attribute__((always_inline)) {
+        // One k step; COPY: issue the first half of step s + 2's copies (into the buffer the
+        // step frees), NEXT: read step s + 1's first operands; REST: issue the second half of
+        // step s + 1's copies in the first chunk (half a step's copies per chunk keeps the
+        // address unit's queue from filling).
+        auto step = [&](int s, auto copy, auto next, auto rest) __attribute__((always_inline)) {
             const int st = (s - k_begin) & 1;
+            // the resources of the copies this step issues: step s + 1's second half, step
+            // s + 2's first half
+            u32x4 rw1, rx1, rw2, rx2;
+            if constexpr (decltype(rest)::value) {
+                rw1 = rsrc_words(W0 + (s + 1) * BK * 2, wbytes);
+                rx1 = rsrc_words(X0 + (s + 1) * BK * 2, xbytes);
+            }
+            if constexpr (decltype(copy)::value) {
+                rw2 = rsrc_words(W0 + (s + 2) * BK * 2, wbytes);
+                rx2 = rsrc_words(X0 + (s + 2) * BK * 2, xbytes);
+            }
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
                 const int cb = c & 1;          // NCH is even: chunk 0 of every step is in buffer 0
@@ -265,8 +281,13 @@ void linear_kernel(const LinearParams p) {
 #pragma unroll
                     for (int mb = 0; mb < 4; ++mb) {
                         acc[nb][mb] = mfma32(a[cb][nb], b[cb][mb], acc[nb][mb]);
-                        if (decltype(copy)::value && c == NCH - 1) {
-                            copy_one(s + 2, st, 4 * nb + mb);      // one copy per product
+                        const int pr = 4 * nb + mb;                // product of the chunk
+                        if (decltype(copy)::value && c == NCH - 1 && (pr & 1) == 0) {
+                            copy_with(rw2, rx2, st, pr / 2);       // copies 0 .. CPT-1
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                        if (decltype(rest)::value && c == 0 && (pr & 1) == 0) {
+                            copy_with(rw1, rx1, st ^ 1, CPT + pr / 2);   // CPT .. 2*CPT-1
                             __builtin_amdgcn_sched_barrier(0);
                         }
                     }
@@ -275,9 +296,9 @@ void linear_kernel(const LinearParams p) {
         using yes = std::true_type;
         using no = std::false_type;
         int s = k_begin;
-        for (; s + 2 < k_end; ++s) step(s, yes{}, yes{});
-        if (s + 1 < k_end) step(s++, no{}, yes{});
-        step(s, no{}, no{});
+        for (; s + 2 < k_end; ++s) step(s, yes{}, yes{}, yes{});
+        if (s + 1 < k_end) step(s++, no{}, yes{}, yes{});
+        step(s, no{}, no{}, no{});
 
         if constexpr (decltype(tail)::value) {
             // A tail range: its accumulators, in register order, for the fixup.
