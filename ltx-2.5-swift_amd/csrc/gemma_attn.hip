@@ -322,7 +322,7 @@ void gemma_attn_kernel(const GemmaAttnParams p) {
     f32x16 o[NDW];
     float m, l;
     const f32x16 zero = splat16(0.f);               // the S chains' first SrcC
-    float *xs = (float *)(smem + NS * G::BLOCK);     // [4 waves][64 lanes][16] partial S
+    float *xs = (float *)(smem + NS * G::BLOCK);     // [4 waves][4][64 lanes][4] partial S
     bool overflow = false;                           // some row's weights passed the bound
 
     // One pass over the range's key blocks. SAFE: the exact online softmax (O and l rescaled
@@ -370,18 +370,17 @@ void gemma_attn_kernel(const GemmaAttnParams p) {
             if constexpr (SPLIT > 1) {
                 // the partner wave holds the other half of the channels: exchange the partial
                 // sums and add them in a fixed order, so both waves hold the same S
-                float *mine = xs + (wave * 64 + lane) * 16;
+                // layout [wave][i4][lane][4]: a wave's 16-byte accesses are lane-contiguous,
+                // free of bank conflicts
 #pragma unroll
                 for (int i4 = 0; i4 < 4; ++i4)
-                    *(f32x4 *)(mine + 4 * i4) =
+                    *(f32x4 *)(xs + ((wave * 4 + i4) * 64 + lane) * 4) =
                         f32x4{s[4 * i4], s[4 * i4 + 1], s[4 * i4 + 2], s[4 * i4 + 3]};
                 __syncthreads();
-                const float *lo_ = xs + ((2 * grp) * 64 + lane) * 16;
-                const float *hi_ = xs + ((2 * grp + 1) * 64 + lane) * 16;
 #pragma unroll
                 for (int i4 = 0; i4 < 4; ++i4) {
-                    const f32x4 a0 = *(const f32x4 *)(lo_ + 4 * i4);
-                    const f32x4 a1 = *(const f32x4 *)(hi_ + 4 * i4);
+                    const f32x4 a0 = *(const f32x4 *)(xs + (((2 * grp) * 4 + i4) * 64 + lane) * 4);
+                    const f32x4 a1 = *(const f32x4 *)(xs + (((2 * grp + 1) * 4 + i4) * 64 + lane) * 4);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) s[4 * i4 + e] = a0[e] + a1[e];
                 }
