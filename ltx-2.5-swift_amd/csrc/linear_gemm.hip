@@ -20,10 +20,12 @@
 //   * the barrier certifies that every wave's copies for the next step have landed (each wave
 //     waits for its own first: the copies are untracked assembly, counted by vmcnt) and that
 //     every wave has finished reading the current step's buffer;
-//   * right after it, the wave reads the next step's first operands and issues the copies for
-//     the step after next into the buffer just freed, one after each of the chunk's products,
-//     so the matrix cores have the chunk's products to run while the reads return, and the
-//     copies have a whole step to land.
+//   * right after it, the wave reads the next step's first operands and issues half of the
+//     copies for the step after next into the buffer just freed, one after every other product
+//     of the chunk, so the matrix cores have the chunk's products to run while the reads
+//     return; the other half follows during the next step's first chunk. Half a step's copies
+//     per chunk keeps the texture address unit's queues from filling (all sixteen in one chunk
+//     stalled the wave's issue), and the later half still has 2.5 chunks to land.
 // Within a step, the operands of chunk c + 1 are read while the products of chunk c run.
 //
 // Rounding follows the reference's two operations: the fp32 accumulator is rounded to bf16
