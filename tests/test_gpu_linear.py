@@ -72,6 +72,7 @@ def check_partials(parts, y_bits, label):
 
 @pytest.mark.parametrize("M,N,K,bias", [
     (256, 256, 64, False),      # one tile, one k step
+    (256, 264, 128, True),      # two k steps (the first issues the second's later copies)
     (300, 520, 192, True),      # ragged rows and columns, three k steps
     (1000, 4096, 2048, True),   # audio-width projection rows of a stage-1 video
     (77, 32, 4096, True),       # to_gate_logits: 32 heads
