@@ -142,7 +142,9 @@ typedef struct ltx_attn_args {
 void ltx_attn_args_init(ltx_attn_args *a);
 
 /* Bytes of workspace ltx_attn_fwd needs for these arguments (0 if none). Pure host function;
- * returns 0 and sets the thread's error detail if the arguments are invalid. */
+ * returns 0 and sets the thread's error detail if the arguments are invalid. It plans for a
+ * whole gfx950 part (256 CUs); on a device with another CU count ltx_attn_fwd plans its tail
+ * splits for that count when the given workspace covers that plan, else runs the sized one. */
 size_t ltx_attn_workspace_bytes(const ltx_attn_args *a);
 
 /* Check the arguments without launching anything (the first step of ltx_attn_fwd). */
@@ -222,7 +224,9 @@ int32_t ltx_linear_sumsq_blocks(int32_t N);
  * whole round of 256 (one per CU) are cut along K into as many ranges as fill the CUs, and a
  * fixup launch sums each tile's ranges (256 KiB of fp32 per range; 0 when the tiles fill
  * whole rounds or the tail is more than half a round). Pure host function; 0 for invalid
- * arguments. No counterpart in the reference, whose matmul (MLX) manages its own scratch. */
+ * arguments. Sized for a whole gfx950 part (256 CUs): on a device with another CU count
+ * ltx_linear splits by that count when the workspace covers it, else as sized. No
+ * counterpart in the reference, whose matmul (MLX) manages its own scratch. */
 size_t ltx_linear_workspace_bytes(const ltx_linear_args *a);
 
 /* Run the projection asynchronously on `stream` (a hipStream_t or NULL). The fp32

@@ -10,6 +10,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -34,10 +35,31 @@ bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// Attention workgroups resident at once: one per CU (each holds most of a CU's LDS) of a
-// gfx950 part, 256 CUs. The planner is a pure host function (workspace sizing and validation
-// run without touching the HIP runtime), so the count is a constant, not a device query.
+// Attention and projection workgroups resident at once: one per CU (each holds most of a CU's
+// LDS). Workspace sizing and validation are pure host functions and plan for a whole gfx950
+// part, 256 CUs; a call plans again for its device's CU count (device_groups) and runs that
+// plan when the caller's workspace covers it, else the sized one. Both are correct; only the
+// tail splitting differs.
 constexpr int64_t kConcurrentGroups = 256;
+
+// CU count of the calling thread's current device; kConcurrentGroups if the runtime cannot
+// say (the error of a failed query is cleared so that the launches' checks do not see it).
+// LTX_ATTN_RESIDENT_GROUPS, a positive integer, stands in for the count (tests of the plans of
+// other part sizes).
+int64_t device_groups() {
+    if (const char *e = getenv("LTX_ATTN_RESIDENT_GROUPS")) {
+        const long v = strtol(e, nullptr, 10);
+        if (v > 0 && v <= 65536) return v;
+    }
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0) {
+        (void)hipGetLastError();
+        return kConcurrentGroups;
+    }
+    return cus;
+}
 // Charge per extra split of a tail item, in rounds: its fp32 partial O is written and read
 // back by the combine kernel.
 constexpr double kSplitCharge = 0.02;
@@ -89,7 +111,8 @@ ltx_attn_status check_tensor(const char *name, const void *ptr, int64_t bs, int6
     return LTX_ATTN_OK;
 }
 
-ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
+ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl,
+                          int64_t groups = kConcurrentGroups) {
     g_err[0] = 0;
     if (!a) return fail(LTX_ATTN_EINVAL, "args is NULL");
     if (a->B < 1 || a->H < 1 || a->Lq < 1 || a->Lk < 1)
@@ -213,11 +236,11 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
         pl->k_prologue = k_work;
         pl->kprep_rows = pl->kmax;
         // Eight waves of 32-query blocks per workgroup (two per SIMD); one workgroup per CU:
-        // B*H*G workgroups over 256 CUs, no more groups than a head's query blocks fill.
+        // B*H*G workgroups over the CUs, no more groups than a head's query blocks fill.
         const int waves = 8, qw = 32;
         const int64_t heads = (int64_t)B * H;
         const int64_t nqb = (a->Lq + qw - 1) / qw;
-        int64_t G = (kConcurrentGroups + heads - 1) / heads;
+        int64_t G = (groups + heads - 1) / heads;
         G = std::max<int64_t>(1, std::min(G, (nqb + waves - 1) / waves));
         pl->short_groups = (int)G;
         pl->n_items = pl->n_full = heads * G;
@@ -270,29 +293,29 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl) {
         splits = a->num_splits > 0
                      ? a->num_splits
                      : (int)std::min<int64_t>(ltx::kMaxSplits,
-                                              (kConcurrentGroups + N - 1) / N);
+                                              (groups + N - 1) / N);
         splits = std::max(1, std::min(splits, (pl->ntiles_max + 1) / 2));
         n_full = 0;
     } else if (a->num_splits > 0) {
         splits = a->num_splits;
         n_full = 0;
     } else if (B <= ltx::kMaxBatch) {
-        const int64_t rounds = N / kConcurrentGroups, rem = N - rounds * kConcurrentGroups;
+        const int64_t rounds = N / groups, rem = N - rounds * groups;
         // A last round on at most half the CUs is split; a fuller one is not: with fewer
         // workgroups resident each runs its tiles faster (measured at 3120 tokens: the 160
         // tail items unsplit finish as fast as split three ways, without the combine).
-        if (rem > 0 && 2 * rem <= kConcurrentGroups) {
+        if (rem > 0 && 2 * rem <= groups) {
             double best = 1.0;
             for (int sp = 2; sp <= ltx::kMaxSplits && sp <= pl->ntiles_max; ++sp) {
                 const double c =
-                    (double)((rem * sp + kConcurrentGroups - 1) / kConcurrentGroups) / sp +
+                    (double)((rem * sp + groups - 1) / groups) / sp +
                     kSplitCharge * (sp - 1);
                 if (c < best - 1e-9) {
                     best = c;
                     splits = sp;
                 }
             }
-            if (splits > 1) n_full = rounds * kConcurrentGroups;
+            if (splits > 1) n_full = rounds * groups;
         }
     }
     splits = std::max(1, std::min(splits, pl->ntiles_max));
@@ -453,7 +476,12 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     ltx_attn_status s = ltx_attn_validate(a);
     if (s) return s;
     Plan pl;
-    make_plan(a, &pl);
+    // the device's own plan when the workspace covers it, else the one it was sized for
+    const int64_t groups = device_groups();
+    make_plan(a, &pl, groups);
+    if (groups != kConcurrentGroups && pl.bytes > 0 &&
+        (!a->workspace || pl.bytes > a->workspace_bytes))
+        make_plan(a, &pl);
     char *ws = (char *)a->workspace;
     const int B = a->B, H = a->H, D = a->D;
 
@@ -714,25 +742,26 @@ int32_t ltx_linear_sumsq_blocks(int32_t N) {
 
 namespace {
 
-// Tail split of a projection: the tiles past the last whole round of kConcurrentGroups, when
-// they fill at most half a round, are cut into k ranges of at least two 64-wide steps, as many
-// per tile as keep every CU busy. Pure host arithmetic.
+// Tail split of a projection: the tiles past the last whole round of `groups` resident
+// workgroups, when they fill at most half a round, are cut into k ranges of at least two
+// 64-wide steps, as many per tile as keep every CU busy. Pure host arithmetic.
 struct LinearSplit {
     int64_t tiles = 0, n_full = 0;
     int32_t splits = 1, steps_per_split = 0;
     size_t bytes = 0;
 };
 
-LinearSplit linear_split(int64_t M, int64_t N, int64_t K) {
+LinearSplit linear_split(int64_t M, int64_t N, int64_t K,
+                         int64_t groups = kConcurrentGroups) {
     LinearSplit ls;
     const int64_t T = ((M + ltx::kLinearTile - 1) / ltx::kLinearTile) *
                       ((N + ltx::kLinearTile - 1) / ltx::kLinearTile);
     const int64_t nsteps = K / 64;
     ls.tiles = ls.n_full = T;
     ls.steps_per_split = (int32_t)nsteps;
-    const int64_t rem = T % kConcurrentGroups;
-    if (T == 0 || rem == 0 || 2 * rem > kConcurrentGroups || nsteps < 4) return ls;
-    int64_t s = std::min<int64_t>(kConcurrentGroups / rem, nsteps / 2);
+    const int64_t rem = T % groups;
+    if (T == 0 || rem == 0 || 2 * rem > groups || nsteps < 4) return ls;
+    int64_t s = std::min<int64_t>(groups / rem, nsteps / 2);
     const int64_t per = (nsteps + s - 1) / s;
     s = (nsteps + per - 1) / per;          // no empty range
     if (s < 2) return ls;
@@ -806,7 +835,12 @@ ltx_attn_status ltx_linear(const ltx_linear_args *a, void *stream) {
     p.sumsq = a->sumsq; p.ss_rs = a->sumsq_rs;
     p.M = a->M; p.N = a->N; p.K = a->K;
     p.tiles_m = (int32_t)tiles_m; p.tiles_n = (int32_t)tiles_n;
-    const LinearSplit ls = linear_split(a->M, a->N, a->K);
+    // the device's own tail split when the workspace covers it, else the one it was sized for
+    const int64_t groups = device_groups();
+    LinearSplit ls = linear_split(a->M, a->N, a->K, groups);
+    if (groups != kConcurrentGroups && ls.splits > 1 &&
+        (!a->workspace || a->workspace_bytes < ls.bytes))
+        ls = linear_split(a->M, a->N, a->K);
     p.n_full = (int32_t)ls.tiles;
     p.splits = 1;
     p.steps_per_split = a->K / 64;

@@ -464,15 +464,18 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
     st = lib.ltx_attn_validate(ctypes.byref(a))
     if st not in (OK, EWORKSPACE):
         _check(st)
-    if need:
-        if workspace is None or workspace.numel() * workspace.element_size() < need:
-            workspace = torch.empty(need + 256, dtype=torch.uint8, device=q.device)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need + 256):
+        workspace = torch.empty(need + 256, dtype=torch.uint8, device=q.device)
+    if workspace is not None:
+        # all of it: on a part with another CU count the call may plan for that count when
+        # the workspace covers it
         base = workspace.data_ptr()
-        a.workspace = ctypes.c_void_p((base + 255) // 256 * 256)
-        a.workspace_bytes = need
+        aligned = (base + 255) // 256 * 256
+        a.workspace = ctypes.c_void_p(aligned)
+        a.workspace_bytes = workspace.numel() * workspace.element_size() - (aligned - base)
     _check(lib.ltx_attn_fwd(ctypes.byref(a), ctypes.c_void_p(stream)))
     # keep the workspace alive until the stream has consumed it
-    if need:
+    if workspace is not None:
         out._ltx_workspace = workspace  # noqa: SLF001 -- lifetime anchor
     return out
 

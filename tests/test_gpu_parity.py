@@ -531,6 +531,30 @@ def test_whole_and_tail_items_ragged(device, kprep):
                 {"k_valid_len": valid}, "whole+tail", kprep=kprep)
 
 
+@pytest.mark.parametrize("H,T,groups", [(12, 1300, 32), (12, 1300, 100), (12, 1300, 200),
+                                         (16, 2400, 150)])
+def test_plans_for_other_part_sizes(device, H, T, groups, monkeypatch):
+    """A call plans its tail splits for the device's CU count (LTX_ATTN_RESIDENT_GROUPS stands
+    in for it) when the workspace covers that plan, and runs the plan the workspace was sized
+    for (256 CUs) otherwise. 12 heads x 6 query blocks = 72 items: 32 groups split the 8 tail
+    items four ways, 100 run all 72 whole, 200 split every item two ways (the sized plan: three
+    ways; both fit its workspace). 16 heads x 10 query blocks = 160 items: 150 groups split the
+    10 tail items, which the sized plan (no split, no workspace) cannot hold, so that call runs
+    the sized plan; with a large workspace it runs its own. Every head and row against the C
+    oracle."""
+    import torch
+
+    monkeypatch.setenv("LTX_ATTN_RESIDENT_GROUPS", str(groups))
+    tq, qb = _gpu_bits((1, T, H * 128), 0x5EED + 70, device)
+    tk, kb = _gpu_bits((1, T, H * 128), 0x5EED + 71, device)
+    tv, vb = _gpu_bits((1, T, H * 128), 0x5EED + 72, device)
+    _say(f"{H} heads x {T} tokens, plan for {groups} resident groups, sized workspace")
+    _full_check(device, tq, tk, tv, H, (qb, kb, vb), {}, {}, f"groups {groups} sized")
+    _say(f"{H} heads x {T} tokens, plan for {groups} resident groups, large workspace")
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=device)
+    _full_check(device, tq, tk, tv, H, (qb, kb, vb), {}, {"workspace": ws}, f"groups {groups} own")
+
+
 @pytest.mark.parametrize("direction", ["video_q", "audio_q"])
 def test_c3_cross_modal(device, direction):
     _say(f"c3 cross-modal {direction}")
