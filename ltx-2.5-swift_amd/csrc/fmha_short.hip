@@ -5,11 +5,12 @@
 //
 // These calls move far more bytes than they compute (Q in and O out per query, a few KB of
 // K/V per head): HBM bounds them, and what matters is keeping loads in flight. A workgroup of
-// eight waves owns one (batch, head) and 1/G of its query blocks. It copies the head's K and V
-// into LDS once (LDS DMA, the tile layout of fmha_dma.hip: K rows swizzled for 16-byte
-// operand reads, V rows for transposing reads), then each wave walks its own query blocks
-// with no further barrier, loading the next block's Q, statistic and RoPE table rows into
-// registers while it computes the current one, two waves per SIMD. Per block: S^T = K.Q'^T
+// eight waves (twelve at D = 64) owns one (batch, head) and 1/G of its query blocks. It copies
+// the head's K and V into LDS once (LDS DMA, the tile layout of fmha_dma.hip: K rows swizzled
+// for 16-byte operand reads, V rows for transposing reads), then each wave walks its own
+// query blocks with no further barrier. At D = 128 a wave loads the next block's Q, statistic
+// and RoPE table rows into registers while it computes the current one, two waves per SIMD;
+// at D = 64 three waves per SIMD overlap one another's loads instead. Per block: S^T = K.Q'^T
 // on the matrix cores (Q' normalised, rotated and scaled by scale*log2(e) in fp32, rounded
 // once), the first 32-key block sets the row max, p = exp2(s - m) rounded to bf16 with row
 // sums of those bf16 weights, O^T += V^T.P^T, then O * gate / l is staged in the wave's LDS
@@ -19,17 +20,24 @@
 namespace ltx {
 namespace {
 
-// Eight waves of 32-query blocks per workgroup, two waves per SIMD, so that one wave's
-// arithmetic overlaps the other's loads (four waves of 64-query blocks, one per SIMD, reached
-// 2.9-3.6 TB/s on the block set's calls against 3.8-5.0 TB/s with this shape). The per-group
-// arrays below are indexed by the 32-query group of the wave block (QB of them).
+// Waves of 32-query blocks, several per SIMD, so that one wave's arithmetic overlaps the
+// others' loads (four waves of 64-query blocks, one per SIMD, reached 2.9-3.6 TB/s on the
+// block set's calls against 3.8-5.0 TB/s with two waves of 32). At D = 128 a workgroup holds
+// eight waves, each prefetching its next block into registers; at D = 64 it holds twelve,
+// three per SIMD, which load their blocks when they reach them (the prefetch registers do not
+// fit three waves; this shape took the 3120x126 video-over-audio call from 20 to 16 us). The
+// per-group arrays below are indexed by the 32-query group of the wave block (QB of them).
+constexpr int short_waves(int D) { return D == 64 ? 12 : 8; }
+
 template <int D, bool ROPE>
-__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
+__global__ __attribute__((amdgpu_flat_work_group_size(short_waves(D) * 64, short_waves(D) * 64),
+                          amdgpu_waves_per_eu(short_waves(D) / 4, short_waves(D) / 4)))
 void fmha_short_kernel(const FmhaParams p) {
     constexpr int NC = D / 16, NDB = D / 32, KU = D / 8;
     constexpr int QB = 1;                             // 32-query groups per wave block
     constexpr int SQW = 32 * QB;                      // queries per wave block
-    constexpr int SNW = 8;                            // waves per workgroup
+    constexpr int SNW = short_waves(D);               // waves per workgroup
+    constexpr bool PREFETCH = SNW == 8;               // next block's loads during this one
     constexpr int TE = KT * D;                        // elements of a 64-key tile
     constexpr int TILES = short_max_keys(D) / KT;     // resident tiles
     constexpr int CPT = TE / 512;                     // 1 KB copies per tile
@@ -169,11 +177,12 @@ void fmha_short_kernel(const FmhaParams p) {
     bf16 *Ob = (bf16 *)p.o + (int64_t)b * p.o_bs + (int64_t)h * p.o_hs;
     int j = gi * SNW + wave;
     Raw cur;
-    if (j < nqb) fetch(j, cur);
+    if (PREFETCH && j < nqb) fetch(j, cur);
     for (; j < nqb; j += stride) {
         bf16x8 qf[QB][NC];
+        if (!PREFETCH) fetch(j, cur);
         convert(cur, qf);
-        if (j + stride < nqb) fetch(j + stride, cur);  // in flight while this block computes
+        if (PREFETCH && j + stride < nqb) fetch(j + stride, cur);  // in flight during this block
 
         f32x16 o[NDB][QB];
         float l[QB];
@@ -321,7 +330,7 @@ void fmha_short_kernel(const FmhaParams p) {
 }  // namespace
 
 int launch_fmha_short(const FmhaParams &p, int D, void *stream) {
-    const dim3 grid(p.grid), block(512);
+    const dim3 grid(p.grid), block(short_waves(D) * 64);
     hipStream_t st = (hipStream_t)stream;
     const bool rope = p.q_cos != nullptr;
     // D = 128 with RoPE does not fit the register file with a block in flight; the host plan

@@ -235,9 +235,9 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl,
         pl->shortk = true;
         pl->k_prologue = k_work;
         pl->kprep_rows = pl->kmax;
-        // Eight waves of 32-query blocks per workgroup (two per SIMD); one workgroup per CU:
-        // B*H*G workgroups over the CUs, no more groups than a head's query blocks fill.
-        const int waves = 8, qw = 32;
+        // Eight waves of 32-query blocks per workgroup (twelve at D = 64); one workgroup per
+        // CU: B*H*G workgroups over the CUs, no more groups than a head's query blocks fill.
+        const int waves = D == 64 ? 12 : 8, qw = 32;
         const int64_t heads = (int64_t)B * H;
         const int64_t nqb = (a->Lq + qw - 1) / qw;
         int64_t G = (groups + heads - 1) / heads;
