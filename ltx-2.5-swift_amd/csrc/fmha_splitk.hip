@@ -9,12 +9,12 @@
 // copied HBM -> LDS by the buffer-load-to-LDS path three tiles ahead: the raw K rows (their
 // 16-byte units XOR-swizzled as the MFMA operand reads expect), V row-major, and, when K is
 // normalised or rotated, the statistic of the tile's keys and their cos/sin table rows. After
-// a tile lands, waves 4-7 normalise and rotate its K in place in LDS (x * rstd * w, then the
-// split-half rotation, one bf16 rounding -- the arithmetic of the K prologue) while every
-// wave with queries computes on the tile before it: S^T = K.Q'^T, the softmax with each row's
-// max taken from its first block and -max as the S accumulators' start (an exact online
-// softmax redoes the range when a row sum overflows), and O^T += V^T.P^T. One
-// barrier per tile separates the phases. The range's partial O, max and row sum go to the
+// a tile lands, waves 4-7 (waves 6-7 when three query groups keep waves 4-5 busy) normalise
+// and rotate its K in place in LDS (x * rstd * w, then the split-half rotation, one bf16
+// rounding -- the arithmetic of the K prologue) while every wave with queries computes on
+// the tile before it: S^T = K.Q'^T, the softmax with each row's max taken from its first
+// block and -max as the S accumulators' start (an exact online softmax redoes the range when
+// a row sum overflows), and O^T += V^T.P^T. One barrier per tile separates the phases. The range's partial O, max and row sum go to the
 // split-KV workspace the combine kernel merges; a call with a single range writes O directly.
 #include <type_traits>
 
@@ -123,11 +123,14 @@ void fmha_splitk_kernel(const FmhaParams p) {
         else wait_copies();
     };
 
-    // ---- the in-place K transform: waves 4-7, thread (row, part) of the tile -------------
-    // Each of the 4 threads of a row takes one unit of the first half and the unit of the
-    // second half it is rotated with.
-    const int trow = (tid & 255) >> 2, tpart = tid & 3;
-    const bool tthread = tid >= 256;
+    // ---- the in-place K transform: waves 4-7, or waves 6-7 when three query groups are
+    // active (waves 4 and 5 then compute). A unit (row, part) of the tile is one 16-byte unit
+    // of the row's first half and the unit of the second half it is rotated with; 4 units
+    // per row, 256 per tile, dealt to the transform threads in turn.
+    const int tw0 = (p.Lq + QW - 1) / QW == 3 ? 6 : 4;
+    const bool tthread = wave >= tw0;
+    const int tfirst = tid - 64 * tw0, tstride = 64 * (kSplitWaves - tw0);
+    const int tpart = tid & 3;                       // the same for every unit of a thread
     float wlo[8], whi[8];                            // k norm weights of the thread's channels
     if constexpr (NORM) {
         const bf16 *w = (const bf16 *)p.k_w + h * D;
@@ -136,6 +139,8 @@ void fmha_splitk_kernel(const FmhaParams p) {
     }
     typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
     auto transform = [&](int st) __attribute__((always_inline)) {
+      for (int u = tfirst; u < KT * 4; u += tstride) {
+        const int trow = u >> 2;
         float rs = 1.f;
         if constexpr (NORM)
             rs = ((__attribute__((address_space(3))) float *)lds(st, T::OFF_R + wave * T::RSTD))[trow];
@@ -165,6 +170,7 @@ void fmha_splitk_kernel(const FmhaParams p) {
         }
         *pl = pack8(x1);
         *ph = pack8(x2);
+      }
     };
 
     // ---- operands ------------------------------------------------------------------------

@@ -576,6 +576,31 @@ def test_c3_cross_modal(device, direction):
     _full_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, f"c3 {direction}")
 
 
+@pytest.mark.parametrize("Lq", [40, 126, 152, 230])
+def test_split_key_kernel_query_groups(device, Lq):
+    """The split-key kernel (one query block over a long key stream, D 64, K's norm and RoPE
+    applied in LDS) with 1, 2, 3 and 4 active 64-query groups: the K transform runs on the
+    waves without queries (waves 4-7, or 6-7 with three groups) or beside the products (four
+    groups). B = 2 with a ragged key length in each row."""
+    H, D, Lk = 4, 64, 2500
+    seed = 0x5EED + 700 + Lq
+    _say(f"split-key kernel Lq={Lq} Lk={Lk} H={H}")
+    qt = _index_rotary(np.arange(Lq), H * D, H)
+    kt = _index_rotary(np.arange(Lk) // 7, H * D, H)
+    tq, qb = _gpu_bits((2, Lq, H * D), seed, device)
+    tk, kb = _gpu_bits((2, Lk, H * D), seed + 1, device)
+    tv, vb = _gpu_bits((2, Lk, H * D), seed + 2, device)
+    wq, wqb = _gpu_bits((H * D,), seed + 3, device, 1.0, 0.02)
+    wk, wkb = _gpu_bits((H * D,), seed + 4, device, 1.0, 0.02)
+    valid = [Lk - 37, 1601]
+    kw_host = dict(q_norm_w=wqb, k_norm_w=wkb, q_cos=qt[0], q_sin=qt[1], k_cos=kt[0],
+                   k_sin=kt[1], valid_len=valid)
+    kw_dev = dict(q_norm_w=wq, k_norm_w=wk, k_valid_len=valid,
+                  rotary=L.Rotary(dev(qt[0], device), dev(qt[1], device)),
+                  key_rotary=L.Rotary(dev(kt[0], device), dev(kt[1], device)))
+    _full_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, f"split-key Lq={Lq}")
+
+
 @pytest.mark.parametrize("kprep", [L.KPREP_PROLOGUE, L.KPREP_FUSED])
 def test_c4_stage2_self_12480_norm_rope(device, kprep):
     _say(f"c4 12480 self-attention, norm + 3-D RoPE, kprep={kprep}")
