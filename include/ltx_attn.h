@@ -144,7 +144,9 @@ void ltx_attn_args_init(ltx_attn_args *a);
 /* Bytes of workspace ltx_attn_fwd needs for these arguments (0 if none). Pure host function;
  * returns 0 and sets the thread's error detail if the arguments are invalid. It plans for a
  * whole gfx950 part (256 CUs); on a device with another CU count ltx_attn_fwd plans its tail
- * splits for that count when the given workspace covers that plan, else runs the sized one. */
+ * splits for that count when the given workspace covers that plan, else runs the sized one.
+ * The environment variable LTX_ATTN_RESIDENT_GROUPS (an integer 1..65536), when set, stands in
+ * for the device's CU count in that choice (ltx_linear's too). */
 size_t ltx_attn_workspace_bytes(const ltx_attn_args *a);
 
 /* Check the arguments without launching anything (the first step of ltx_attn_fwd). */
