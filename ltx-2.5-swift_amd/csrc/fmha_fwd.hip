@@ -102,12 +102,13 @@ void fmha_fwd_kernel(const FmhaParams p) {
     u32x4 kcs[KFUSED ? T::KFP : 1], ksn[KFUSED ? T::KFP : 1];
     float krs[KFUSED ? T::KFP : 1];
     u32x4 vreg[4];
-    float kw1[8], kw2[8];
+    // k_norm weights of the thread's two channel units, kept as bf16 (unpacked where used)
+    u32x4 kw1p = {0u, 0u, 0u, 0u}, kw2p = {0u, 0u, 0u, 0u};
     if (KFUSED && p.k_rstd) {
         const int c = tid % T::KPPR;
         const bf16 *w = (const bf16 *)p.k_w + h * D;
-        unpack8(ldg16(w + 8 * c), kw1);
-        unpack8(ldg16(w + D / 2 + 8 * c), kw2);
+        kw1p = ldg16(w + 8 * c);
+        kw2p = ldg16(w + D / 2 + 8 * c);
     }
     const bool vthr = tid < T::VUNITS;
     const int vkg = tid & 15;
@@ -165,6 +166,11 @@ void fmha_fwd_kernel(const FmhaParams p) {
                 unpack8(kreg[2 * i], x1);
                 unpack8(kreg[2 * i + 1], x2);
                 if (p.k_rstd) {
+                    u32x4 w1 = kw1p, w2 = kw2p;
+                    asm volatile("" : "+v"(w1), "+v"(w2));   // unpacked here, not held as fp32
+                    float kw1[8], kw2[8];
+                    unpack8(w1, kw1);
+                    unpack8(w2, kw2);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         x1[e] = (x1[e] * krs[i]) * kw1[e];
