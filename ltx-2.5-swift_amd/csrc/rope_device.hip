@@ -6,10 +6,13 @@
 // instead of on the host and uploaded.
 //
 // Arithmetic matches the host builder step for step: the frequency grid in double then float,
-// the patch centre, fraction and angle in float, one bf16 rounding at the end. cos and sin of
-// the float angle are evaluated in double and rounded to float: the correctly rounded float
-// value, which gives the host builder's bf16 bits (checked over every angle of the model's
-// tables on the host, and against the host builder on the GPU by the tests).
+// the patch centre, fraction and angle in float, one bf16 rounding at the end. The host builder
+// takes cos and sin of the float angle in double and rounds them to float; here the device
+// library's single-precision sincosf (within 4 ulp, the OpenCL bound its library meets) gives
+// the same bf16 bits whenever its result lies more than kGuard ulp from a bf16 rounding
+// midpoint: the double-rounded value is within 4.5 ulp of it, so no midpoint separates them.
+// Closer to a midpoint (about 1 value in 2000) the angle is evaluated in double as on the
+// host. The tests compare every table of the model's geometries with the host builder.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -36,6 +39,14 @@ __device__ __forceinline__ uint16_t bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// A float whose bf16 rounding could differ from that of a value within kGuard ulp of it: its
+// low 16 bits are within kGuard of the midpoint 0x8000 between two bf16 neighbours.
+constexpr int kGuard = 16;
+__device__ __forceinline__ bool near_bf16_midpoint(float x) {
+    const int low = (int)(__float_as_uint(x) & 0xffffu);
+    return abs(low - 0x8000) <= kGuard;
+}
+
 __global__ __launch_bounds__(256) void rope_table_kernel(const RopeParams p) {
     const int nj = (p.half + 255) / 256;
     const int t0 = (blockIdx.x / nj) * kTok;
@@ -59,10 +70,13 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const RopeParams p) {
             const float frac = middle / p.max_pos[d];
             const float scaled = frac * 2.0f - 1.0f;
             const float angle = f * scaled;
-            double sd, cd;
-            sincos((double)angle, &sd, &cd);
-            c = (float)cd;
-            s = (float)sd;
+            sincosf(angle, &s, &c);
+            if (near_bf16_midpoint(s) || near_bf16_midpoint(c)) {
+                double sd, cd;
+                sincos((double)angle, &sd, &cd);
+                c = (float)cd;
+                s = (float)sd;
+            }
         }
         const int64_t o = ((int64_t)hh * p.tokens + t) * p.per_head + k;
         p.cos[o] = bf16_rne(c);
