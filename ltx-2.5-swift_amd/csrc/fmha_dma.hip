@@ -3,8 +3,8 @@
 // needs no preparation) -- every call with two or more query blocks per (batch, head).
 //
 // Same arithmetic as fmha_fwd.hip's register-staged kernel (MFMA mapping, exp2 softmax with
-// the -m accumulator start, 2^64 overflow bound and safe pass, bf16 row sums); what changes
-// is the staging:
+// the -m accumulator start, 2^64 overflow bound and safe pass, row sums of the bf16 weights);
+// what changes is the staging, and the row sums run on the matrix cores:
 //   * Each wave copies its share of the next K and V tiles straight from the caller's
 //     tensors into LDS, row-major; no staging registers, no LDS stores, no prologue for V.
 //     The 16-byte units of each LDS row are XOR-swizzled (swz for K, vswz for V) so the
@@ -22,6 +22,9 @@
 //     waits for them itself (vmcnt) at the next window, and a barrier makes everyone's
 //     visible. The two parities of the steady state are unrolled so every buffer is a
 //     compile-time LDS object.
+//   * The row sums of P are 16x16x32 products of a 0/1 selector with P's operand registers,
+//     issued among the P.V products, instead of 32 VALU adds per 32-key step (the VALU is
+//     what the step waits on; 3% faster at 12480 tokens, 4% at 3120).
 #include <type_traits>
 
 #include "lds_copy.hpp"
@@ -145,7 +148,7 @@ void fmha_dma_kernel(const FmhaParams p) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db) o[db][0] = o[db][1] = splat16(0.f);
     float m[2] = {0.f, 0.f};   // running max (log2 units), identical in lanes l and l^32
-    float l[2] = {0.f, 0.f};   // this lane's share of the row sum
+    float l[2] = {0.f, 0.f};   // safe pass: this lane's share of the row sum
     f32x16 negm[2] = {splat16(0.f), splat16(0.f)};
 
     // Software pipeline over 32-key blocks (block s = keys [32s, 32s+32) of tile s/2):
@@ -203,7 +206,22 @@ void fmha_dma_kernel(const FmhaParams p) {
             }
     };
 
-    bool overflow = false;    // wave-uniform: some block's row sum passed the bound
+    bool overflow = false;    // wave-uniform: some row sum passed the bound
+    // Row sums on the matrix cores: a 16x16x32 product of a 0/1 selector with P's operand
+    // registers. Read as a 16x16x32 B operand, lane L of P(qb, hf) holds 8 weights of query
+    // (L & 15) + 16 * ((L >> 4) & 1); the selector's row m takes the lanes of query
+    // (L & 15) + 16 * (m >= 8), so rows 0-7 of the result hold the sums of queries 0-15 and
+    // rows 8-15 those of queries 16-31 of the group.
+    f32x4 lsum[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    bf16x8 rsel;
+    {
+        const uint32_t one2 = (((lane >> 4) & 1) == ((lane & 15) >= 8 ? 1 : 0)) ? 0x3f803f80u : 0u;
+        rsel = __builtin_bit_cast(bf16x8, u32x4{one2, one2, one2, one2});
+    }
+    auto rowsum_mfma = [&](int k) __attribute__((always_inline)) {
+        const int qb = k & 1, hf = k >> 1;
+        lsum[qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rsel, pp[qb][hf], lsum[qb], 0, 0, 0);
+    };
 
     // Steady-state step: the 2*(NC + 2*NDB) products are issued one at a time with a slice of
     // the softmax of S(s) after every other one, and each LDS operand is read three operands
@@ -218,7 +236,6 @@ void fmha_dma_kernel(const FmhaParams p) {
             const int j = i - NC;
             return v_opnd(Vp, 2 * kbp + j / NDB, j % NDB);
         };
-        float ts[2][2] = {{0.f, 0.f}, {0.f, 0.f}};   // [qb][even/odd key of a pair]
         u32x4 w[2][2];
         f32x16 sn[2];
         bf16x8 a[NOP];
@@ -226,18 +243,14 @@ void fmha_dma_kernel(const FmhaParams p) {
         a[1] = opnd(1);
         a[2] = opnd(2);
         // Softmax of S(s) as a two-stage pipeline over pairs of weights: slice k takes the
-        // exps of its pairs and packs the previous slice's to bf16, adding them in fp32 to the
-        // row sums, so no instruction waits for an exp just issued. (Summing the fp32 weights
-        // costs half the instructions of summing their bf16 roundings; the two sums differ by
-        // the unbiased rounding of the weights, far below the output's bf16 rounding.)
+        // exps of its pairs and packs the previous slice's to bf16, so no instruction waits
+        // for an exp just issued. The row sums of P(s-1) are four products among the P.V ones.
         float ex[NPAIR][2];
         int pe = 0, pc = 0;
         auto stage_c = [&](int n) __attribute__((always_inline)) {
             for (int k = 0; k < n && pc < pe; ++k, ++pc) {
                 const int qb = pc >> 3, hf = (pc >> 2) & 1, e = pc & 3;
                 w[qb][hf][e] = pack_bf2(ex[pc][0], ex[pc][1]);
-                ts[qb][0] += ex[pc][0];
-                ts[qb][1] += ex[pc][1];
             }
         };
         auto slice = [&](int n) __attribute__((always_inline)) {
@@ -261,16 +274,17 @@ void fmha_dma_kernel(const FmhaParams p) {
                     o[j % NDB][qb] = mfma32(a[i], pp[qb][j / NDB], o[j % NDB][qb]);
                 }
                 if (qb == 0) hook(i);
+                if (qb == 1 && i >= NC) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (i - NC == (2 * k + 1) * 2 * NDB / 8) rowsum_mfma(k);
+                }
                 if (qb == 1 || 2 * NOP <= NPAIR) slice(PER);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
         stage_c(NPAIR);
         s_defined(sn[0], sn[1], negm[0], negm[1]);   // 16 products and the slices after S's last
-        const float ts0 = ts[0][0] + ts[0][1], ts1 = ts[1][0] + ts[1][1];
-        overflow |= !(ts0 <= kRebaseBound) || !(ts1 <= kRebaseBound);
-        l[0] += ts0;
-        l[1] += ts1;
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
             sc[qb] = sn[qb];
@@ -308,14 +322,15 @@ void fmha_dma_kernel(const FmhaParams p) {
         }
         f32x16 sn[2];
         if (do_s) qk_block(Kc, (s + 1) & 1, sn);
-        if (do_pv) pv_block(Vp, (s - 1) & 1);
+        if (do_pv) {
+            pv_block(Vp, (s - 1) & 1);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) rowsum_mfma(k);
+        }
         bf16x8 pn[2][2];
         if (do_sm) {
             float ts[2];
             softmax_block(sc, pn, ts);
-            overflow |= !(ts[0] <= kRebaseBound) || !(ts[1] <= kRebaseBound);
-            l[0] += ts[0];
-            l[1] += ts[1];
         }
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
@@ -441,6 +456,15 @@ void fmha_dma_kernel(const FmhaParams p) {
     }
     for (; w < nwin; ++w) window(no{}, w & 1, w, no{});
     wait_copies();
+    // Row sums of this lane's queries (lane (r, g): query r of each group), out of the lanes of
+    // the accumulator that hold them. A sum past 2^64 (some weight outgrew the first block's
+    // max by that much) sends the item to the safe pass.
+    float lt[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        lt[qb] = __shfl(lsum[qb][0], (r & 15) + 32 * (r >> 4), 64);
+        overflow |= !(lt[qb] <= kRebaseBound);
+    }
 
     // ---- safe pass: only when some wave's running max was outgrown -------------------
     // Tile by tile, each 32-key block rebasing O and l as soon as its weights would exceed
@@ -490,13 +514,12 @@ void fmha_dma_kernel(const FmhaParams p) {
                 pv_block((lds_bf16 *)sV0, kb);
             }
         }
+        lt[0] = l[0] + xlane32(l[0]);
+        lt[1] = l[1] + xlane32(l[1]);
     }
     __syncthreads();
 
     // ---- epilogue ---------------------------------------------------------------------
-    float lt[2];
-    lt[0] = l[0] + xlane32(l[0]);
-    lt[1] = l[1] + xlane32(l[1]);
 
     if (wi.tail >= 0) {
         // Tail split: fp32 partial O (unnormalised), running max and row sum, for the
