@@ -51,6 +51,18 @@ void fmha_short_kernel(const FmhaParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane & 31;
     const int g = lane >> 5;
+    // At D = 64 the row sums of P run on the matrix cores: read as a 16x16x32 B operand, lane
+    // L of P holds 8 weights of query (L & 15) + 16 * ((L >> 4) & 1); row m of this 0/1
+    // selector takes the lanes of query (L & 15) + 16 * (m >= 8), so rows 0-7 of the 16x16
+    // sums hold queries 0-15 of the block and rows 8-15 queries 16-31 (5-8% faster there; at
+    // D = 128, whose eight waves already fill the register file, the VALU adds stay: 1-3%
+    // faster than the products).
+    constexpr bool MSUM = D == 64;
+    bf16x8 rsel;
+    {
+        const uint32_t one2 = (((lane >> 4) & 1) == ((lane & 15) >= 8 ? 1 : 0)) ? 0x3f803f80u : 0u;
+        rsel = __builtin_bit_cast(bf16x8, u32x4{one2, one2, one2, one2});
+    }
     const int G = p.short_groups;
     const int bh = blockIdx.x / G, gi = blockIdx.x - bh * G;
     const int h = bh % p.H, b = bh / p.H;
@@ -187,12 +199,14 @@ void fmha_short_kernel(const FmhaParams p) {
         f32x16 o[NDB][QB];
         float l[QB];
         f32x16 negm[QB];
+        f32x4 lsum[QB];              // MSUM: the row sums' accumulators
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
             for (int db = 0; db < NDB; ++db) o[db][qb] = splat16(0.f);
             l[qb] = 0.f;
             negm[qb] = splat16(0.f);
+            lsum[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
         bool over = false;
         // S of key block kb, accumulated from C = init; keys past the valid ones -> -inf.
@@ -227,16 +241,26 @@ void fmha_short_kernel(const FmhaParams p) {
                     u32x4 w;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        w[e] = pack_bf2_opaque(__builtin_amdgcn_exp2f(s[qb][8 * hf + 2 * e]),
-                                               __builtin_amdgcn_exp2f(s[qb][8 * hf + 2 * e + 1]));
-                        ts[qb] = add_bf2(ts[qb], w[e]);
+                        const float x0 = __builtin_amdgcn_exp2f(s[qb][8 * hf + 2 * e]);
+                        const float x1 = __builtin_amdgcn_exp2f(s[qb][8 * hf + 2 * e + 1]);
+                        if constexpr (MSUM) {
+                            w[e] = pack_bf2(x0, x1);
+                        } else {
+                            w[e] = pack_bf2_opaque(x0, x1);
+                            ts[qb] = add_bf2(ts[qb], w[e]);
+                        }
                     }
                     pn[qb][hf] = __builtin_bit_cast(bf16x8, w);
+                    if constexpr (MSUM)
+                        lsum[qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rsel, pn[qb][hf],
+                                                                           lsum[qb], 0, 0, 0);
                 }
+            if constexpr (!MSUM) {
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb) {
-                over |= !(ts[qb] <= kRebaseBound);
-                l[qb] += ts[qb];
+                for (int qb = 0; qb < QB; ++qb) {
+                    over |= !(ts[qb] <= kRebaseBound);
+                    l[qb] += ts[qb];
+                }
             }
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf)
@@ -272,6 +296,7 @@ void fmha_short_kernel(const FmhaParams p) {
 #pragma unroll
                     for (int db = 0; db < NDB; ++db) o[db][qb] = splat16(0.f);
                     l[qb] = 0.f;
+                    lsum[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
                 }
                 over = false;
             }
@@ -290,6 +315,17 @@ void fmha_short_kernel(const FmhaParams p) {
                     }
                 }
                 p_block(s, kb);
+            }
+            if constexpr (MSUM) {
+                // lane (r, g) takes query r's sum from the accumulator lane that holds it, in
+                // the g = 0 lane so that l + xlane32(l) is the sum; a sum past 2^64 sends the
+                // block to pass 1
+#pragma unroll
+                for (int qb = 0; qb < QB; ++qb) {
+                    const float full = __shfl(lsum[qb][0], (r & 15) + 32 * (r >> 4), 64);
+                    over |= !(full <= kRebaseBound);
+                    l[qb] = g == 0 ? full : 0.f;
+                }
             }
             if (__builtin_amdgcn_ballot_w64(over) == 0) break;
         }
