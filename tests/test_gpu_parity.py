@@ -309,6 +309,29 @@ def test_rebase_path_large_logits(device):
     check(got, truth, None, "rebase split")
 
 
+@pytest.mark.parametrize("D,groups", [(64, None), (128, None), (128, "6")])
+def test_dma_kernel_large_logits(device, D, groups, monkeypatch):
+    """The LDS-DMA kernel (three query blocks per head) on logits growing along the keys, far
+    past the first block's max: its row sums (matrix-core products) pass 2^64, so the fast pass
+    is discarded and the items redo their keys with the exact online softmax. With the
+    device's CU count the six items run as split key ranges (and the combine); with six
+    resident groups they run whole. scale = ln 2 folds to exactly 1, so the logits are exact."""
+    if groups:
+        monkeypatch.setenv("LTX_ATTN_RESIDENT_GROUPS", groups)
+    B, H, Lq, Lk = 1, 2, 600, 1200
+    _say(f"LDS-DMA kernel, large logits: D={D} groups={groups}")
+    rng = np.random.default_rng(11 + D)
+    qf = rng.standard_normal((B, Lq, H * D)).astype(np.float32) * 2.0
+    kf = rng.standard_normal((B, Lk, H * D)).astype(np.float32)
+    kf *= (1.0 + np.arange(Lk, dtype=np.float32) / 40.0)[None, :, None]
+    q, k = O.f32_to_bf16_bits(qf), O.f32_to_bf16_bits(kf)
+    v = O.randn_bf16_bits((B, Lk, H * D), 12)
+    scale = float(np.float32(math.log(2.0)))
+    truth = O.attention(q, k, v, H, scale=scale, mode="exact")
+    got = run(device, q, k, v, H, scale=scale)
+    check(got, truth, None, f"LDS-DMA large logits D={D} groups={groups}")
+
+
 @pytest.mark.parametrize("B,H,Lq,Lk,D,valid,rope", [
     (2, 4, 1000, 1024, 128, [128, 1], False),   # most keys kept at D=128; a single key
     (2, 4, 1000, 300, 64, [256, 129], True),    # most keys kept at D=64, norm + RoPE
