@@ -316,22 +316,73 @@ def bench_short_keys(device, steps, warmup, hip, block=True):
     # 1024 text keys (norm on both sides) and video queries over the 152 audio keys (norm +
     # temporal RoPE); bytes are the attention kernel's own (the statistic and K passes are
     # separate launches).
+    # Q, K and V are separate draws and q_norm / k_norm separate weights (separate seeds per
+    # operand, as BenchGEMM.swift:627-632 draws them), as the module's projections are.
     B, Tv, Ta = 2, 15360, 152
     tabs = L.rotaries(121, 768, 1280, audio_tokens=Ta)
     rvc = L.Rotary(*(_dev_bits(t, device) for t in tabs["videoCross"]))
     rac = L.Rotary(*(_dev_bits(t, device) for t in tabs["audioCross"]))
-    w4 = _randn((4096,), 0x5EED + 100, device, 1.0, 0.02)
-    w2 = _randn((2048,), 0x5EED + 101, device, 1.0, 0.02)
+    wq4, wk4 = (_randn((4096,), 0x5EED + 100 + i, device, 1.0, 0.02) for i in range(2))
+    wq2, wk2 = (_randn((2048,), 0x5EED + 102 + i, device, 1.0, 0.02) for i in range(2))
     qv = _randn((B, Tv, 4096), 0x5EED + 50, device)
     kt = _randn((B, 1024, 4096), 0x5EED + 70, device)
-    measure("block_text_cross_15360_B2", qv, kt, kt, 2 * (2 * B * Tv + 2 * 188) * 4096,
-            4.0 * B * Tv * 94 * 4096, q_norm_w=w4, k_norm_w=w4, k_valid_len=[94, 94])
-    del qv, kt
+    vt = _randn((B, 1024, 4096), 0x5EED + 71, device)
+    measure("block_text_cross_15360_B2", qv, kt, vt, 2 * (2 * B * Tv + 2 * 188) * 4096,
+            4.0 * B * Tv * 94 * 4096, q_norm_w=wq4, k_norm_w=wk4, k_valid_len=[94, 94])
+    del qv, kt, vt
     qv2 = _randn((B, Tv, 2048), 0x5EED + 90, device)
     ka = _randn((B, Ta, 2048), 0x5EED + 60, device)
-    measure("block_video_q_15360x152_B2", qv2, ka, ka,
+    va = _randn((B, Ta, 2048), 0x5EED + 61, device)
+    measure("block_video_q_15360x152_B2", qv2, ka, va,
             2 * (2 * B * Tv + 2 * B * Ta) * 2048 + 2 * (Tv + Ta) * 2048,
-            4.0 * B * Tv * Ta * 2048, q_norm_w=w2, k_norm_w=w2, rotary=rvc, key_rotary=rac)
+            4.0 * B * Tv * Ta * 2048, q_norm_w=wq2, k_norm_w=wk2, rotary=rvc, key_rotary=rac)
+    return res
+
+
+def bench_text_cross_unmasked(device, steps, warmup, hip):
+    """The text cross-attention as the DiT runs it: every one of the 1024 text tokens
+    attended, no mask (DiTForward.swift:38-42 passes none; DiTAttention.swift:374-376 runs
+    mask: .none). The reference bench's attn2 / audio_attn2 cases at the production shape
+    (BenchGEMM.swift:478-484: B = 1, raw SDPA, 3120 video / 126 audio queries over 1024 keys),
+    and the block set's pair at 1280x768x121 with CFG (B = 2, 2 x 15360 video and 2 x 152
+    audio queries, q / k norm over the inner dim). Q, K, V separate draws. Per call: the
+    attention kernel's median time over `steps` calls (events the library records around it),
+    the whole call's, TFLOP/s (4 * Sq * Skv * H * D) and % of the dense bf16 peak."""
+    import torch
+
+    import ltx_attn as L
+
+    H, Tt = 32, 1024
+    ws = torch.empty(256 << 20, dtype=torch.uint8, device=device)
+    res = {}
+    cases = (("attn2_3120x1024_B1", 1, 3120, 4096, False, 200),
+             ("audio_attn2_126x1024_B1", 1, 126, 2048, False, 210),
+             ("attn2_15360x1024_B2_norm", 2, 15360, 4096, True, 220),
+             ("audio_attn2_152x1024_B2_norm", 2, 152, 2048, True, 230))
+    for name, B, Tq, inner, norm, seed in cases:
+        q = _randn((B, Tq, inner), 0x5EED + seed, device)
+        k = _randn((B, Tt, inner), 0x5EED + seed + 1, device)
+        v = _randn((B, Tt, inner), 0x5EED + seed + 2, device)
+        kw = {}
+        if norm:
+            kw = dict(q_norm_w=_randn((inner,), 0x5EED + seed + 3, device, 1.0, 0.02),
+                      k_norm_w=_randn((inner,), 0x5EED + seed + 4, device, 1.0, 0.02))
+        out = torch.empty_like(q)
+
+        def call(ev):
+            L.attention_fwd(q, k, v, heads=H, out=out, workspace=ws,
+                            events=None if ev is None else (ev[0], ev[1]), **kw)
+
+        wall, _ = time_steps(call, steps, warmup, hip, events_per_step=False)
+        _, kms = time_steps(call, steps, 0, hip)
+        st = stats(kms)
+        fl = 4.0 * B * Tq * Tt * inner
+        res[name] = {"kernel_ms": st["median_ms"], "call_ms": round(wall / steps * 1e3, 4),
+                     "kernel_tflops": round(fl / (st["median_ms"] * 1e-3) / 1e12, 1),
+                     "pct_peak": round(100 * fl / (st["median_ms"] * 1e-3) / 1e12
+                                       / PEAK_BF16_TFLOPS, 2),
+                     "gflop": round(fl / 1e9, 2), "kernel_time_stats": st}
+        del q, k, v, out
     return res
 
 
@@ -400,10 +451,16 @@ def bench_gemma(device, steps, warmup):
     return res
 
 
-def bench_c5(device, steps, warmup, hip):
+def bench_c5(device, steps, warmup, hip, per_call_repeats=10):
     """The six attentions of one DiT block at 1280x768x121, B=2 (CFG), in block order
     (Sources/LTXModules/DiTBlock.swift:343-438): attn1, audio_attn1, attn2, audio_attn2,
-    audio_to_video, video_to_audio."""
+    audio_to_video, video_to_audio. Every call's Q, K and V are separate draws and every
+    module's q_norm / k_norm separate weights (separate seeds per operand, as
+    BenchGEMM.swift:627-632 draws them), as the module's projections and norms are. The text
+    keys have 94 valid of 1024 per row (the block-set configuration); the unmasked text cross
+    the DiT runs is timed by bench_text_cross_unmasked. Per call, the attention kernel's
+    median over `per_call_repeats` calls after 3 warm-up calls (the reference's protocol,
+    BenchGEMM.swift:96-100)."""
     import torch
 
     import ltx_attn as L
@@ -411,36 +468,27 @@ def bench_c5(device, steps, warmup, hip):
     Tv, Ta, Tt, B = 15360, 152, 1024, 2
     tabs = L.rotaries(121, 768, 1280, audio_tokens=Ta)
     rot = {k: L.Rotary(_dev_bits(c, device), _dev_bits(s, device)) for k, (c, s) in tabs.items()}
-    s = {}
-    for name, T, inner, seed in (("v", Tv, 4096, 50), ("a", Ta, 2048, 60),
-                                 ("t4096", Tt, 4096, 70), ("t2048", Tt, 2048, 80),
-                                 ("v2048", Tv, 2048, 90)):
-        s[name] = _randn((B, T, inner), 0x5EED + seed, device)
-    w4 = _randn((4096,), 0x5EED + 100, device, 1.0, 0.02)
-    w2 = _randn((2048,), 0x5EED + 101, device, 1.0, 0.02)
-    ws = torch.empty(512 << 20, dtype=torch.uint8, device=device)
     valid = [94, 94]
-    calls = [
-        ("attn1", s["v"], s["v"], w4, rot["videoSelf"], None, None),
-        ("audio_attn1", s["a"], s["a"], w2, rot["audioSelf"], None, None),
-        ("attn2", s["v"], s["t4096"], w4, None, None, valid),
-        ("audio_attn2", s["a"], s["t2048"], w2, None, None, valid),
-        ("audio_to_video_attn", s["v2048"], s["a"], w2, rot["videoCross"], rot["audioCross"],
-         None),
-        ("video_to_audio_attn", s["a"], s["v2048"], w2, rot["audioCross"], rot["videoCross"],
-         None),
+    # name, query stream (tokens, width), key stream, q table, k table, text valid lengths
+    spec = [
+        ("attn1", (Tv, 4096), (Tv, 4096), "videoSelf", None, None),
+        ("audio_attn1", (Ta, 2048), (Ta, 2048), "audioSelf", None, None),
+        ("attn2", (Tv, 4096), (Tt, 4096), None, None, valid),
+        ("audio_attn2", (Ta, 2048), (Tt, 2048), None, None, valid),
+        ("audio_to_video_attn", (Tv, 2048), (Ta, 2048), "videoCross", "audioCross", None),
+        ("video_to_audio_attn", (Ta, 2048), (Tv, 2048), "audioCross", "videoCross", None),
     ]
-    outs = [torch.empty_like(c[1]) for c in calls]
-    flops = 0.0
-    for _, q, kv, _, _, _, vl in calls:
-        Lq, Lk, inner = q.shape[1], kv.shape[1], q.shape[2]
-        nk = Lk if vl is None else vl[0]
-        flops += 4.0 * q.shape[0] * Lq * nk * inner
-
-    # the block driver runs the six calls in block order (the same calls as listed above)
-    norms = {name: (w, w) for name, _, _, w, _, _, _ in calls}
-    names = [c[0] for c in calls]
-    io = {name: (c[1], c[2], c[2], outs[i]) for i, (name, c) in enumerate(zip(names, calls))}
+    ops, norms, flops = {}, {}, 0.0
+    for i, (name, (Lq, wq_), (Lk, wk_), _, _, vl) in enumerate(spec):
+        seed = 0x5EED + 50 + 10 * i
+        ops[name] = (_randn((B, Lq, wq_), seed, device), _randn((B, Lk, wk_), seed + 1, device),
+                     _randn((B, Lk, wk_), seed + 2, device))
+        norms[name] = (_randn((wq_,), seed + 3, device, 1.0, 0.02),
+                       _randn((wk_,), seed + 4, device, 1.0, 0.02))
+        flops += 4.0 * B * Lq * (Lk if vl is None else vl[0]) * wq_
+    outs = {name: torch.empty_like(ops[name][0]) for name in ops}
+    ws = torch.empty(512 << 20, dtype=torch.uint8, device=device)
+    io = {name: ops[name] + (outs[name],) for name in ops}
     tables = {"videoSelf": rot["videoSelf"], "audioSelf": rot["audioSelf"],
               "videoCross": rot["videoCross"], "audioCross": rot["audioCross"]}
     block = L.DiTBlockAttention(norms)
@@ -452,19 +500,24 @@ def bench_c5(device, steps, warmup, hip):
                           workspace=ws)
 
     wall, _ = time_steps(call, steps, warmup, hip, events_per_step=False)
-    # per-attention kernel time (one call each, events around the attention kernel)
-    per = {}
-    for i, (name, q, kv, w, r, kr, vl) in enumerate(calls):
-        a, b = hip.create(), hip.create()
-        L.attention_fwd(q, kv, kv, heads=32, q_norm_w=w, k_norm_w=w, rotary=r, key_rotary=kr,
-                        k_valid_len=vl, out=outs[i], workspace=ws, events=(a, b))
-        torch.cuda.synchronize()
-        per[name] = round(hip.elapsed_ms(a, b), 4)
-        hip.destroy(a)
-        hip.destroy(b)
+    # per-attention kernel time: events around the attention kernel, median of the repeats
+    per, per_stats = {}, {}
+    for name, _, _, pe, kpe, vl in spec:
+        q, k, v = ops[name]
+
+        def one(ev, q=q, k=k, v=v, name=name, pe=pe, kpe=kpe, vl=vl):
+            L.attention_fwd(q, k, v, heads=32, q_norm_w=norms[name][0],
+                            k_norm_w=norms[name][1], rotary=rot[pe] if pe else None,
+                            key_rotary=rot[kpe] if kpe else None, k_valid_len=vl,
+                            out=outs[name], workspace=ws,
+                            events=None if ev is None else (ev[0], ev[1]))
+
+        _, kms = time_steps(one, per_call_repeats, 3, hip)
+        per_stats[name] = stats(kms)
+        per[name] = per_stats[name]["median_ms"]
     ms = wall / steps * 1e3
     return {"ms_per_block": ms, "tflops": flops / (ms * 1e-3) / 1e12,
-            "kernel_ms": per}
+            "kernel_ms": per, "kernel_time_stats": per_stats}
 
 
 def bench_rope_tables(device):
@@ -665,6 +718,10 @@ def main():
     ap.add_argument("--block-only", action="store_true",
                     help="only run one DiT block's six attentions at 1280x768x121, B=2, "
                          "--steps times (for counter passes)")
+    ap.add_argument("--text-cross-only", action="store_true",
+                    help="only run the unmasked text cross-attention calls (3120 and 126 "
+                         "queries over 1024 keys, B=1; 2 x 15360 and 2 x 152 with norm), "
+                         "--steps timed calls each")
     ap.add_argument("--gemma-only", action="store_true",
                     help="only run the Gemma-4 encoder attention (sliding and full layer at "
                          "1024 tokens), --steps timed calls each")
@@ -722,6 +779,11 @@ def main():
         print(json.dumps({"dit_block_attn": res}), flush=True)
         return
 
+    if args.text_cross_only:
+        res = bench_text_cross_unmasked(device, args.steps, args.warmup, hip)
+        print(json.dumps({"text_cross_unmasked": res}), flush=True)
+        return
+
     if args.gemma_only:
         res = bench_gemma(device, args.steps, args.warmup)
         print(json.dumps({"gemma_text_encoder_attn": res}), flush=True)
@@ -745,6 +807,10 @@ def main():
                                                  f"({v['kernel_gbs']:.0f} GB/s)"
                                                  for k, v in short.items()),
               file=sys.stderr, flush=True)
+        tcu = bench_text_cross_unmasked(device, 10, 3, hip)
+        print("# text cross, unmasked 1024 keys: " + ", ".join(
+            f"{k} {v['kernel_ms']:.4f} ms ({v['kernel_tflops']:.0f} TFLOP/s)"
+            for k, v in tcu.items()), file=sys.stderr, flush=True)
         conn = bench_connector(device, 10, 3, hip)
         gemma = bench_gemma(device, 10, 3)
         c5 = bench_c5(device, 5, 2, hip)
@@ -766,11 +832,13 @@ def main():
             "video_self_3120_call_ms": round(c1["ms_per_call"], 4),
             "video_self_3120_call_tflops": round(c1["tflops"], 2),
             "short_key_calls": short,
+            "text_cross_unmasked": tcu,
             "connector_attn_1024": conn,
             "gemma_text_encoder_attn": gemma,
             "dit_block_attn_ms": round(c5["ms_per_block"], 4),
             "dit_block_attn_tflops": round(c5["tflops"], 2),
             "dit_block_attn_kernel_ms": c5["kernel_ms"],
+            "dit_block_attn_kernel_time_stats": c5["kernel_time_stats"],
             "video_self_3120_kernel_time_stats": c1["kernel_stats"],
             "video_self_3120_call_time_stats": c1["call_stats"],
             "rope_tables_12480_device_ms": round(rope["device_ms"], 4),

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define LTX_ATTN_ABI_VERSION 7
+#define LTX_ATTN_ABI_VERSION 8
 
 /* Status codes. The reference throws `DiTAttention.Failure` for structural errors
  * (DiTAttention.swift:107-121); a Swift wrapper maps these onto thrown errors. */
@@ -136,6 +136,12 @@ typedef struct ltx_attn_args {
     const float *q_sumsq, *k_sumsq;
     int64_t q_sumsq_rs, k_sumsq_rs;   /* >= sumsq_blocks                                  */
     int32_t sumsq_blocks;             /* >= 1 when either pointer is given                */
+
+    /* Work planning. 0 (the default) = plan the tail splits for the current device's CU count
+     * (queried once per device); n > 0 = plan as if n workgroups were resident at once instead
+     * (a test of the plan of another part size; at most 65536). Results agree within the
+     * fp32 merge order whatever the plan. */
+    int32_t resident_groups;
 } ltx_attn_args;
 
 /* Fill `a` with defaults: zero sizes and pointers, norm_eps = 1e-6, kprep AUTO, splits auto. */
@@ -143,10 +149,9 @@ void ltx_attn_args_init(ltx_attn_args *a);
 
 /* Bytes of workspace ltx_attn_fwd needs for these arguments (0 if none). Pure host function;
  * returns 0 and sets the thread's error detail if the arguments are invalid. It plans for a
- * whole gfx950 part (256 CUs); on a device with another CU count ltx_attn_fwd plans its tail
- * splits for that count when the given workspace covers that plan, else runs the sized one.
- * The environment variable LTX_ATTN_RESIDENT_GROUPS (an integer 1..65536), when set, stands in
- * for the device's CU count in that choice (ltx_linear's too). */
+ * whole gfx950 part (256 CUs); on a device with another CU count (or with resident_groups
+ * set) ltx_attn_fwd plans its tail splits for that count when the given workspace covers that
+ * plan and is 256-byte aligned, else runs the sized one. */
 size_t ltx_attn_workspace_bytes(const ltx_attn_args *a);
 
 /* Check the arguments without launching anything (the first step of ltx_attn_fwd). */
@@ -166,7 +171,8 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream);
  * `workspace` / `workspace_bytes` are ignored: the call's scratch (statistics, prepared K,
  * split-KV partials) is a file-scope device array of LTX_ATTN_STATIC_SCRATCH_BYTES per
  * device, looked up on the first call on each device and held until the process ends. Same
- * plan, kernels and results as ltx_attn_fwd. Calls needing more scratch than that (see
+ * plan, kernels and results as ltx_attn_fwd given a workspace of exactly
+ * ltx_attn_workspace_bytes for the same arguments. Calls needing more scratch than that (see
  * ltx_attn_workspace_bytes) return LTX_ATTN_EUNSUPPORTED before anything is launched. The
  * array is shared by every call on a device: calls that overlap on one device race, so the
  * caller serialises them. Allocates nothing. */
@@ -217,6 +223,9 @@ typedef struct ltx_linear_args {
      * tiles run whole: same result up to fp32 summation order, slower. */
     void *workspace;
     size_t workspace_bytes;
+    /* 0 = split the tail for the current device's CU count; n > 0 = for n resident workgroups
+     * (as in ltx_attn_args). */
+    int32_t resident_groups;
 } ltx_linear_args;
 
 /* ceil(N / LTX_LINEAR_SUMSQ_COLS): partial sums per row of y. */

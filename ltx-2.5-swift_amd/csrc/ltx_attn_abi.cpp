@@ -14,6 +14,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <utility>
 
 #include "../../include/ltx_attn.h"
@@ -42,22 +43,31 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // tail splitting differs.
 constexpr int64_t kConcurrentGroups = 256;
 
-// CU count of the calling thread's current device; kConcurrentGroups if the runtime cannot
-// say (the error of a failed query is cleared so that the launches' checks do not see it).
-// LTX_ATTN_RESIDENT_GROUPS, a positive integer, stands in for the count (tests of the plans of
-// other part sizes).
-int64_t device_groups() {
-    if (const char *e = getenv("LTX_ATTN_RESIDENT_GROUPS")) {
-        const long v = strtol(e, nullptr, 10);
-        if (v > 0 && v <= 65536) return v;
+// CU count of the calling thread's current device, queried once per device (the count does
+// not change while the process runs); kConcurrentGroups if the runtime cannot say (the error
+// of a failed query is cleared so that the launches' checks do not see it). A caller's
+// resident_groups > 0 stands in for it (tests of the plans of other part sizes).
+constexpr int kMaxDevices = 64;
+std::atomic<int32_t> g_device_cus[kMaxDevices];   // 0 = not queried yet
+
+int64_t device_groups(int32_t override_groups) {
+    if (override_groups > 0) return override_groups;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return kConcurrentGroups;
     }
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+    if (dev >= 0 && dev < kMaxDevices) {
+        const int32_t known = g_device_cus[dev].load(std::memory_order_relaxed);
+        if (known > 0) return known;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0) {
         (void)hipGetLastError();
         return kConcurrentGroups;
     }
+    if (dev >= 0 && dev < kMaxDevices) g_device_cus[dev].store(cus, std::memory_order_relaxed);
     return cus;
 }
 // Charge per extra split of a tail item, in rounds: its fp32 partial O is written and read
@@ -202,6 +212,8 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl,
     }
     if (a->kprep < LTX_ATTN_KPREP_AUTO || a->kprep > LTX_ATTN_KPREP_PROLOGUE)
         return fail(LTX_ATTN_EINVAL, "kprep %d is not an ltx_attn_kprep", a->kprep);
+    if (a->resident_groups < 0 || a->resident_groups > 65536)
+        return fail(LTX_ATTN_EINVAL, "resident_groups %d outside [0, 65536]", a->resident_groups);
     if (a->num_splits < 0 || a->num_splits > ltx::kMaxSplits)
         return fail(LTX_ATTN_EINVAL, "num_splits %d outside [0, %d]", a->num_splits,
                     ltx::kMaxSplits);
@@ -476,11 +488,12 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     ltx_attn_status s = ltx_attn_validate(a);
     if (s) return s;
     Plan pl;
-    // the device's own plan when the workspace covers it, else the one it was sized for
-    const int64_t groups = device_groups();
+    // the device's own plan when the workspace covers it (and is aligned for it), else the
+    // one it was sized for, which ltx_attn_validate has checked
+    const int64_t groups = device_groups(a->resident_groups);
     make_plan(a, &pl, groups);
     if (groups != kConcurrentGroups && pl.bytes > 0 &&
-        (!a->workspace || pl.bytes > a->workspace_bytes))
+        (!a->workspace || pl.bytes > a->workspace_bytes || ((uintptr_t)a->workspace & 255u)))
         make_plan(a, &pl);
     char *ws = (char *)a->workspace;
     const int B = a->B, H = a->H, D = a->D;
@@ -836,7 +849,9 @@ ltx_attn_status ltx_linear(const ltx_linear_args *a, void *stream) {
     p.M = a->M; p.N = a->N; p.K = a->K;
     p.tiles_m = (int32_t)tiles_m; p.tiles_n = (int32_t)tiles_n;
     // the device's own tail split when the workspace covers it, else the one it was sized for
-    const int64_t groups = device_groups();
+    if (a->resident_groups < 0 || a->resident_groups > 65536)
+        return fail(LTX_ATTN_EINVAL, "resident_groups %d outside [0, 65536]", a->resident_groups);
+    const int64_t groups = device_groups(a->resident_groups);
     LinearSplit ls = linear_split(a->M, a->N, a->K, groups);
     if (groups != kConcurrentGroups && ls.splits > 1 &&
         (!a->workspace || a->workspace_bytes < ls.bytes))

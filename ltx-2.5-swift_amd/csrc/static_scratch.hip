@@ -3,7 +3,8 @@
 // scratch -- the Q/K statistics, the prepared K' of the K prologue and the split-KV partials,
 // which ltx_attn_fwd takes from the caller's workspace -- lives in one file-scope device
 // array of kScratchBytes instead. Same plan, same kernels, same results as ltx_attn_fwd with
-// a workspace; calls that need more scratch than the array holds are refused.
+// a workspace of ltx_attn_workspace_bytes; calls that need more scratch than the array holds
+// are refused.
 //
 // The array's name is only a host-side stand-in: its device address is looked up once per
 // device (hipGetSymbolAddress, with that device current) on the first call there, and that
@@ -71,7 +72,10 @@ extern "C" ltx_attn_status ltx_attn_fwd_static(const ltx_attn_args *a, void *str
     if (g_lookup[dev] != hipSuccess || !g_scratch[dev])
         return fail(LTX_ATTN_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
                     hipGetErrorString(g_lookup[dev]));
+    // exactly the sized workspace: ltx_attn_fwd then picks the plan it would pick for a
+    // caller's workspace of ltx_attn_workspace_bytes (the device's own plan only where that
+    // fits in it), so both entry points run the same plan on any part
     b.workspace = g_scratch[dev];
-    b.workspace_bytes = kScratchBytes;
+    b.workspace_bytes = need;
     return ltx_attn_fwd(&b, stream);
 }

@@ -65,6 +65,7 @@ class Args(ctypes.Structure):
         ("q_sumsq", ctypes.c_void_p), ("k_sumsq", ctypes.c_void_p),
         ("q_sumsq_rs", ctypes.c_int64), ("k_sumsq_rs", ctypes.c_int64),
         ("sumsq_blocks", ctypes.c_int32),
+        ("resident_groups", ctypes.c_int32),
     ]
 
 
@@ -78,6 +79,7 @@ class LinearArgs(ctypes.Structure):
         ("x_rs", ctypes.c_int64), ("w_rs", ctypes.c_int64), ("y_rs", ctypes.c_int64),
         ("sumsq", ctypes.c_void_p), ("sumsq_rs", ctypes.c_int64),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("resident_groups", ctypes.c_int32),
     ]
 
 
@@ -358,7 +360,8 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
                   k_valid_len: Optional[Sequence[int]] = None, scale: Optional[float] = None,
                   out=None, kprep: int = KPREP_AUTO, num_splits: int = 0, stream=None,
                   workspace=None, events=None, gate_logits=None, all_perturbed: bool = False,
-                  q_sumsq=None, k_sumsq=None, no_alloc: bool = False):
+                  q_sumsq=None, k_sumsq=None, no_alloc: bool = False,
+                  resident_groups: int = 0):
     """One call of ``ltx_attn_fwd``. Tensors are torch bf16 on the current HIP device.
 
     ``layout="merged"``: q ``[B, Lq, H*D]``, k/v ``[B, Lk, H*D]``, out ``[B, Lq, H*D]``.
@@ -374,6 +377,8 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
     ``no_alloc``: call ``ltx_attn_fwd_static`` instead, whose scratch is the library's own
     per-device array (no workspace is made or passed; calls needing more than
     ``STATIC_SCRATCH_BYTES`` raise ``Failure``).
+    ``resident_groups``: 0 plans the work for the device's CU count; n > 0 plans it as if n
+    workgroups were resident at once (a test of another part size's plan).
     Returns ``out``.
     """
     import torch
@@ -431,6 +436,7 @@ def attention_fwd(q, k, v, *, heads: int, layout: str = "merged", q_norm_w=None,
     a.o_bs, a.o_rs, a.o_hs = os_
     a.kprep = kprep
     a.num_splits = num_splits
+    a.resident_groups = resident_groups
     if events is not None:
         a.ev_attn_start, a.ev_attn_stop = events
     a.all_perturbed = 1 if all_perturbed else 0
@@ -493,7 +499,8 @@ def linear_workspace_bytes(M: int, N: int, K: int) -> int:
     return load_library().ltx_linear_workspace_bytes(ctypes.byref(a))
 
 
-def linear(x, weight, bias=None, *, out=None, sumsq=False, stream=None, workspace=None):
+def linear(x, weight, bias=None, *, out=None, sumsq=False, stream=None, workspace=None,
+           resident_groups: int = 0):
     """``linear(_:_:)`` of ``DiTAttention.swift:178-188`` through ``ltx_linear``:
     ``y = x . weight^T (+ bias)``, bf16 in and out, fp32 accumulation.
 
@@ -505,6 +512,7 @@ def linear(x, weight, bias=None, *, out=None, sumsq=False, stream=None, workspac
     squares of its bf16 outputs over columns ``[256 j, 256 j + 256)``. ``workspace``: a
     device tensor of at least ``linear_workspace_bytes(M, N, K)`` bytes for the split tail;
     None allocates one when the shape splits, ``False`` runs every tile whole.
+    ``resident_groups``: as in ``attention_fwd`` (0: the device's CU count).
     Returns ``y`` or ``(y, partials)``.
     """
     import torch
@@ -530,6 +538,7 @@ def linear(x, weight, bias=None, *, out=None, sumsq=False, stream=None, workspac
         raise Failure(EINVAL, f"bias must be a contiguous [{N}] tensor")
     a = LinearArgs()
     a.M, a.N, a.K = M, N, K
+    a.resident_groups = resident_groups
     a.x, a.w, a.bias, a.y = _ptr(x2), _ptr(weight), _ptr(bias), _ptr(y2)
     a.x_rs = x2.stride(0) if M > 1 else K
     a.w_rs = weight.stride(0) if N > 1 else K

@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layout_and_version():
     lib = L.load_library()
     assert lib.ltx_attn_args_size() == ctypes.sizeof(L.Args)
-    assert lib.ltx_attn_abi_version() == 7
+    assert lib.ltx_attn_abi_version() == 8
     assert "gfx950" in L.provenance()
     for s in range(5):
         assert lib.ltx_attn_status_string(s)
@@ -111,6 +111,8 @@ def test_valid_arguments_pass():
     ("scale", float("nan"), L.EINVAL),
     ("kprep", 7, L.EINVAL),
     ("num_splits", 17, L.EINVAL),
+    ("resident_groups", -1, L.EINVAL),
+    ("resident_groups", 65537, L.EINVAL),
 ])
 def test_invalid_arguments_are_rejected(field, value, status):
     a = _args()
@@ -294,6 +296,7 @@ def _linear_args(M=12480, N=4096, K=4096, **kw):
     ("x_rs", 1 << 23, L.EUNSUPPORTED),  # a 256-row tile past 32-bit offsets
     ("sumsq", FAKE + (3 << 32) + 2, L.EINVAL),
     ("y", FAKE + 1024, L.EINVAL),       # y overlaps x
+    ("resident_groups", -3, L.EINVAL),
 ])
 def test_linear_rejects_bad_arguments(field, value, status):
     """Every rejection happens on the host before a launch (this host has no GPU)."""
@@ -339,9 +342,13 @@ def test_linear_workspace_is_checked():
     launch; a smaller one (or none) means whole tiles, not an error."""
     lib = L.load_library()
     need = L.linear_workspace_bytes(12480, 4096, 4096)
+    assert need > 0                       # 784 tiles: the 16 past three rounds split along K
     base = FAKE + (8 << 32)
     a = _linear_args(M=12480, N=4096, K=4096, x=base, w=base + (1 << 30),
                      y=base + (2 << 30), x_rs=4096, w_rs=4096, y_rs=4096)
+    # the plan the workspace was sized for, whatever device (or none) this host has: the
+    # checks below run before any launch on the fake pointers
+    a.resident_groups = 256
     a.workspace, a.workspace_bytes = base + (3 << 30) + 128, need
     assert lib.ltx_linear(ctypes.byref(a), None) == L.EINVAL          # not 256-byte aligned
     a.workspace = base + (2 << 30)                                    # on top of y

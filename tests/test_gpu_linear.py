@@ -253,15 +253,14 @@ def test_tail_split_matches_whole_tiles(device, M, N, K):
 
 
 @pytest.mark.parametrize("groups", [32, 100])
-def test_tail_split_for_other_part_sizes(device, groups, monkeypatch):
-    """ltx_linear splits its tail for the device's CU count (LTX_ATTN_RESIDENT_GROUPS stands in
-    for it) when the workspace sized for 256 CUs covers that split: 3000 x 1024 x 512 is 48
+def test_tail_split_for_other_part_sizes(device, groups):
+    """ltx_linear splits its tail for the device's CU count (the resident_groups argument
+    stands in for it) when the workspace sized for 256 CUs covers that split: 3000 x 1024 x 512 is 48
     tiles; 32 groups split the 16 past one round two ways, 100 split all 48 two ways (the sized
     split: four ways). The oracle on the rows of a whole tile and of a split one, and the
     statistic partials of every row."""
     import torch
 
-    monkeypatch.setenv("LTX_ATTN_RESIDENT_GROUPS", str(groups))
     M, N, K = 3000, 1024, 512
     need = L.linear_workspace_bytes(M, N, K)
     assert need > 0
@@ -270,7 +269,8 @@ def test_tail_split_for_other_part_sizes(device, groups, monkeypatch):
     b = O.randn_bf16_bits((N,), 1000 + groups, std=0.5)
     _say(f"linear {M}x{N}x{K}, tail split for {groups} resident groups")
     ws = torch.empty(need, dtype=torch.uint8, device=device)
-    y, parts = L.linear(dev(x, device), dev(w, device), dev(b, device), sumsq=True, workspace=ws)
+    y, parts = L.linear(dev(x, device), dev(w, device), dev(b, device), sumsq=True, workspace=ws,
+                        resident_groups=groups)
     torch.cuda.synchronize()
     yb = host_bits(y)
     rows = np.r_[0:64, 1024:1088, M - 64:M]

@@ -309,15 +309,13 @@ def test_rebase_path_large_logits(device):
     check(got, truth, None, "rebase split")
 
 
-@pytest.mark.parametrize("D,groups", [(64, None), (128, None), (128, "6")])
-def test_dma_kernel_large_logits(device, D, groups, monkeypatch):
+@pytest.mark.parametrize("D,groups", [(64, 0), (128, 0), (128, 6)])
+def test_dma_kernel_large_logits(device, D, groups):
     """The LDS-DMA kernel (three query blocks per head) on logits growing along the keys, far
     past the first block's max: its row sums (matrix-core products) pass 2^64, so the fast pass
     is discarded and the items redo their keys with the exact online softmax. With the
     device's CU count the six items run as split key ranges (and the combine); with six
     resident groups they run whole. scale = ln 2 folds to exactly 1, so the logits are exact."""
-    if groups:
-        monkeypatch.setenv("LTX_ATTN_RESIDENT_GROUPS", groups)
     B, H, Lq, Lk = 1, 2, 600, 1200
     _say(f"LDS-DMA kernel, large logits: D={D} groups={groups}")
     rng = np.random.default_rng(11 + D)
@@ -328,7 +326,7 @@ def test_dma_kernel_large_logits(device, D, groups, monkeypatch):
     v = O.randn_bf16_bits((B, Lk, H * D), 12)
     scale = float(np.float32(math.log(2.0)))
     truth = O.attention(q, k, v, H, scale=scale, mode="exact")
-    got = run(device, q, k, v, H, scale=scale)
+    got = run(device, q, k, v, H, scale=scale, resident_groups=groups)
     check(got, truth, None, f"LDS-DMA large logits D={D} groups={groups}")
 
 
@@ -556,9 +554,9 @@ def test_whole_and_tail_items_ragged(device, kprep):
 
 @pytest.mark.parametrize("H,T,groups", [(12, 1300, 32), (12, 1300, 100), (12, 1300, 200),
                                          (16, 2400, 150)])
-def test_plans_for_other_part_sizes(device, H, T, groups, monkeypatch):
-    """A call plans its tail splits for the device's CU count (LTX_ATTN_RESIDENT_GROUPS stands
-    in for it) when the workspace covers that plan, and runs the plan the workspace was sized
+def test_plans_for_other_part_sizes(device, H, T, groups):
+    """A call plans its tail splits for the device's CU count (the resident_groups argument
+    stands in for it) when the workspace covers that plan, and runs the plan the workspace was sized
     for (256 CUs) otherwise. 12 heads x 6 query blocks = 72 items: 32 groups split the 8 tail
     items four ways, 100 run all 72 whole, 200 split every item two ways (the sized plan: three
     ways; both fit its workspace). 16 heads x 10 query blocks = 160 items: 150 groups split the
@@ -567,15 +565,16 @@ def test_plans_for_other_part_sizes(device, H, T, groups, monkeypatch):
     oracle."""
     import torch
 
-    monkeypatch.setenv("LTX_ATTN_RESIDENT_GROUPS", str(groups))
     tq, qb = _gpu_bits((1, T, H * 128), 0x5EED + 70, device)
     tk, kb = _gpu_bits((1, T, H * 128), 0x5EED + 71, device)
     tv, vb = _gpu_bits((1, T, H * 128), 0x5EED + 72, device)
     _say(f"{H} heads x {T} tokens, plan for {groups} resident groups, sized workspace")
-    _full_check(device, tq, tk, tv, H, (qb, kb, vb), {}, {}, f"groups {groups} sized")
+    _full_check(device, tq, tk, tv, H, (qb, kb, vb), {}, {}, f"groups {groups} sized",
+                resident_groups=groups)
     _say(f"{H} heads x {T} tokens, plan for {groups} resident groups, large workspace")
     ws = torch.empty(64 << 20, dtype=torch.uint8, device=device)
-    _full_check(device, tq, tk, tv, H, (qb, kb, vb), {}, {"workspace": ws}, f"groups {groups} own")
+    _full_check(device, tq, tk, tv, H, (qb, kb, vb), {}, {"workspace": ws}, f"groups {groups} own",
+                resident_groups=groups)
 
 
 @pytest.mark.parametrize("direction", ["video_q", "audio_q"])
@@ -764,56 +763,96 @@ def test_text_cross_unmasked_as_the_dit_calls_it(device):
 
 def test_block_driver_matches_single_calls(device):
     """The block driver (DiTBlock.swift:343-438 order, one workspace) gives each module's
-    output bit for bit as its own call does: CFG rows with different text lengths, a gated
-    audio->video call, and a perturbed (STG passthrough) video self-attention."""
+    output bit for bit as its own call does, with every call's Q, K and V separate draws and
+    every module's q_norm / k_norm separate weights, so a Q/K/V or q_norm/k_norm mix-up inside
+    the driver changes the output: CFG rows with different text lengths, a gated
+    audio->video call, both self-attentions computed and then both perturbed (STG
+    passthrough). The driver's self-attention and cross-modal outputs are also checked
+    against the oracle over every head and row."""
     import torch
 
-    B, Ta, Tt = 2, 152, 1024
+    B, Ta, Tt, H = 2, 152, 1024, 32
     rot = L.rotaries_device(25, 320, 480, audio_tokens=Ta)
     Tv = rot["videoSelf"].cos.shape[1]
     _say(f"block driver: {Tv} video / {Ta} audio / {Tt} text tokens, B={B}")
+    seeds = iter(range(0x5EED + 900, 0x5EED + 1000))
 
-    def t(shape, seed, mean=0.0, std=1.0):
-        g = torch.Generator(device=device)
-        g.manual_seed(0x5EED + seed)
-        return (torch.randn(shape, generator=g, device=device) * std + mean).to(torch.bfloat16)
+    def t(shape, mean=0.0, std=1.0):
+        return _gpu_bits(shape, next(seeds), device, mean, std)
 
-    norms = {v.value: (t((4096 if v in (L.Variant.videoSelf, L.Variant.videoCross) else 2048,),
-                         100 + i, 1.0, 0.02),) * 2 for i, v in enumerate(L.Variant)}
-    v4, a2, t4, t2, v2 = (t((B, Tv, 4096), 1), t((B, Ta, 2048), 2), t((B, Tt, 4096), 3),
-                          t((B, Tt, 2048), 4), t((B, Tv, 2048), 5))
-    gate = t((B, Tv, 32), 6, 0.0, 2.0)
+    video = (L.Variant.videoSelf, L.Variant.videoCross)
+    norms = {v.value: tuple(t((4096 if v in video else 2048,), 1.0, 0.02) for _ in range(2))
+             for v in L.Variant}
+    shapes = {                                   # (query stream, key stream)
+        "attn1": ((Tv, 4096), (Tv, 4096)),
+        "audio_attn1": ((Ta, 2048), (Ta, 2048)),
+        "attn2": ((Tv, 4096), (Tt, 4096)),
+        "audio_attn2": ((Ta, 2048), (Tt, 2048)),
+        "audio_to_video_attn": ((Tv, 2048), (Ta, 2048)),
+        "video_to_audio_attn": ((Ta, 2048), (Tv, 2048)),
+    }
+    ops = {n: tuple(t((B,) + s) for s in (qs, ks, ks)) for n, (qs, ks) in shapes.items()}
+    gate = t((B, Tv, H), 0.0, 2.0)
     valid = [94, 11]
-    io = {
-        "attn1": (v4, v4, v4, torch.empty_like(v4)),
-        "audio_attn1": (a2, a2, a2, torch.empty_like(a2)),
-        "attn2": (v4, t4, t4, torch.empty_like(v4)),
-        "audio_attn2": (a2, t2, t2, torch.empty_like(a2)),
-        "audio_to_video_attn": (v2, a2, a2, torch.empty_like(v2), gate),
-        "video_to_audio_attn": (a2, v2, v2, torch.empty_like(a2)),
-    }
+
+    def io(name, gated=False):
+        q, k, v = (x[0] for x in ops[name])
+        out = torch.full_like(q, 7.0)
+        return (q, k, v, out, gate[0]) if gated else (q, k, v, out)
+
+    calls = {n: io(n, n == "audio_to_video_attn") for n in shapes}
     ws = torch.empty(256 << 20, dtype=torch.uint8, device=device)
-    blk = L.DiTBlockAttention(norms)
-    blk.self_attention(io["attn1"], io["audio_attn1"], rot, video_perturbed=True, workspace=ws)
-    blk.text_cross(io["attn2"], io["audio_attn2"], valid, workspace=ws)
-    blk.cross_modal(io["audio_to_video_attn"], io["video_to_audio_attn"], rot, workspace=ws)
+    blk = L.DiTBlockAttention({k: (w[0][0], w[1][0]) for k, w in norms.items()})
+    blk.self_attention(calls["attn1"], calls["audio_attn1"], rot, workspace=ws)
+    blk.text_cross(calls["attn2"], calls["audio_attn2"], valid, workspace=ws)
+    blk.cross_modal(calls["audio_to_video_attn"], calls["video_to_audio_attn"], rot,
+                    workspace=ws)
+    perturbed = {n: io(n) for n in ("attn1", "audio_attn1")}
+    blk.self_attention(perturbed["attn1"], perturbed["audio_attn1"], rot,
+                       video_perturbed=True, audio_perturbed=True, workspace=ws)
     torch.cuda.synchronize()
 
-    def single(name, **kw):
-        q, k, v = io[name][:3]
-        w = norms[name][0]
-        return L.attention_fwd(q, k, v, heads=32, q_norm_w=w, k_norm_w=w, **kw)
-
-    want = {
-        "attn1": v4,                                   # passthrough: V itself
-        "audio_attn1": single("audio_attn1", rotary=rot["audioSelf"]),
-        "attn2": single("attn2", k_valid_len=valid),
-        "audio_attn2": single("audio_attn2", k_valid_len=valid),
-        "audio_to_video_attn": single("audio_to_video_attn", rotary=rot["videoCross"],
-                                      key_rotary=rot["audioCross"], gate_logits=gate),
-        "video_to_audio_attn": single("video_to_audio_attn", rotary=rot["audioCross"],
-                                      key_rotary=rot["videoCross"]),
+    tables = {
+        "attn1": ("videoSelf", None), "audio_attn1": ("audioSelf", None),
+        "attn2": (None, None), "audio_attn2": (None, None),
+        "audio_to_video_attn": ("videoCross", "audioCross"),
+        "video_to_audio_attn": ("audioCross", "videoCross"),
     }
-    torch.cuda.synchronize()
-    for name, w in want.items():
-        assert torch.equal(io[name][3], w), name
+
+    def single(name):
+        q, k, v = (x[0] for x in ops[name])
+        wq, wk = (w[0] for w in norms[name])
+        pe, kpe = tables[name]
+        kw = dict(q_norm_w=wq, k_norm_w=wk)
+        if pe:
+            kw["rotary"] = rot[pe]
+        if kpe:
+            kw["key_rotary"] = rot[kpe]
+        if name in ("attn2", "audio_attn2"):
+            kw["k_valid_len"] = valid
+        if name == "audio_to_video_attn":
+            kw["gate_logits"] = gate[0]
+        return L.attention_fwd(q, k, v, heads=H, **kw)
+
+    for name in shapes:
+        assert torch.equal(calls[name][3], single(name)), name
+    for name in ("attn1", "audio_attn1"):                  # passthrough: V itself
+        assert torch.equal(perturbed[name][3], ops[name][2][0]), name
+
+    # the driver's outputs against the oracle (exact, and with the reference's rounding
+    # points), every head and row
+    for name in ("attn1", "audio_attn1", "audio_to_video_attn", "video_to_audio_attn"):
+        bits = tuple(x[1] for x in ops[name])
+        kw = dict(q_norm_w=norms[name][0][1], k_norm_w=norms[name][1][1])
+        pe, kpe = tables[name]
+        if pe:
+            kw.update(q_cos=host_bits(rot[pe].cos), q_sin=host_bits(rot[pe].sin))
+        if kpe:
+            kw.update(k_cos=host_bits(rot[kpe].cos), k_sin=host_bits(rot[kpe].sin))
+        truth = O.c_attention(*bits, H, mode="exact", **kw)
+        refm = O.round_bf16(O.c_attention(*bits, H, mode="reference", **kw))
+        if name == "audio_to_video_attn":
+            truth = truth * O.head_gate(gate[1])[..., None]
+            refm = O.round_bf16(refm * O.head_gate(gate[1], "reference")[..., None])
+        got = host_f32(calls[name][3]).reshape(truth.shape)
+        check_heads(got, truth, refm, f"block driver {name}")
