@@ -4,8 +4,9 @@
  * Swift imports this module and sees two things:
  *   - the attention library's C ABI (ltx_attn.h: ltx_attn_fwd, ltx_linear,
  *     ltx_gemma_attn_fwd, the RoPE table builders, ltx_device_query), unchanged;
- *   - cltx_*: device memory, host<->device copies and one stream, as plain C over the HIP
- *     runtime, so no HIP header has to be imported into Swift.
+ *   - cltx_*: device memory, page-locked host memory, host<->device copies, one stream and a
+ *     free-memory query, as plain C over the HIP runtime, so no HIP header has to be
+ *     imported into Swift.
  * Every function returns 0 on success or the hipError_t code; cltx_error_string() names it.
  */
 #ifndef CLTX_HIP_H
@@ -32,11 +33,19 @@ int32_t cltx_stream_create(void **out);
 int32_t cltx_stream_destroy(void *stream);
 int32_t cltx_stream_synchronize(void *stream);
 
-/* Copies between host memory and device memory, ordered on `stream`. The host side of an
- * upload may be reused once the call returns (the copy is staged); a download has landed
- * when cltx_stream_synchronize(stream) returns. */
+/* Page-locked host memory (`bytes` > 0) into *out: copies from and to it run asynchronously,
+ * without a staging copy by the runtime. */
+int32_t cltx_host_alloc(size_t bytes, void **out);
+int32_t cltx_host_free(void *ptr);
+
+/* Copies between host memory and device memory, ordered on `stream`, asynchronous: the host
+ * side must stay valid and unchanged until cltx_stream_synchronize(stream) returns (use
+ * cltx_host_alloc memory; pageable memory is staged by the runtime, slower). */
 int32_t cltx_upload(void *dst_device, const void *src_host, size_t bytes, void *stream);
 int32_t cltx_download(void *dst_host, const void *src_device, size_t bytes, void *stream);
+
+/* Free and total device memory of the current device, measured now (hipMemGetInfo). */
+int32_t cltx_mem_info(size_t *free_bytes, size_t *total_bytes);
 
 const char *cltx_error_string(int32_t code);
 

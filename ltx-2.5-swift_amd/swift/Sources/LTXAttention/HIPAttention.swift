@@ -179,6 +179,95 @@ public enum HIPAttention {
     }
 }
 
+/// The Gemma-4 text encoder's attention (`GemmaTextEncoder.swift:158-239`, with the mask of
+/// `:288-321`) through `ltx_gemma_attn_fwd`: from the q/k/v projections to the merged output
+/// before `o_proj`, fp32. Per head over D: q and k RMS-normed with their weights, v with none;
+/// `rotate_half` RoPE from the layer's tables; the KV-head repeat (GQA); scale 1.0; causal,
+/// sliding-window and left-padding mask, fully masked rows attending to every key.
+public enum HIPGemmaAttention {
+    /// One call's arguments (device pointers, element strides).
+    public struct Call {
+        public var batch: Int32, tokens: Int32
+        public var queryHeads: Int32, keyValueHeads: Int32, headDim: Int32
+        /// bf16 projections [B, T, heads * D]; `v == k` on the K-shares-V layers (V from the
+        /// pre-norm K projection, `:183-188`).
+        public var q: UnsafeRawPointer, k: UnsafeRawPointer, v: UnsafeRawPointer
+        public var qRowStride: Int64, kRowStride: Int64, vRowStride: Int64
+        public var qNormWeight: UnsafeRawPointer, kNormWeight: UnsafeRawPointer   // bf16 [D]
+        public var eps: Float
+        /// fp32 [T, D/2]: the first half of the layer's duplicated cos / sin rows (`:135-145`).
+        public var cos: UnsafeRawPointer, sin: UnsafeRawPointer
+        /// Sliding window (keys q - window < k <= q), 0 for the full layers.
+        public var window: Int32
+        /// Left padding per batch row (keys below are padding), or nil for none.
+        public var leftPadding: [Int32]?
+        /// `GemmaAttentionSpec.attentionScaling`.
+        public var scale: Float
+        /// fp32 [B, T, queryHeads * D].
+        public var out: UnsafeMutableRawPointer
+
+        public init(batch: Int32, tokens: Int32, queryHeads: Int32, keyValueHeads: Int32,
+                    headDim: Int32, q: UnsafeRawPointer, k: UnsafeRawPointer,
+                    v: UnsafeRawPointer, qRowStride: Int64, kRowStride: Int64,
+                    vRowStride: Int64, qNormWeight: UnsafeRawPointer,
+                    kNormWeight: UnsafeRawPointer, eps: Float, cos: UnsafeRawPointer,
+                    sin: UnsafeRawPointer, window: Int32, leftPadding: [Int32]?,
+                    scale: Float = 1.0, out: UnsafeMutableRawPointer) {
+            self.batch = batch; self.tokens = tokens
+            self.queryHeads = queryHeads; self.keyValueHeads = keyValueHeads
+            self.headDim = headDim
+            self.q = q; self.k = k; self.v = v
+            self.qRowStride = qRowStride; self.kRowStride = kRowStride
+            self.vRowStride = vRowStride
+            self.qNormWeight = qNormWeight; self.kNormWeight = kNormWeight
+            self.eps = eps; self.cos = cos; self.sin = sin
+            self.window = window; self.leftPadding = leftPadding
+            self.scale = scale; self.out = out
+        }
+
+        func withArgs<R>(_ body: (inout ltx_gemma_attn_args) throws -> R) rethrows -> R {
+            var a = ltx_gemma_attn_args()
+            a.B = batch; a.T = tokens; a.Hq = queryHeads; a.Hkv = keyValueHeads; a.D = headDim
+            a.q = q; a.k = k; a.v = v
+            a.q_rs = qRowStride; a.k_rs = kRowStride; a.v_rs = vRowStride
+            a.q_bs = qRowStride * Int64(tokens); a.k_bs = kRowStride * Int64(tokens)
+            a.v_bs = vRowStride * Int64(tokens)
+            a.q_norm_w = qNormWeight; a.k_norm_w = kNormWeight; a.eps = eps
+            a.cos = cos.assumingMemoryBound(to: Float.self)
+            a.sin = sin.assumingMemoryBound(to: Float.self)
+            a.window = window; a.scale = scale
+            a.out = out.assumingMemoryBound(to: Float.self)
+            a.o_rs = Int64(queryHeads * headDim); a.o_bs = a.o_rs * Int64(tokens)
+            guard let pad = leftPadding else { return try body(&a) }
+            return try pad.withUnsafeBufferPointer { p in
+                a.first_valid = p.baseAddress
+                return try body(&a)
+            }
+        }
+    }
+
+    /// Bytes of workspace `attend` needs (a pure host computation).
+    public static func workspaceBytes(_ call: Call) throws -> Int {
+        try call.withArgs { a in
+            let n = ltx_gemma_attn_workspace_bytes(&a)
+            guard n > 0 else {
+                throw HIPAttention.Failure.invalid(String(cString: ltx_attn_last_error()))
+            }
+            return Int(n)
+        }
+    }
+
+    /// Enqueue the call on `stream`. Inputs must stay alive until the stream passes it.
+    public static func attend(_ call: Call, workspace: UnsafeMutableRawPointer,
+                              workspaceBytes: Int, stream: UnsafeMutableRawPointer?) throws {
+        try call.withArgs { a in
+            a.workspace = workspace
+            a.workspace_bytes = workspaceBytes
+            try HIPAttention.check(ltx_gemma_attn_fwd(&a, stream))
+        }
+    }
+}
+
 /// Device memory owned by Swift (freed with the object).
 public final class HIPBuffer {
     public let pointer: UnsafeMutableRawPointer
@@ -194,15 +283,48 @@ public final class HIPBuffer {
     deinit { _ = cltx_free(pointer) }
 }
 
-/// Everything the `.hip` `AttentionPath` needs at run time, created explicitly by the
-/// caller for the device it selected (`HIPDevice.select`): one stream and a workspace that
-/// grows to the largest call seen. The reference runs its model on one worker task and does
-/// not share MLX across threads (`DistilledRenderer.swift:441-446`); this context follows
-/// the same rule, one per worker.
+/// Page-locked host memory owned by Swift (freed with the object): copies from and to it are
+/// asynchronous and need no staging copy by the runtime.
+public final class HIPHostBuffer {
+    public let pointer: UnsafeMutableRawPointer
+    public let bytes: Int
+
+    public init(bytes: Int) throws {
+        var p: UnsafeMutableRawPointer?
+        try HIPAttention.checkHIP(cltx_host_alloc(max(bytes, 256), &p), "host allocation")
+        pointer = p!
+        self.bytes = bytes
+    }
+
+    deinit { _ = cltx_host_free(pointer) }
+}
+
+/// Everything the `.hip` attention paths need at run time, created explicitly by the caller
+/// for the device it selected (`HIPDevice.select`): one stream, a workspace, and one pair of
+/// arenas -- page-locked host memory and device memory of the same size -- that hold a call's
+/// operands and result at the same offsets on both sides. All three grow to the largest call
+/// seen and are reused after that: a call allocates nothing once the context has seen a call
+/// as large. The reference runs its model on one worker task and does not share MLX across
+/// threads (`DistilledRenderer.swift:441-446`); a context follows the same rule, one per
+/// worker, and calls on it run one at a time.
 public final class HIPAttentionContext {
     public let ordinal: Int32
     public let stream: UnsafeMutableRawPointer
-    private var workspace: HIPBuffer?
+    private var workspaceBuffer: HIPBuffer?
+    private var deviceArena: HIPBuffer?
+    private var hostArena: HIPHostBuffer?
+
+    /// Offsets of one call's operands in the arenas, each 256-byte aligned.
+    public struct Layout {
+        public private(set) var bytes = 0
+        public init() {}
+        /// Reserve `count` bytes; returns their offset.
+        public mutating func place(_ count: Int) -> Int {
+            let offset = bytes
+            bytes = (offset + count + 255) / 256 * 256
+            return offset
+        }
+    }
 
     public init(ordinal: Int32) throws {
         try HIPAttention.checkHIP(cltx_set_device(ordinal), "select device \(ordinal)")
@@ -212,26 +334,53 @@ public final class HIPAttentionContext {
         self.stream = s!
     }
 
-    deinit { _ = cltx_stream_destroy(stream) }
+    deinit {
+        _ = cltx_stream_synchronize(stream)
+        _ = cltx_stream_destroy(stream)
+    }
 
     /// A workspace of at least `bytes` (the previous one when it is large enough).
     public func workspace(bytes: Int) throws -> HIPBuffer? {
         if bytes == 0 { return nil }
-        if let w = workspace, w.bytes >= bytes { return w }
+        if let w = workspaceBuffer, w.bytes >= bytes { return w }
         try synchronize()                  // the old buffer may still be in use on the stream
-        workspace = try HIPBuffer(bytes: bytes)
-        return workspace
+        workspaceBuffer = try HIPBuffer(bytes: bytes)
+        return workspaceBuffer
     }
 
-    public func upload(_ host: UnsafeRawBufferPointer) throws -> HIPBuffer {
-        let b = try HIPBuffer(bytes: host.count)
-        try HIPAttention.checkHIP(cltx_upload(b.pointer, host.baseAddress, host.count, stream),
-                                  "upload")
-        return b
+    /// The two arenas, at least `bytes` each: the host side to fill before `upload`, the
+    /// device side the call reads and writes. Grown (after the stream has drained) only when
+    /// a call needs more than any before it.
+    public func arenas(bytes: Int) throws
+        -> (host: UnsafeMutableRawPointer, device: UnsafeMutableRawPointer) {
+        if let h = hostArena, let d = deviceArena, h.bytes >= bytes, d.bytes >= bytes {
+            return (h.pointer, d.pointer)
+        }
+        try synchronize()
+        let size = max(bytes, (hostArena?.bytes ?? 0) * 5 / 4)
+        hostArena = nil
+        deviceArena = nil
+        hostArena = try HIPHostBuffer(bytes: size)
+        deviceArena = try HIPBuffer(bytes: size)
+        return (hostArena!.pointer, deviceArena!.pointer)
     }
 
-    public func download(_ buffer: HIPBuffer, into host: UnsafeMutableRawBufferPointer) throws {
-        try HIPAttention.checkHIP(cltx_download(host.baseAddress, buffer.pointer, host.count,
+    /// The host arena's first `bytes` to the device arena, asynchronously on the stream; the
+    /// host side stays untouched until `download` has synchronised.
+    public func upload(bytes: Int) throws {
+        guard let h = hostArena, let d = deviceArena, bytes <= h.bytes else {
+            throw HIPAttention.Failure.invalid("upload of \(bytes) bytes past the arenas")
+        }
+        try HIPAttention.checkHIP(cltx_upload(d.pointer, h.pointer, bytes, stream), "upload")
+    }
+
+    /// Bytes [offset, offset + bytes) of the device arena back to the same range of the host
+    /// arena, then wait for the stream: the result is readable at `host + offset`.
+    public func download(offset: Int, bytes: Int) throws {
+        guard let h = hostArena, let d = deviceArena, offset + bytes <= h.bytes else {
+            throw HIPAttention.Failure.invalid("download of \(bytes) bytes past the arenas")
+        }
+        try HIPAttention.checkHIP(cltx_download(h.pointer + offset, d.pointer + offset, bytes,
                                                 stream), "download")
         try synchronize()
     }
