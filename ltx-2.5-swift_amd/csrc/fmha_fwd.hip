@@ -697,16 +697,30 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineParams p) {
     const int hh = bh % p.H, b = bh / p.H;
     const int d = 4 * (tid % TPR);
     const int S = p.num_splits;
+    // Every split's (max, sum) and partial O are loaded before any is used, so the row waits
+    // for one round trip, not one per split (every range writes its partials, an empty one
+    // max -inf and zeros). The sums then run in split order, skipping empty ranges.
+    f32x2 ml[kMaxSplits];
+    f32x4 po[kMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) {
+        if (s < S) {
+            ml[s] = *(const f32x2 *)(p.part_ml + (s * rows + row) * 2);
+            po[s] = *(const f32x4 *)(p.part_o + (s * rows + row) * D + d);
+        }
+    }
     float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, p.part_ml[(s * rows + row) * 2]);
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s)
+        if (s < S) M = fmaxf(M, ml[s][0]);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     float den = 0.f;
-    for (int s = 0; s < S; ++s) {
-        const float ms = p.part_ml[(s * rows + row) * 2];
-        if (ms == -INFINITY) continue;
-        const float w = __builtin_amdgcn_exp2f(ms - M);
-        den += w * p.part_ml[(s * rows + row) * 2 + 1];
-        acc += w * *(const f32x4 *)(p.part_o + (s * rows + row) * D + d);
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) {
+        if (s >= S || ml[s][0] == -INFINITY) continue;
+        const float w = __builtin_amdgcn_exp2f(ml[s][0] - M);
+        den += w * ml[s][1];
+        acc += w * po[s];
     }
     const float inv = gate_factor(p.gate, p.g_bs, p.g_rs, p.g_hs, b, q, hh) / den;
     u32x2 w;
