@@ -156,11 +156,39 @@ struct GemmaAttnParams {
     // Key split: a query block's key blocks (32 keys each) run in ranges of `chunk` blocks,
     // at most `nch_max` per query block; with more than one, each range writes fp32 partials
     // (unnormalised O, then the row's max and sum) that gemma_combine_kernel merges. The grid
-    // is nch_max layers of B * Hq * query blocks.
+    // is nch_max layers of B * Hq * query blocks. Partials exist only for the ranges of query
+    // blocks with more than one: batch row b's start at row part_row0[b], head-major, each head
+    // holding part_chunks[b] ranges of `queries` rows, a query block's ranges after those of
+    // the earlier split blocks of its head (gemma_part_offset).
     int32_t chunk, nch_max;          // nch_max <= kGemmaMaxChunks
-    float *part_o;                   // [B * Hq * query blocks][nch_max][queries][D]
-    float *part_ml;                  // [B * Hq * query blocks][nch_max][queries][2]
+    float *part_o;                   // [rows][D]
+    float *part_ml;                  // [rows][2]
+    int64_t part_row0[kMaxBatch];
+    int32_t part_chunks[kMaxBatch];
 };
+
+// Key blocks (32 keys) [lo, hi] of the Gemma query block of nq queries from q0 in a batch row
+// whose keys below fv are left padding: causal, and within the window when one is set; a block
+// with rows inside the padding walks every key. Its range count, at `chunk` blocks per range.
+// Shared by the host's workspace layout and the kernels (constexpr: callable from both).
+constexpr int gemma_key_lo(int q0, int fv, int window) {
+    return q0 < fv ? 0 : (window > 0 && q0 - window + 1 > fv ? q0 - window + 1 : fv) / 32;
+}
+constexpr int gemma_key_hi(int T, int q0, int nq, int fv) {
+    return q0 < fv ? (T + 31) / 32 - 1 : ((q0 + nq - 1 < T - 1 ? q0 + nq - 1 : T - 1) / 32);
+}
+constexpr int gemma_ranges(int T, int window, int chunk, int q0, int nq, int fv) {
+    return (gemma_key_hi(T, q0, nq, fv) - gemma_key_lo(q0, fv, window) + chunk) / chunk;
+}
+// Ranges of the split query blocks before query block qblk (queries qwg each) of one head.
+constexpr int gemma_part_offset(int T, int window, int chunk, int qwg, int fv, int qblk) {
+    int off = 0;
+    for (int j = 0; j < qblk; ++j) {
+        const int n = gemma_ranges(T, window, chunk, j * qwg, qwg, fv);
+        if (n > 1) off += n;
+    }
+    return off;
+}
 
 // Host side: set the calling thread's error detail (ltx_attn_last_error) from a printf
 // format and its va_list, and return `s`. Defined in ltx_attn_abi.cpp, not exported.

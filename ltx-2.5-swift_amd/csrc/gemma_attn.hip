@@ -227,15 +227,7 @@ struct KeyBlocks {
 };
 __device__ __forceinline__ KeyBlocks gemma_key_blocks(const GemmaAttnParams &p, int q0, int nq,
                                                       int fv) {
-    const int nkb = (p.T + 31) / 32;
-    KeyBlocks r{0, nkb - 1};
-    if (q0 >= fv) {
-        r.hi = min(q0 + nq - 1, p.T - 1) / 32;
-        int lo = fv;
-        if (p.window > 0) lo = max(lo, q0 - p.window + 1);
-        r.lo = max(0, lo) / 32;
-    }
-    return r;
+    return KeyBlocks{gemma_key_lo(q0, fv, p.window), gemma_key_hi(p.T, q0, nq, fv)};
 }
 
 // The fast pass keeps each row's max from its first block with an allowed key; a later block
@@ -454,7 +446,10 @@ void gemma_attn_kernel(const GemmaAttnParams p) {
     const float lt = l + xlane32(l);
     if (nch > 1) {
         // one key range of several: unnormalised O, then (max, sum) per row, for the combine
-        const int64_t row = ((int64_t)(bh * nqb + qblk) * p.nch_max + chunk) * QWG + 32 * grp + r;
+        const int64_t row = p.part_row0[b] +
+                            ((int64_t)h * p.part_chunks[b] +
+                             gemma_part_offset(T, p.window, p.chunk, QWG, fv, qblk) + chunk) * QWG +
+                            32 * grp + r;
         float *po = p.part_o + row * D + 256 * half;
 #pragma unroll
         for (int db = 0; db < NDW; ++db)
@@ -509,7 +504,10 @@ __global__ __launch_bounds__(256) void gemma_combine_kernel(const GemmaAttnParam
     const int c4 = (int)threadIdx.x % U;
     const int q = q0 + rr;
     if (q >= p.T) return;
-    const int64_t row0 = ((int64_t)blk * p.nch_max) * QWG + rr;
+    const int64_t row0 = p.part_row0[b] +
+                         ((int64_t)h * p.part_chunks[b] +
+                          gemma_part_offset(p.T, p.window, p.chunk, QWG, p.first_valid[b], qblk)) *
+                             QWG + rr;
     float mc[kGemmaMaxChunks], lc[kGemmaMaxChunks];
     f32x4 oc[kGemmaMaxChunks];
     float mx = -INFINITY;

@@ -369,6 +369,8 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl,
 struct GemmaPlan {
     size_t off_q = 0, off_qlo = 0, off_k = 0, off_v = 0, off_po = 0, off_pml = 0, bytes = 0;
     int32_t chunk = 0, nch_max = 1;
+    int64_t part_row0[ltx::kMaxBatch] = {};   // first partial row of each batch row
+    int32_t part_chunks[ltx::kMaxBatch] = {}; // split ranges per head of each batch row
 };
 
 // Key blocks (32 keys) per range of a Gemma query block. The latest query blocks of a causal
@@ -437,7 +439,20 @@ ltx_attn_status gemma_plan(const ltx_gemma_attn_args *a, GemmaPlan *pl) {
     pl->chunk = gemma_chunk_blocks(a->T);
     pl->nch_max = (nkb + pl->chunk - 1) / pl->chunk;
     if (pl->nch_max > 1) {
-        const size_t rows = (size_t)a->B * a->Hq * nqb * pl->nch_max * qwg;
+        // partials only for the ranges of query blocks that have more than one, laid out per
+        // batch row (its padding decides which blocks split), head-major
+        size_t rows = 0;
+        for (int b = 0; b < a->B; ++b) {
+            const int fv = a->first_valid ? a->first_valid[b] : 0;
+            int chunks = 0;
+            for (int j = 0; j < nqb; ++j) {
+                const int n = ltx::gemma_ranges(a->T, a->window, pl->chunk, j * qwg, qwg, fv);
+                if (n > 1) chunks += n;
+            }
+            pl->part_row0[b] = (int64_t)rows;
+            pl->part_chunks[b] = chunks;
+            rows += (size_t)a->Hq * chunks * qwg;
+        }
         pl->off_po = pl->bytes;
         pl->off_pml = pl->off_po + align_up(rows * D * 4, 256);
         pl->bytes = pl->off_pml + align_up(rows * 2 * 4, 256);
@@ -689,6 +704,10 @@ ltx_attn_status ltx_gemma_attn_fwd(const ltx_gemma_attn_args *a, void *stream) {
     ap.nch_max = pl.nch_max;
     ap.part_o = (float *)(ws + pl.off_po);
     ap.part_ml = (float *)(ws + pl.off_pml);
+    for (int b = 0; b < a->B; ++b) {
+        ap.part_row0[b] = pl.part_row0[b];
+        ap.part_chunks[b] = pl.part_chunks[b];
+    }
     if (int e = ltx::launch_gemma_attn(ap, a->D, stream))
         return fail(LTX_ATTN_EHIP, "gemma attention launch: %s", hipGetErrorString((hipError_t)e));
     return LTX_ATTN_OK;

@@ -528,6 +528,46 @@ def test_gemma_rope_tables_match_oracle():
             assert np.all(cos[:, 64:] == 1.0) and np.all(sin[:, 64:] == 0.0)
 
 
+def test_gemma_partials_at_a_long_prompt():
+    """Split partials only for the query blocks that split, per batch row: a full layer (D 512,
+    64-query workgroups, one KV head) at 8192 tokens runs its 256 key blocks in ranges of 32;
+    query block j walks 2j + 2 key blocks, so blocks 0-15 run one range and 16-127 run 2..8
+    (16 blocks each): 16 * (2 + ... + 8) = 560 ranges per head, 16 heads, 64 rows each, fp32 O
+    (512) and (max, sum) per row: 1.18 GB (every block sized for 8 ranges would be 2.16 GB).
+    A second batch row padded on the left by 4000 tokens walks every key in its first 63 blocks
+    (8 ranges each) and the causal range after that."""
+    lib = L.load_library()
+    T, D, Hq = 8192, 512, 16
+    a = L.GemmaArgs()
+    a.B, a.T, a.Hq, a.Hkv, a.D = 1, T, Hq, 1, D
+    a.q = a.k = a.v = FAKE
+    a.q_bs, a.q_rs = T * Hq * D, Hq * D
+    a.k_bs = a.v_bs = T * D
+    a.k_rs = a.v_rs = D
+    a.q_norm_w = a.k_norm_w = FAKE
+    a.eps, a.scale = 1e-6, 1.0
+    a.cos = a.sin = FAKE
+    a.out = FAKE
+    a.o_bs, a.o_rs = T * Hq * D, Hq * D
+    prep = 2 * T * D * (2 * Hq + 1 + 1)                # q' hi + lo, k', v'^T
+    rows = Hq * 16 * sum(range(2, 9)) * 64
+    need = lib.ltx_gemma_attn_workspace_bytes(ctypes.byref(a))
+    assert need == prep + rows * D * 4 + rows * 2 * 4
+    assert 1.17e9 < need - prep < 1.19e9
+    # B = 2, the second row left-padded by 4000 tokens: its blocks 0-62 (rows below 4032)
+    # hold padding rows and walk all 256 key blocks (8 ranges); block 63 onward starts at key
+    # block 4000 // 32 = 125 and ends at 2j + 1
+    fv = (ctypes.c_int32 * 2)(0, 4000)
+    a.B = 2
+    a.q_bs, a.k_bs, a.v_bs, a.o_bs = T * Hq * D, T * D, T * D, T * Hq * D
+    a.first_valid = ctypes.cast(fv, ctypes.POINTER(ctypes.c_int32))
+    second = 63 * 8 + sum(n for n in ((2 * j + 1 - 125 + 32) // 32 for j in range(63, 128))
+                          if n > 1)
+    rows2 = rows + Hq * second * 64
+    assert lib.ltx_gemma_attn_workspace_bytes(ctypes.byref(a)) == \
+        2 * prep + rows2 * D * 4 + rows2 * 2 * 4
+
+
 def test_gemma_attention_rejects_bad_arguments():
     lib = L.load_library()
 
@@ -556,8 +596,9 @@ def test_gemma_attention_rejects_bad_arguments():
     a = args()
     need = lib.ltx_gemma_attn_workspace_bytes(ctypes.byref(a))
     # q' (hi, lo), k', v'^T, then the key split's partials: 128-query workgroups, whose 4..32
-    # key blocks run in ranges of at most 16 (two per query block): fp32 O and (max, sum) rows
-    rows = 1 * 16 * 8 * 2 * 128
+    # key blocks run in ranges of at most 16; query blocks 4-7 (20..32 blocks) have two ranges,
+    # 0-3 one (no partials): 16 heads x 4 blocks x 2 ranges x 128 rows of fp32 O and (max, sum)
+    rows = 16 * 4 * 2 * 128
     assert need == 2 * 1024 * 256 * (2 * 16 + 8 + 8) + rows * 256 * 4 + rows * 2 * 4
     assert status(a)[0] == L.EWORKSPACE
     assert status(args(D=128))[0] == L.EUNSUPPORTED
