@@ -350,7 +350,8 @@ typedef struct ltx_gemma_attn_args {
     size_t workspace_bytes;
 } ltx_gemma_attn_args;
 
-/* Workspace for the prepared q (two bf16 parts), k (normed, rotated) and v^T; 0 on bad args. */
+/* Workspace for the prepared q, k (normed, rotated) and v^T (fp16 MFMA operands) and the key
+ * split's partials; 0 on bad args. */
 size_t ltx_gemma_attn_workspace_bytes(const ltx_gemma_attn_args *a);
 
 /* Validate, then run asynchronously on `stream`: the per-head prologue, then the attention.

@@ -142,12 +142,12 @@ struct GemmaPrepParams {
     float eps;
     float q_factor;                  // scale * log2(e), folded into q'
     const float *cos, *sin;          // fp32 [T][D/2]
-    void *qp, *qp_lo, *kp, *vt;      // bf16 outputs (workspace); q' as hi + lo parts
+    void *qp, *kp, *vt;              // fp16 outputs (workspace)
 };
 constexpr int kGemmaMaxChunks = 8;  // key ranges per Gemma query block, at most
 
 struct GemmaAttnParams {
-    const void *qp, *qp_lo, *kp, *vt;
+    const void *qp, *kp, *vt;
     float *out;                      // fp32 [B][T][Hq*D], element strides below
     int64_t o_bs, o_rs;
     int32_t B, T, Hq, Hkv;
@@ -159,7 +159,7 @@ struct GemmaAttnParams {
     // is nch_max layers of B * Hq * query blocks. Partials exist only for the ranges of query
     // blocks with more than one: batch row b's start at row part_row0[b], head-major, each head
     // holding part_chunks[b] ranges of `queries` rows, a query block's ranges after those of
-    // the earlier split blocks of its head (gemma_part_offset).
+    // the earlier split blocks of its head.
     int32_t chunk, nch_max;          // nch_max <= kGemmaMaxChunks
     float *part_o;                   // [rows][D]
     float *part_ml;                  // [rows][2]
@@ -177,17 +177,14 @@ constexpr int gemma_key_lo(int q0, int fv, int window) {
 constexpr int gemma_key_hi(int T, int q0, int nq, int fv) {
     return q0 < fv ? (T + 31) / 32 - 1 : ((q0 + nq - 1 < T - 1 ? q0 + nq - 1 : T - 1) / 32);
 }
+// (The count is at most kGemmaMaxChunks -- the host sizes `chunk` so -- and is taken by
+// comparisons rather than an integer division, which the kernels would expand into a long
+// sequence per call.)
 constexpr int gemma_ranges(int T, int window, int chunk, int q0, int nq, int fv) {
-    return (gemma_key_hi(T, q0, nq, fv) - gemma_key_lo(q0, fv, window) + chunk) / chunk;
-}
-// Ranges of the split query blocks before query block qblk (queries qwg each) of one head.
-constexpr int gemma_part_offset(int T, int window, int chunk, int qwg, int fv, int qblk) {
-    int off = 0;
-    for (int j = 0; j < qblk; ++j) {
-        const int n = gemma_ranges(T, window, chunk, j * qwg, qwg, fv);
-        if (n > 1) off += n;
-    }
-    return off;
+    const int x = gemma_key_hi(T, q0, nq, fv) - gemma_key_lo(q0, fv, window) + chunk;
+    int n = 0;
+    for (int k = 1; k <= kGemmaMaxChunks; ++k) n += x >= k * chunk ? 1 : 0;
+    return n;
 }
 
 // Host side: set the calling thread's error detail (ltx_attn_last_error) from a printf

@@ -8,36 +8,37 @@
 //                       RoPE with the fp32 tables, q scaled by scale*log2(e). Rounding points:
 //                       the reference's norm returns the input dtype (GemmaTextEncoder.swift
 //                       :114), so its normed q and k are bf16, and its fp32 RoPE leaves both
-//                       fp32. Here q is normed, rotated and scaled in fp32 without that
-//                       rounding and kept as two bf16 parts (hi + lo, ~16 significant bits)
-//                       [B][Hq][T][D]; k is rotated from its unrounded normed value and
-//                       rounded once, after the rotation, to the single bf16 part the products
-//                       take -- one rounding, as the reference's, at a different point. Both
-//                       differences bring the result nearer the exact one than the
+//                       fp32. Here q and k are normed and rotated in fp32 without that
+//                       rounding and rounded once, after the rotation, to fp16 (11
+//                       significant bits, against bf16's 8): q' [B][Hq][T][D] and k' are the
+//                       fp16 operands of the products, far inside fp16's range: the RMS norm
+//                       bounds a channel, and the rotation a channel pair, by sqrt(D) times
+//                       the weight (times log2(e) for q'). The single rounding, finer than the
+//                       reference's, brings the result nearer the exact one than the
 //                       reference's own arithmetic (its rounded normed q alone moves the
 //                       1024-token layers' max-abs error to about 2e-2).
 //                       k' is stored in MFMA operand order: per (batch row, KV head, 32-key
 //                       block) D/16 units of 1 KB, lane r + 32g of unit c holding channels
 //                       16c + 8g .. +7 of key r.
-//   (same launch)       v with the weightless per-head norm, transposed through an LDS tile of
-//                       one 32-key block into operand order: per key half hf and 32-channel
-//                       block cb one 1 KB unit, lane r + 32g holding channel 32cb + r at keys
-//                       16hf + 4g + {0..3, 8..11}. Keys past T are zeros in both layouts, and
+//   (same launch)       v with the weightless per-head norm, in fp16, transposed through an
+//                       LDS tile of one 32-key block into operand order: per key half hf and
+//                       32-channel block cb one 1 KB unit, lane r + 32g holding channel
+//                       32cb + r at keys 16hf + 4g + {0..3, 8..11}. Keys past T are zeros in both layouts, and
 //                       a key block's k' and v'^T are each one contiguous run of units.
 //   gemma_attn_kernel   a wave owns 32 queries over 256 channels (D = 256: the whole head;
 //                       D = 512: half of it, its partner wave the other half), four waves per
 //                       workgroup: 128 queries at D = 256, 64 at D = 512. The key blocks of
 //                       the workgroup's range are copied HBM -> LDS by the buffer-load-to-LDS
 //                       path into a ring (4 blocks at D = 256, 2 at D = 512) and read from LDS
-//                       by every wave. Per key block: S^T = K.Q'^T over the hi and lo parts of
-//                       q' (inline products with S in VGPRs and Q' in AGPRs; at D = 512 the two
-//                       halves' partial sums are exchanged through LDS and added in a fixed
-//                       order), the mask, exp2 with each row's max fixed at its first block with
-//                       an allowed key, and O^T += V^T.P^T with P as two bf16 parts (the
-//                       reference's weights are fp32). A block whose weights would pass 2^64
-//                       sends the workgroup to an exact pass (online max with rescaling) over
-//                       its range. O is written in fp32, the dtype the reference's explicit
-//                       path returns.
+//                       by every wave. Per key block: S^T = K.Q'^T in fp16 products (inline,
+//                       S in VGPRs and Q' in AGPRs; at D = 512 the two halves' partial sums are
+//                       exchanged through LDS and added in a fixed order), the mask, exp2 with
+//                       each row's max fixed at its first block with an allowed key, and
+//                       O^T += V^T.P^T with v' and P in fp16 (the reference's weights are
+//                       fp32; with the max fixed a weight stays below 2^kGemmaBound). A block
+//                       whose weights would pass 2^kGemmaBound sends the workgroup to an exact
+//                       pass (online max with rescaling) over its range. O is written in
+//                       fp32, the dtype the reference's explicit path returns.
 //   gemma_combine_kernel  the long query blocks' keys run as ranges of at most 16 blocks on
 //                       separate workgroups, each writing unnormalised O and (max, sum); the
 //                       merge rescales and adds them.
@@ -97,9 +98,9 @@ __device__ __forceinline__ void gemma_prep_rows(const GemmaPrepParams &p, int wg
         // first half: x1 c - x2 s; second half: x2 c + x1 s
         y[e] = (first ? x[e] * c - other * s : x[e] * c + other * s) * f;
     }
-    // q as two bf16 parts (hi + lo carries ~16 significant bits into the products); k as one
-    auto put = [&](bf16 *dst, const float (&z)[E]) __attribute__((always_inline)) {
-        *(u32x4 *)dst = pack8(z);
+    // q' and k' as fp16 (11 significant bits, rounded once, to nearest)
+    auto put = [&](_Float16 *dst, const float (&z)[E]) __attribute__((always_inline)) {
+        *(u32x4 *)dst = pack8_f16(z);
     };
     if (kind == 1) {
         // k' in operand order: 32-key block t/32, 16-channel chunk c, lane (t%32) + 32g holds
@@ -108,14 +109,10 @@ __device__ __forceinline__ void gemma_prep_rows(const GemmaPrepParams &p, int wg
         const int nkb = (p.T + 31) / 32;
         const int64_t off = ((((int64_t)b * p.Hkv + h) * nkb + (t >> 5)) * (D / 16) + c) * 512 +
                             ((t & 31) + 32 * g) * 8 + (ch & 7);
-        put((bf16 *)p.kp + off, y);
+        put((_Float16 *)p.kp + off, y);
     } else {
         const int64_t off = (((int64_t)b * p.Hq + h) * p.T + t) * D + lane * E;
-        put((bf16 *)p.qp + off, y);
-        float lo[E];
-#pragma unroll
-        for (int e = 0; e < E; ++e) lo[e] = y[e] - (float)(bf16)y[e];
-        put((bf16 *)p.qp_lo + off, lo);
+        put((_Float16 *)p.qp + off, y);
     }
 }
 
@@ -125,7 +122,7 @@ __device__ __forceinline__ void gemma_prep_rows(const GemmaPrepParams &p, int wg
 // of the v part of the launch.
 template <int D>
 __device__ __forceinline__ void gemma_vt_block(const GemmaPrepParams &p, int wg,
-                                               bf16 (&tile)[32][D + 8]) {
+                                               _Float16 (&tile)[32][D + 8]) {
     constexpr int E = D / 64;
     constexpr int TT = 32;                          // tokens per workgroup: one key block
     constexpr int RW = TT / 4;                      // rows per wave
@@ -161,14 +158,14 @@ __device__ __forceinline__ void gemma_vt_block(const GemmaPrepParams &p, int wg,
         for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
         const float rs = powf(ss / (float)D + p.eps, -0.5f);
 #pragma unroll
-        for (int e = 0; e < E; ++e) tile[wave * RW + j][lane * E + e] = (bf16)(x[j][e] * rs);
+        for (int e = 0; e < E; ++e) tile[wave * RW + j][lane * E + e] = (_Float16)(x[j][e] * rs);
     }
     __syncthreads();
     // Operand units of the block: per key half hf and 32-channel block cb one 1 KB unit whose
     // lane r + 32g holds channel 32cb + r at keys 32kb + 16hf + 4g + {0..3, 8..11}. Keys past T
     // are written as zeros (their weights are 0, and 0 * 0 keeps the products finite); the
     // last block's k' rows past T are zeroed too.
-    bf16 *vbase = (bf16 *)p.vt + (((int64_t)b * p.Hkv + h) * nkb + kb) * (D * 32);
+    _Float16 *vbase = (_Float16 *)p.vt + (((int64_t)b * p.Hkv + h) * nkb + kb) * (D * 32);
     for (int u = threadIdx.x; u < 2 * (D / 32) * 64; u += 256) {
         const int l = u & 63, rest = u >> 6;
         const int cb = rest % (D / 32), hf = rest / (D / 32);
@@ -179,10 +176,10 @@ __device__ __forceinline__ void gemma_vt_block(const GemmaPrepParams &p, int wg,
             const int tl = 16 * hf + 4 * g + (e & 3) + 8 * (e >> 2);
             f[e] = t0 + tl < p.T ? (float)tile[tl][32 * cb + r] : 0.f;
         }
-        *(u32x4 *)(vbase + ((int64_t)hf * (D / 32) + cb) * 512 + l * 8) = pack8(f);
+        *(u32x4 *)(vbase + ((int64_t)hf * (D / 32) + cb) * 512 + l * 8) = pack8_f16(f);
     }
     if ((p.T & 31) && kb == nkb - 1) {
-        bf16 *kbase = (bf16 *)p.kp + (((int64_t)b * p.Hkv + h) * nkb + kb) * (D * 32);
+        _Float16 *kbase = (_Float16 *)p.kp + (((int64_t)b * p.Hkv + h) * nkb + kb) * (D * 32);
         for (int u = threadIdx.x; u < (D / 16) * 64; u += 256) {
             const int l = u & 63;
             if (t0 + (l & 31) >= p.T) *(u32x4 *)(kbase + u * 8) = u32x4{0, 0, 0, 0};
@@ -194,7 +191,7 @@ __device__ __forceinline__ void gemma_vt_block(const GemmaPrepParams &p, int wg,
 // disjoint parts of k': rows below T, and the zeroed rows past T of the last block).
 template <int D>
 __global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p, int row_wgs) {
-    __shared__ __attribute__((aligned(16))) bf16 tile[32][D + 8];
+    __shared__ __attribute__((aligned(16))) _Float16 tile[32][D + 8];
     const int wg = blockIdx.x;
     if (wg < row_wgs) gemma_prep_rows<D>(p, wg);
     else gemma_vt_block<D>(p, wg - row_wgs, tile);
@@ -233,7 +230,27 @@ __device__ __forceinline__ KeyBlocks gemma_key_blocks(const GemmaAttnParams &p, 
 // The fast pass keeps each row's max from its first block with an allowed key; a later block
 // whose weights would pass 2^kGemmaBound (log2 units over that max) sends the workgroup to
 // the exact pass, which rescales O and l whenever a row's max grows.
-constexpr float kGemmaBound = 64.0f;
+constexpr float kGemmaBound = 15.0f;   // the fp16 weights stay below 65504
+
+// Partial rows before query block qblk's within its head: the key ranges of the earlier query
+// blocks that split (more than one range). Spread over the wave: lane j counts block j (j + 64,
+// ...), and four ballots add the counts (at most kGemmaMaxChunks = 8: four bits), so the wave
+// spends a few vector instructions instead of a scalar loop over every earlier block, which the
+// CU's one scalar unit would run for each of its waves in turn. Every lane must be active; the
+// result is uniform.
+__device__ __forceinline__ int gemma_part_offset(int T, int window, int chunk, int qwg, int fv,
+                                                 int qblk) {
+    const int lane = (int)threadIdx.x & 63;
+    int off = 0;
+    for (int j0 = 0; j0 < qblk; j0 += 64) {
+        const int j = j0 + lane;
+        int n = j < qblk ? gemma_ranges(T, window, chunk, j * qwg, qwg, fv) : 0;
+        if (n < 2) n = 0;
+#pragma unroll
+        for (int bit = 0; bit < 4; ++bit) off += __popcll(__ballot((n >> bit) & 1)) << bit;
+    }
+    return off;
+}
 
 template <int D>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
@@ -263,7 +280,7 @@ void gemma_attn_kernel(const GemmaAttnParams p) {
     const int q0 = qblk * QWG;
     const int fv = p.first_valid[b];
     const KeyBlocks kr = gemma_key_blocks(p, q0, QWG, fv);
-    const int nch = (kr.hi - kr.lo + p.chunk) / p.chunk;
+    const int nch = gemma_ranges(T, p.window, p.chunk, q0, QWG, fv);
     if (chunk >= nch) return;                        // this block has fewer key ranges
     const int kb_lo = kr.lo + chunk * p.chunk;
     const int kb_hi = min(kb_lo + p.chunk - 1, kr.hi);
@@ -295,15 +312,13 @@ void gemma_attn_kernel(const GemmaAttnParams p) {
     const int q = q0 + 32 * grp + r;                 // this lane's query row
     const int qr = min(q, T - 1);
     const int64_t qoff = (((int64_t)b * p.Hq + h) * T + qr) * D + 256 * half + 8 * g;
-    bf16x8 qh[NCW], ql[NCW];
+    f16x8 qh[NCW];
 #pragma unroll
-    for (int c = 0; c < NCW; ++c) {
-        qh[c] = __builtin_bit_cast(bf16x8, ldg16((const bf16 *)p.qp + qoff + 16 * c));
-        ql[c] = __builtin_bit_cast(bf16x8, ldg16((const bf16 *)p.qp_lo + qoff + 16 * c));
-    }
+    for (int c = 0; c < NCW; ++c)
+        qh[c] = __builtin_bit_cast(f16x8, ldg16((const _Float16 *)p.qp + qoff + 16 * c));
     // Q' is only an MFMA operand: home it in AGPRs, leaving the VGPRs to S, P and operands
 #pragma unroll
-    for (int c = 0; c < NCW; ++c) asm volatile("" : "+a"(qh[c]), "+a"(ql[c]));
+    for (int c = 0; c < NCW; ++c) asm volatile("" : "+a"(qh[c]));
     // The row's allowed keys as one range [k_lo, k_hi]: all keys for a row inside the left
     // padding, else causal (k <= q), past the padding (k >= fv) and inside the window
     // (q - k < window); k_hi <= T - 1 also masks the keys past T of the last block.
@@ -341,24 +356,18 @@ void gemma_attn_kernel(const GemmaAttnParams p) {
             const char *Ks = smem + (i % NS) * G::BLOCK;
             const char *Vs = Ks + G::KBYTES;
             const int kb = kb_lo + i;
-            // S^T over this wave's channels: the hi and lo parts of q' in two interleaved
-            // chains, so consecutive products are independent and the matrix cores never wait
-            // for a result (inline products with S in VGPRs and Q' in AGPRs, mfma_s.hpp)
-            f32x16 sh, sl;
+            // S^T over this wave's channels: one chain of inline products with S in VGPRs and
+            // Q' in AGPRs (mfma_s.hpp); a product whose SrcC is the previous result issues
+            // without waiting for it
+            f32x16 s;
 #pragma unroll
             for (int c = 0; c < NCW; ++c) {
-                const bf16x8 a = *(const __attribute__((address_space(3))) bf16x8 *)(
+                const f16x8 a = *(const __attribute__((address_space(3))) f16x8 *)(
                     (lds_void *)(Ks + (half * NCW + c) * 1024 + lane * 16));
-                if (c == 0) {
-                    sh = mfma_s_first(a, qh[0], zero);
-                    sl = mfma_s_first(a, ql[0], zero);
-                } else {
-                    mfma_s_next(sh, a, qh[c]);
-                    mfma_s_next(sl, a, ql[c]);
-                }
+                if (c == 0) s = mfma_s_first(a, qh[0], zero);
+                else mfma_s_next(s, a, qh[c]);
             }
-            s_ready(sh, sl, zero, zero);
-            f32x16 s = sh + sl;
+            s_ready(s, zero);
             if constexpr (SPLIT > 1) {
                 // the partner wave holds the other half of the channels: exchange the partial
                 // sums and add them in a fixed order, so both waves hold the same S
@@ -399,13 +408,13 @@ void gemma_attn_kernel(const GemmaAttnParams p) {
                 if (m == -INFINITY) m = mx;              // the row's first allowed keys
                 overflow |= mx > m + kGemmaBound;
             }
-            // fp32 weights, their fp32 row sums, and P as two bf16 parts for P.V (the
+            // fp32 weights, their fp32 row sums, and P in fp16 for P.V (11 significant bits; the
             // reference's explicit path multiplies fp32 weights); a row with no allowed key
             // so far has none
-            u32x4 wh[2], wl[2];
+            u32x4 wh[2];
             float ts = 0.f;
             if (m == -INFINITY) {
-                wh[0] = wh[1] = wl[0] = wl[1] = u32x4{0, 0, 0, 0};
+                wh[0] = wh[1] = u32x4{0, 0, 0, 0};
             } else {
 #pragma unroll
                 for (int hf = 0; hf < 2; ++hf)
@@ -414,27 +423,22 @@ void gemma_attn_kernel(const GemmaAttnParams p) {
                         const float x0 = __builtin_amdgcn_exp2f(s[8 * hf + 2 * e] - m);
                         const float x1 = __builtin_amdgcn_exp2f(s[8 * hf + 2 * e + 1] - m);
                         ts += x0 + x1;
-                        const uint32_t hi = pack_bf2_opaque(x0, x1);
-                        wh[hf][e] = hi;
-                        wl[hf][e] = pack_bf2(x0 - bf_lo(hi), x1 - bf_hi(hi));
+                        wh[hf][e] = pack_f16x2(x0, x1);
                     }
             }
             l += ts;
             // O^T += V^T.P^T for this wave's channels; consecutive products update different
-            // accumulators (the hi parts of a key half over all channel blocks, then the lo)
+            // accumulators (a key half over all channel blocks)
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
-                bf16x8 va[NDW];
+                f16x8 va[NDW];
 #pragma unroll
                 for (int db = 0; db < NDW; ++db)
-                    va[db] = *(const __attribute__((address_space(3))) bf16x8 *)(
+                    va[db] = *(const __attribute__((address_space(3))) f16x8 *)(
                         (lds_void *)(Vs + (hf * (D / 32) + half * NDW + db) * 1024 + lane * 16));
 #pragma unroll
                 for (int db = 0; db < NDW; ++db)
-                    o[db] = mfma32(va[db], __builtin_bit_cast(bf16x8, wh[hf]), o[db]);
-#pragma unroll
-                for (int db = 0; db < NDW; ++db)
-                    o[db] = mfma32(va[db], __builtin_bit_cast(bf16x8, wl[hf]), o[db]);
+                    o[db] = mfma32(va[db], __builtin_bit_cast(f16x8, wh[hf]), o[db]);
             }
         }
     };
@@ -483,60 +487,88 @@ void gemma_attn_kernel(const GemmaAttnParams p) {
 
 // Merge of a query block's key ranges: O = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c over
 // its ranges c (M the largest max; a range in which a row allows no key has m = -inf and adds
-// nothing), written in fp32. A thread per 4 channels of a row, 256 / (D / 4) rows per
-// workgroup, all of one query block (blocks with one range wrote their output themselves).
+// nothing), written in fp32. A thread per 4 channels of kCombineRows rows (RPW rows apart);
+// the workgroup's rows all belong to one query block (blocks with one range wrote their
+// output themselves). The loads of a pass -- N ranges of `rows` rows, about 48 registers --
+// are all issued before the first use: the merge is a chain of dependent loads otherwise, and
+// several rows per thread keep the workgroups few enough that the launch runs in one round.
+constexpr int kCombineRows = 4;
+
+template <int D, int N>
+__device__ __forceinline__ void gemma_merge_rows(const GemmaAttnParams &p, int64_t row0, int ch,
+                                                 int q, float *out) {
+    constexpr int QWG = GemmaTile<D>::QWG;
+    constexpr int RPW = 256 / (D / 4);
+    constexpr int PASS = N <= 2 ? kCombineRows : N <= 4 ? kCombineRows / 2 : 1;
+#pragma unroll
+    for (int g0 = 0; g0 < kCombineRows; g0 += PASS) {
+        f32x2 ml[PASS][N];
+        f32x4 oc[PASS][N];
+#pragma unroll
+        for (int r = 0; r < PASS; ++r)
+#pragma unroll
+            for (int c = 0; c < N; ++c) {
+                const int64_t row = row0 + (int64_t)(g0 + r) * RPW + (int64_t)c * QWG;
+                ml[r][c] = *(const f32x2 *)(p.part_ml + row * 2);
+                oc[r][c] = *(const f32x4 *)(p.part_o + row * D + ch);
+            }
+#pragma unroll
+        for (int r = 0; r < PASS; ++r) {
+            if (q + (g0 + r) * RPW >= p.T) continue;   // rows past T: partials, no output
+            float mx = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < N; ++c) mx = fmaxf(mx, ml[r][c][0]);
+            float lsum = 0.f;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < N; ++c) {
+                const float m = ml[r][c][0];
+                const float wgt = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mx);
+                lsum += wgt * ml[r][c][1];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[e] += wgt * oc[r][c][e];
+            }
+            const float inv = 1.0f / lsum;
+            f32x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = acc[e] * inv;
+            *(f32x4 *)(out + (int64_t)(g0 + r) * RPW * p.o_rs) = w;
+        }
+    }
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void gemma_combine_kernel(const GemmaAttnParams p) {
     constexpr int QWG = GemmaTile<D>::QWG;
     constexpr int U = D / 4;                        // threads per row
-    constexpr int RPW = 256 / U;                    // rows per workgroup
+    constexpr int RPW = 256 / U;                    // rows per pass of the workgroup
+    constexpr int WG_PER_QB = QWG / (RPW * kCombineRows);
+    static_assert(WG_PER_QB * RPW * kCombineRows == QWG, "a query block's rows split evenly");
     const int nqb = (p.T + QWG - 1) / QWG;
-    const int wg_per_qb = QWG / RPW;
-    const int blk = (int)blockIdx.x / wg_per_qb;    // (batch row, head, query block)
+    const int blk = (int)blockIdx.x / WG_PER_QB;    // (batch row, head, query block)
     const int qblk = blk % nqb;
     const int bh = blk / nqb;
     const int h = bh % p.Hq, b = bh / p.Hq;
     const int q0 = qblk * QWG;
-    const KeyBlocks kr = gemma_key_blocks(p, q0, QWG, p.first_valid[b]);
-    const int nch = (kr.hi - kr.lo + p.chunk) / p.chunk;
+    const int nch = gemma_ranges(p.T, p.window, p.chunk, q0, QWG, p.first_valid[b]);
     if (nch <= 1) return;
-    const int rr = ((int)blockIdx.x % wg_per_qb) * RPW + (int)threadIdx.x / U;
+    const int off = gemma_part_offset(p.T, p.window, p.chunk, QWG, p.first_valid[b], qblk);
+    const int rr = ((int)blockIdx.x % WG_PER_QB) * RPW * kCombineRows + (int)threadIdx.x / U;
     const int c4 = (int)threadIdx.x % U;
     const int q = q0 + rr;
-    if (q >= p.T) return;
-    const int64_t row0 = p.part_row0[b] +
-                         ((int64_t)h * p.part_chunks[b] +
-                          gemma_part_offset(p.T, p.window, p.chunk, QWG, p.first_valid[b], qblk)) *
-                             QWG + rr;
-    float mc[kGemmaMaxChunks], lc[kGemmaMaxChunks];
-    f32x4 oc[kGemmaMaxChunks];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int c = 0; c < kGemmaMaxChunks; ++c) {
-        if (c < nch) {
-            const int64_t row = row0 + (int64_t)c * QWG;
-            mc[c] = p.part_ml[row * 2];
-            lc[c] = p.part_ml[row * 2 + 1];
-            oc[c] = *(const f32x4 *)(p.part_o + row * D + 4 * c4);
-            mx = fmaxf(mx, mc[c]);
-        }
+    const int64_t row0 = p.part_row0[b] + ((int64_t)h * p.part_chunks[b] + off) * QWG + rr;
+    // partial rows past T exist (a range writes all its block's rows) and are read, not merged
+    float *out = p.out + (int64_t)b * p.o_bs + (int64_t)q * p.o_rs + (int64_t)h * D + 4 * c4;
+    static_assert(kGemmaMaxChunks == 8, "one case per range count");
+    switch (nch) {
+    case 2: gemma_merge_rows<D, 2>(p, row0, 4 * c4, q, out); break;
+    case 3: gemma_merge_rows<D, 3>(p, row0, 4 * c4, q, out); break;
+    case 4: gemma_merge_rows<D, 4>(p, row0, 4 * c4, q, out); break;
+    case 5: gemma_merge_rows<D, 5>(p, row0, 4 * c4, q, out); break;
+    case 6: gemma_merge_rows<D, 6>(p, row0, 4 * c4, q, out); break;
+    case 7: gemma_merge_rows<D, 7>(p, row0, 4 * c4, q, out); break;
+    default: gemma_merge_rows<D, 8>(p, row0, 4 * c4, q, out); break;
     }
-    float lsum = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < kGemmaMaxChunks; ++c) {
-        if (c < nch) {
-            const float wgt = mc[c] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc[c] - mx);
-            lsum += wgt * lc[c];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] += wgt * oc[c][e];
-        }
-    }
-    const float inv = 1.0f / lsum;
-    f32x4 w;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) w[e] = acc[e] * inv;
-    *(f32x4 *)(p.out + (int64_t)b * p.o_bs + (int64_t)q * p.o_rs + (int64_t)h * D + 4 * c4) = w;
 }
 
 }  // namespace
@@ -563,7 +595,7 @@ int launch_gemma_attn(const GemmaAttnParams &p, int D, void *stream) {
     if (D == 512) hipLaunchKernelGGL(gemma_attn_kernel<512>, grid, block, 0, st, p);
     else hipLaunchKernelGGL(gemma_attn_kernel<256>, grid, block, 0, st, p);
     if (p.nch_max > 1) {
-        const dim3 cgrid((unsigned)(per_layer * qwg / (256 / (D / 4))));
+        const dim3 cgrid((unsigned)(per_layer * qwg / (256 / (D / 4) * kCombineRows)));
         if (D == 512) hipLaunchKernelGGL(gemma_combine_kernel<512>, cgrid, block, 0, st, p);
         else hipLaunchKernelGGL(gemma_combine_kernel<256>, cgrid, block, 0, st, p);
     }

@@ -367,7 +367,7 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl,
 // Gemma-4 text-encoder attention: validation and workspace layout.
 
 struct GemmaPlan {
-    size_t off_q = 0, off_qlo = 0, off_k = 0, off_v = 0, off_po = 0, off_pml = 0, bytes = 0;
+    size_t off_q = 0, off_k = 0, off_v = 0, off_po = 0, off_pml = 0, bytes = 0;
     int32_t chunk = 0, nch_max = 1;
     int64_t part_row0[ltx::kMaxBatch] = {};   // first partial row of each batch row
     int32_t part_chunks[ltx::kMaxBatch] = {}; // split ranges per head of each batch row
@@ -430,8 +430,7 @@ ltx_attn_status gemma_plan(const ltx_gemma_attn_args *a, GemmaPlan *pl) {
     // k' and v'^T are stored by whole 32-key blocks (operand order), the last one zero-padded
     const size_t kn = 2 * (size_t)a->B * a->Hkv * ((a->T + 31) / 32 * 32) * D;
     pl->off_q = 0;
-    pl->off_qlo = align_up(qn, 256);
-    pl->off_k = pl->off_qlo + align_up(qn, 256);
+    pl->off_k = align_up(qn, 256);
     pl->off_v = pl->off_k + align_up(kn, 256);
     pl->bytes = pl->off_v + align_up(kn, 256);
     const int qwg = ltx::gemma_queries_per_workgroup(a->D);
@@ -691,12 +690,12 @@ ltx_attn_status ltx_gemma_attn_fwd(const ltx_gemma_attn_args *a, void *stream) {
     pp.eps = a->eps;
     pp.q_factor = (float)((double)a->scale * 1.4426950408889634);
     pp.cos = a->cos; pp.sin = a->sin;
-    pp.qp = ws + pl.off_q; pp.qp_lo = ws + pl.off_qlo; pp.kp = ws + pl.off_k;
+    pp.qp = ws + pl.off_q; pp.kp = ws + pl.off_k;
     pp.vt = ws + pl.off_v;
     if (int e = ltx::launch_gemma_prep(pp, a->D, stream))
         return fail(LTX_ATTN_EHIP, "gemma prologue launch: %s", hipGetErrorString((hipError_t)e));
     ltx::GemmaAttnParams ap{};
-    ap.qp = pp.qp; ap.qp_lo = pp.qp_lo; ap.kp = pp.kp; ap.vt = pp.vt;
+    ap.qp = pp.qp; ap.kp = pp.kp; ap.vt = pp.vt;
     ap.out = a->out; ap.o_bs = a->o_bs; ap.o_rs = a->o_rs;
     ap.B = a->B; ap.T = a->T; ap.Hq = a->Hq; ap.Hkv = a->Hkv; ap.window = a->window;
     for (int b = 0; b < a->B; ++b) ap.first_valid[b] = a->first_valid ? a->first_valid[b] : 0;

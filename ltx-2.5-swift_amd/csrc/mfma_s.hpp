@@ -37,6 +37,21 @@ __device__ __forceinline__ void mfma_s_next(f32x16 &acc, bf16x8 a, bf16x8 b) {
     asm("; mfma_s %0 src %0\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
         : "+v"(acc) : "v"(a), "a"(b));
 }
+// The same statements over fp16 operands (v_mfma_f32_32x32x16_f16), and s_ready for a single
+// chain.
+__device__ __forceinline__ f32x16 mfma_s_first(f16x8 a, f16x8 b, const f32x16 &c) {
+    f32x16 d;
+    asm("; mfma_s %0 src %3\n\ts_nop 1\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %3"
+        : "=&v"(d) : "v"(a), "a"(b), "v"(c));
+    return d;
+}
+__device__ __forceinline__ void mfma_s_next(f32x16 &acc, f16x8 a, f16x8 b) {
+    asm("; mfma_s %0 src %0\n\tv_mfma_f32_32x32x16_f16 %0, %1, %2, %0"
+        : "+v"(acc) : "v"(a), "a"(b));
+}
+__device__ __forceinline__ void s_ready(f32x16 &x, const f32x16 &c0) {
+    asm volatile("; s_ready %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 3" : "+v"(x) : "v"(c0));
+}
 __device__ __forceinline__ void s_ready(f32x16 &x, f32x16 &y, const f32x16 &c0,
                                         const f32x16 &c1) {
     asm volatile("; s_ready %0 %1\n\ts_nop 7\n\ts_nop 7\n\ts_nop 3"

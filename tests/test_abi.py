@@ -549,7 +549,7 @@ def test_gemma_partials_at_a_long_prompt():
     a.cos = a.sin = FAKE
     a.out = FAKE
     a.o_bs, a.o_rs = T * Hq * D, Hq * D
-    prep = 2 * T * D * (2 * Hq + 1 + 1)                # q' hi + lo, k', v'^T
+    prep = 2 * T * D * (Hq + 1 + 1)                    # q', k', v'^T (fp16)
     rows = Hq * 16 * sum(range(2, 9)) * 64
     need = lib.ltx_gemma_attn_workspace_bytes(ctypes.byref(a))
     assert need == prep + rows * D * 4 + rows * 2 * 4
@@ -595,11 +595,11 @@ def test_gemma_attention_rejects_bad_arguments():
 
     a = args()
     need = lib.ltx_gemma_attn_workspace_bytes(ctypes.byref(a))
-    # q' (hi, lo), k', v'^T, then the key split's partials: 128-query workgroups, whose 4..32
+    # q', k', v'^T (fp16), then the key split's partials: 128-query workgroups, whose 4..32
     # key blocks run in ranges of at most 16; query blocks 4-7 (20..32 blocks) have two ranges,
     # 0-3 one (no partials): 16 heads x 4 blocks x 2 ranges x 128 rows of fp32 O and (max, sum)
     rows = 16 * 4 * 2 * 128
-    assert need == 2 * 1024 * 256 * (2 * 16 + 8 + 8) + rows * 256 * 4 + rows * 2 * 4
+    assert need == 2 * 1024 * 256 * (16 + 8 + 8) + rows * 256 * 4 + rows * 2 * 4
     assert status(a)[0] == L.EWORKSPACE
     assert status(args(D=128))[0] == L.EUNSUPPORTED
     assert status(args(Hkv=3))[0] == L.EINVAL

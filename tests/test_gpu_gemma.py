@@ -55,6 +55,8 @@ def _run(device, case):
     got = out.cpu().numpy()
     kw = dict(window=spec["window"], first_valid=fv)
     truth = O.gemma_attention(q, k, v, Hq, Hkv, wq, wk, cos, sin, mode="exact", **kw)
+    if case.get("absolute_only"):
+        return got, truth, None
     ref = O.gemma_attention(q, k, v, Hq, Hkv, wq, wk, cos, sin, mode="reference", **kw)
     return got, truth, ref
 
@@ -86,8 +88,15 @@ CASES = {
     "sliding_window700_T1600_pad200": dict(B=1, T=1600, kind="sliding", fv=[200], window=700,
                                            seed=0x5EED + 510),
     "full_T1600_pad200": dict(B=1, T=1600, kind="full", fv=[200], seed=0x5EED + 520),
+    # two rows that split differently (the second's padding leaves fewer key blocks): each
+    # row's partials sit at their own offset
+    "full_T1600_B2_pad0_900": dict(B=2, T=1600, kind="full", fv=[0, 900], seed=0x5EED + 550),
+    # 65 query blocks of 64: the split blocks before the last number more than a wave's 64
+    # lanes, so the partial offset is counted over two passes of the wave. The float64 truth
+    # only (the bound relative to the reference's arithmetic would double the oracle's time).
+    "full_T4160": dict(B=1, T=4160, kind="full", fv=[0], seed=0x5EED + 560, absolute_only=True),
     # k_norm weights 25x the checkpoint's: logits with a spread of ~70 (log2 units), so later
-    # key blocks pass a row's first-block max by more than 2^64 and the workgroups rerun their
+    # key blocks pass a row's first-block max by more than 2^15 and the workgroups rerun their
     # range with the exact online softmax. Logits that large amplify the inputs' bf16
     # rounding (the reference's own arithmetic is ~2e-2 off), so only the bound relative to
     # the reference's arithmetic applies.
@@ -103,10 +112,14 @@ def test_gemma_attention(device, name):
     _say(f"gemma {name}")
     got, truth, ref = _run(device, CASES[name])
     c = O.compare(got, truth)
-    r = O.compare(ref, truth)
-    _say(f"  relRMS {c['rel_rms']:.3e} maxAbs {c['max_abs']:.3e} "
-         f"(reference arithmetic relRMS {r['rel_rms']:.3e})")
+    if ref is None:
+        _say(f"  relRMS {c['rel_rms']:.3e} maxAbs {c['max_abs']:.3e}")
+    else:
+        r = O.compare(ref, truth)
+        _say(f"  relRMS {c['rel_rms']:.3e} maxAbs {c['max_abs']:.3e} "
+             f"(reference arithmetic relRMS {r['rel_rms']:.3e})")
     if not CASES[name].get("relative_only"):
         assert c["rel_rms"] <= 5e-3, c
         assert c["max_abs"] <= 2e-2, c
-    assert c["rel_rms"] <= max(r["rel_rms"], 2.5e-3) * 1.25, (c, r)
+    if ref is not None:
+        assert c["rel_rms"] <= max(r["rel_rms"], 2.5e-3) * 1.25, (c, r)
