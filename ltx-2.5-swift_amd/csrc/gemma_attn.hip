@@ -52,67 +52,100 @@ namespace {
 
 // ---- prologue ------------------------------------------------------------------------------
 // q/k rows: workgroup wg of the rows' part of the launch.
+// Rows per wave of the q/k part: a wave takes kPrepPasses passes of 64 / (D / 8) rows and
+// issues every pass's loads (the row, its table rows) before the first use, so the launch's
+// waves each wait for one round trip instead of one per row (one row per wave and pass took
+// the 1024-token prologue 18-21 us, most of it waiting).
+constexpr int kPrepPasses = 4;   // 8 measured slower (23.6 / 19.8 against 16.5 / 16.3 us)
+
 template <int D>
 __device__ __forceinline__ void gemma_prep_rows(const GemmaPrepParams &p, int wg) {
     // 8 channels per lane: a row of D = 512 takes a wave, a row of D = 256 half a wave
     constexpr int E = 8;
     constexpr int LPR = D / E;                      // lanes per row: 64 or 32
-    constexpr int RPW = 64 / LPR;                   // rows per wave
+    constexpr int RPW = 64 / LPR;                   // rows per wave and pass
+    constexpr int NP = kPrepPasses;
     const int lane = threadIdx.x & (LPR - 1);       // lane within the row
-    const int64_t row = ((int64_t)wg * 4 + (threadIdx.x >> 6)) * RPW +
-                        ((threadIdx.x & 63) / LPR);
-    const int heads = p.Hq + p.Hkv;                 // q heads, then k heads, per token
-    if (row >= (int64_t)p.B * p.T * heads) return;
-    const int hr = (int)(row % heads);
-    const int64_t bt = row / heads;
-    const int t = (int)(bt % p.T), b = (int)(bt / p.T);
-    const int kind = hr < p.Hq ? 0 : 1;             // q, k
-    const int h = kind == 0 ? hr : hr - p.Hq;
-    const bf16 *src = kind == 0 ? (const bf16 *)p.q + (int64_t)b * p.q_bs + (int64_t)t * p.q_rs
-                                : (const bf16 *)p.k + (int64_t)b * p.k_bs + (int64_t)t * p.k_rs;
-    src += (int64_t)h * D + lane * E;
-    float x[E];
-    unpack8(ldg16(src), x);
-    // the reductions and the partner exchange stay within the row's lanes (offsets < LPR)
-    float ss = 0.f;
+    // (row indices in 32 bits: the launch refuses 2^31 rows or more)
+    const uint32_t heads = p.Hq + p.Hkv;            // q heads, then k heads, per token
+    const uint32_t total = (uint32_t)p.B * p.T * heads;
+    // the wave's rows: RPW * NP consecutive rows, pass j taking rows base + RPW*j + (0..RPW-1)
+    const uint32_t base = ((uint32_t)wg * 4 + (threadIdx.x >> 6)) * (RPW * NP) +
+                          ((threadIdx.x & 63) / LPR);
+    const int col = (lane & (LPR / 2 - 1)) * E;     // table column of the lane's channels
+    u32x4 raw[NP];
+    f32x4 cs[NP][2], sn[NP][2];
+    int hrs[NP], ts[NP], bs[NP];
 #pragma unroll
-    for (int e = 0; e < E; ++e) ss += x[e] * x[e];
-#pragma unroll
-    for (int off = LPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-    const float rs = powf(ss / (float)D + p.eps, -0.5f);
-    const bf16 *w = (const bf16 *)(kind == 0 ? p.q_w : p.k_w) + lane * E;
-#pragma unroll
-    for (int e = 0; e < E; ++e) x[e] = (x[e] * rs) * (float)w[e];
-    // rotate_half pairs channel c with c +- D/2: lane l holds channels E*l ..; its partner is
-    // lane l ^ LPR/2. Table column of channel c is c mod D/2.
-    const int col = (lane & (LPR / 2 - 1)) * E;
-    const float *cs = p.cos + (int64_t)t * (D / 2) + col;
-    const float *sn = p.sin + (int64_t)t * (D / 2) + col;
-    const bool first = lane < LPR / 2;
-    const float f = kind == 0 ? p.q_factor : 1.0f;
-    float y[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const float other = __shfl_xor(x[e], LPR / 2, 64);
-        const float c = cs[e], s = sn[e];
-        // first half: x1 c - x2 s; second half: x2 c + x1 s
-        y[e] = (first ? x[e] * c - other * s : x[e] * c + other * s) * f;
+    for (int j = 0; j < NP; ++j) {
+        const uint32_t row = base + RPW * j;
+        const uint32_t bt = row / heads;
+        hrs[j] = (int)(row - bt * heads);
+        bs[j] = (int)(bt / (uint32_t)p.T);
+        ts[j] = (int)(bt - (uint32_t)bs[j] * p.T);
     }
-    // q' and k' as fp16 (11 significant bits, rounded once, to nearest)
-    auto put = [&](_Float16 *dst, const float (&z)[E]) __attribute__((always_inline)) {
-        *(u32x4 *)dst = pack8_f16(z);
-    };
-    if (kind == 1) {
-        // k' in operand order: 32-key block t/32, 16-channel chunk c, lane (t%32) + 32g holds
-        // channels 16c + 8g .. +7 of key t
-        const int ch = lane * E, c = ch >> 4, g = (ch >> 3) & 1;
-        const int nkb = (p.T + 31) / 32;
-        const int64_t off = ((((int64_t)b * p.Hkv + h) * nkb + (t >> 5)) * (D / 16) + c) * 512 +
-                            ((t & 31) + 32 * g) * 8 + (ch & 7);
-        put((_Float16 *)p.kp + off, y);
-    } else {
-        const int64_t off = (((int64_t)b * p.Hq + h) * p.T + t) * D + lane * E;
-        put((_Float16 *)p.qp + off, y);
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        if (base + RPW * j >= total) continue;
+        const int hr = hrs[j], t = ts[j], b = bs[j];
+        const bf16 *src = hr < p.Hq
+            ? (const bf16 *)p.q + (int64_t)b * p.q_bs + (int64_t)t * p.q_rs + (int64_t)hr * D
+            : (const bf16 *)p.k + (int64_t)b * p.k_bs + (int64_t)t * p.k_rs +
+                  (int64_t)(hr - p.Hq) * D;
+        raw[j] = ldg16(src + lane * E);
+        const float *c = p.cos + (int64_t)t * (D / 2) + col;
+        const float *sv = p.sin + (int64_t)t * (D / 2) + col;
+        cs[j][0] = *(const f32x4 *)c;
+        cs[j][1] = *(const f32x4 *)(c + 4);
+        sn[j][0] = *(const f32x4 *)sv;
+        sn[j][1] = *(const f32x4 *)(sv + 4);
+    }
+    float wq[E], wk[E];
+    unpack8(ldg16((const bf16 *)p.q_w + lane * E), wq);
+    unpack8(ldg16((const bf16 *)p.k_w + lane * E), wk);
+    const bool first = lane < LPR / 2;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        if (base + RPW * j >= total) continue;
+        const int hr = hrs[j], t = ts[j], b = bs[j];
+        const int kind = hr < p.Hq ? 0 : 1;         // q, k
+        const int h = kind == 0 ? hr : hr - p.Hq;
+        float x[E];
+        unpack8(raw[j], x);
+        // the reductions and the partner exchange stay within the row's lanes (offsets < LPR)
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) ss += x[e] * x[e];
+#pragma unroll
+        for (int off = LPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        const float rs = powf(ss / (float)D + p.eps, -0.5f);
+#pragma unroll
+        for (int e = 0; e < E; ++e) x[e] = (x[e] * rs) * (kind == 0 ? wq[e] : wk[e]);
+        // rotate_half pairs channel c with c +- D/2: lane l holds channels E*l ..; its partner
+        // is lane l ^ LPR/2. Table column of channel c is c mod D/2.
+        const float f = kind == 0 ? p.q_factor : 1.0f;
+        float y[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const float other = __shfl_xor(x[e], LPR / 2, 64);
+            const float c = cs[j][e >> 2][e & 3], s = sn[j][e >> 2][e & 3];
+            // first half: x1 c - x2 s; second half: x2 c + x1 s
+            y[e] = (first ? x[e] * c - other * s : x[e] * c + other * s) * f;
+        }
+        // q' and k' as fp16 (11 significant bits, rounded once, to nearest)
+        if (kind == 1) {
+            // k' in operand order: 32-key block t/32, 16-channel chunk c, lane (t%32) + 32g
+            // holds channels 16c + 8g .. +7 of key t
+            const int ch = lane * E, c = ch >> 4, g = (ch >> 3) & 1;
+            const int nkb = (p.T + 31) / 32;
+            const int64_t off =
+                ((((int64_t)b * p.Hkv + h) * nkb + (t >> 5)) * (D / 16) + c) * 512 +
+                ((t & 31) + 32 * g) * 8 + (ch & 7);
+            *(u32x4 *)((_Float16 *)p.kp + off) = pack8_f16(y);
+        } else {
+            const int64_t off = (((int64_t)b * p.Hq + h) * p.T + t) * D + lane * E;
+            *(u32x4 *)((_Float16 *)p.qp + off) = pack8_f16(y);
+        }
     }
 }
 
@@ -131,22 +164,24 @@ __device__ __forceinline__ void gemma_vt_block(const GemmaPrepParams &p, int wg,
     const int kb = wg % nkb, t0 = kb * TT;
     const int bh = wg / nkb;
     const int h = bh % p.Hkv, b = bh / p.Hkv;
+    // every row's load issued before the first use: a row past T loads row T - 1 and is
+    // zeroed afterwards (a branch around each load would make each wait for the one before)
     float x[RW][E];
+    typedef __attribute__((ext_vector_type(E / 2))) uint32_t uvec;
+    uvec raw[RW];
 #pragma unroll
     for (int j = 0; j < RW; ++j) {
-        const int t = t0 + wave * RW + j;
+        const int t = min(t0 + wave * RW + j, p.T - 1);
+        raw[j] = *(const uvec *)((const bf16 *)p.v + (int64_t)b * p.v_bs + (int64_t)t * p.v_rs +
+                                 (int64_t)h * D + lane * E);
+    }
 #pragma unroll
-        for (int e = 0; e < E; ++e) x[j][e] = 0.f;
-        if (t < p.T) {
-            const bf16 *src = (const bf16 *)p.v + (int64_t)b * p.v_bs + (int64_t)t * p.v_rs +
-                              (int64_t)h * D + lane * E;
-            if constexpr (E == 8) {
-                unpack8(ldg16(src), x[j]);
-            } else {
-                const u32x2 w = *(const u32x2 *)src;
-                x[j][0] = bf_lo(w[0]); x[j][1] = bf_hi(w[0]);
-                x[j][2] = bf_lo(w[1]); x[j][3] = bf_hi(w[1]);
-            }
+    for (int j = 0; j < RW; ++j) {
+        const bool in = t0 + wave * RW + j < p.T;
+#pragma unroll
+        for (int e = 0; e < E; e += 2) {
+            x[j][e] = in ? bf_lo(raw[j][e / 2]) : 0.f;
+            x[j][e + 1] = in ? bf_hi(raw[j][e / 2]) : 0.f;
         }
     }
 #pragma unroll
@@ -188,7 +223,9 @@ __device__ __forceinline__ void gemma_vt_block(const GemmaPrepParams &p, int wg,
 }
 
 // The prologue as one launch: the q/k rows' workgroups, then the v blocks' (they write
-// disjoint parts of k': rows below T, and the zeroed rows past T of the last block).
+// disjoint parts of k': rows below T, and the zeroed rows past T of the last block). (The v
+// blocks first measured 1.5 us faster at D = 512, with 32 of them, and 1.6 us slower at
+// D = 256, with 256.)
 template <int D>
 __global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p, int row_wgs) {
     __shared__ __attribute__((aligned(16))) _Float16 tile[32][D + 8];
@@ -196,7 +233,6 @@ __global__ __launch_bounds__(256) void gemma_prep_kernel(const GemmaPrepParams p
     if (wg < row_wgs) gemma_prep_rows<D>(p, wg);
     else gemma_vt_block<D>(p, wg - row_wgs, tile);
 }
-
 // ---- attention -----------------------------------------------------------------------------
 // Geometry: a wave owns 32 queries over 256 channels of the head (D = 256: the whole head; D =
 // 512: one half, its partner wave the other). Four waves per workgroup: 128 queries at D =
@@ -574,9 +610,11 @@ __global__ __launch_bounds__(256) void gemma_combine_kernel(const GemmaAttnParam
 }  // namespace
 
 int launch_gemma_prep(const GemmaPrepParams &p, int D, void *stream) {
-    // rows per workgroup: four waves of one (D = 512) or two (D = 256) rows
+    // rows per workgroup: four waves of kPrepPasses passes of one (D = 512) or two (D = 256)
+    // rows
     const int64_t rows = (int64_t)p.B * p.T * (p.Hq + p.Hkv);
-    const int64_t rows_wg = D == 512 ? 4 : 8;
+    if (rows > 0x7fffffff) return (int)hipErrorInvalidValue;   // 32-bit row indices
+    const int64_t rows_wg = (D == 512 ? 4 : 8) * kPrepPasses;
     const int64_t row_wgs = (rows + rows_wg - 1) / rows_wg;
     const int64_t v_wgs = (int64_t)p.B * p.Hkv * ((p.T + 31) / 32);
     if (row_wgs + v_wgs > 0x7fffffff) return (int)hipErrorInvalidValue;
