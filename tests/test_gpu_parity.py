@@ -623,6 +623,72 @@ def test_split_key_kernel_query_groups(device, Lq):
     _full_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev, f"split-key Lq={Lq}")
 
 
+def test_split_key_ranges_reuse_and_graph_replay(device):
+    """The split-key kernel's key ranges and their merge: 2, 5 and 16 ranges against the
+    oracle; repeated calls on one workspace, and a workspace filled with arbitrary bytes
+    beforehand, give the first call's bits; a HIP graph of the call (kernel and merge launch)
+    replayed several times, with eager work and eager calls between the replays, gives them
+    on every replay."""
+    import torch
+
+    H, D, Lq, Lk = 8, 64, 126, 3120
+    seed = 0x5EED + 800
+    _say(f"split-key ranges, reuse and graph replay Lq={Lq} Lk={Lk} H={H}")
+    qt = _index_rotary(np.arange(Lq), H * D, H)
+    kt = _index_rotary(np.arange(Lk) // 240, H * D, H)
+    tq, qb = _gpu_bits((1, Lq, H * D), seed, device)
+    tk, kb = _gpu_bits((1, Lk, H * D), seed + 1, device)
+    tv, vb = _gpu_bits((1, Lk, H * D), seed + 2, device)
+    kw_host = dict(q_cos=qt[0], q_sin=qt[1], k_cos=kt[0], k_sin=kt[1])
+    kw_dev = dict(rotary=L.Rotary(dev(qt[0], device), dev(qt[1], device)),
+                  key_rotary=L.Rotary(dev(kt[0], device), dev(kt[1], device)))
+    for splits in (2, 5, 16):
+        _full_check(device, tq, tk, tv, H, (qb, kb, vb), kw_host, kw_dev,
+                    f"split-key {splits} ranges", num_splits=splits)
+
+    ws = torch.empty(8 << 20, dtype=torch.uint8, device=device)   # more than the call needs
+    out = torch.empty_like(tq)
+
+    def call():
+        L.attention_fwd(tq, tk, tv, heads=H, num_splits=5, out=out, workspace=ws, **kw_dev)
+
+    call()
+    torch.cuda.synchronize()
+    first = out.clone()
+    for _ in range(3):
+        out.zero_()
+        call()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first)
+    ws.copy_(torch.randint(0, 256, ws.shape, dtype=torch.uint8, device=device))
+    out.zero_()
+    call()
+    torch.cuda.synchronize()
+    assert torch.equal(out, first)
+
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        call()                       # warm the capture stream's path
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    torch.cuda.synchronize()
+    scratch = torch.zeros(1 << 20, device=device)
+    for i in range(4):
+        out.zero_()
+        scratch.add_(1.0)            # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first), f"replay {i}"
+        call()                       # an eager call between replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, first), f"eager after replay {i}"
+
+
 @pytest.mark.parametrize("kprep", [L.KPREP_PROLOGUE, L.KPREP_FUSED])
 def test_c4_stage2_self_12480_norm_rope(device, kprep):
     _say(f"c4 12480 self-attention, norm + 3-D RoPE, kprep={kprep}")
