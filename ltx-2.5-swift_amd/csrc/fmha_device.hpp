@@ -212,8 +212,9 @@ __device__ __forceinline__ float gate_factor(const void *gate, int64_t g_bs, int
 }
 
 // Work item of a workgroup. Workgroup ids are dealt to the 8 XCDs round-robin; within each
-// region of the grid (whole items, then tail splits) an XCD receives a contiguous range, so
-// the query blocks (and splits) sharing one (batch, head) share an L2.
+// region of the grid (the leading tail splits, the whole items, the other tail splits) an XCD
+// receives a contiguous range, so the query blocks (and splits) sharing one (batch, head)
+// share an L2.
 struct WorkItem {
     int qblk, h, b;
     int tail;          // -1 for a whole item, else the tail item's index (0-based)
@@ -230,12 +231,15 @@ __device__ __forceinline__ WorkItem work_item(const FmhaParams &p) {
     const int bid = blockIdx.x;
     WorkItem w;
     int item;
-    if (bid < p.n_full) {
-        item = xcd_major(bid, p.n_full);
+    // grid order: n_lead tail splits, the whole items, the other tail splits
+    const int full_local = bid - p.n_lead;
+    if (full_local >= 0 && full_local < p.n_full) {
+        item = xcd_major(full_local, p.n_full);
         w.tail = -1;
         w.split = 0;
     } else {
-        const int sub = xcd_major(bid - p.n_full, p.grid - p.n_full);
+        const int tail_local = full_local < 0 ? bid : bid - p.n_full;
+        const int sub = xcd_major(tail_local, p.grid - p.n_full);
         w.tail = sub / p.num_splits;
         w.split = sub % p.num_splits;
         item = p.n_full + w.tail;

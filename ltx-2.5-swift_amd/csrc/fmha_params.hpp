@@ -48,6 +48,10 @@ struct FmhaParams {
     int32_t num_splits;              // >= 1 (tail items only)
     int32_t tiles_per_split;         // key tiles per split
     int32_t grid;
+    // The first n_lead workgroups run tail splits, then the whole items, then the other tail
+    // splits (n_lead a multiple of 8): the CUs that start on a short split begin their whole
+    // items that much later, so that the rounds' Q loads and O stores are not all at once.
+    int32_t n_lead;
     float *part_o;                   // tail partials [S][n_tail][256][D] fp32
     float *part_ml;                  // [S][n_tail][256][2]: running max (log2 units), row sum
     int32_t valid[kMaxBatch];        // keys valid per batch row (Lk when unmasked)

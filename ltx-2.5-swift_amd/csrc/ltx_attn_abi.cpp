@@ -95,6 +95,7 @@ struct Plan {
     int64_t n_full = 0;        // items run whole; the rest are split into key ranges
     int splits = 1;
     int tiles_per_split = 0;
+    int32_t n_lead = 0;        // tail splits placed ahead of the whole items (multiple of 8)
     int64_t grid = 0;
     // workspace layout (byte offsets)
     size_t off_qrstd = 0, off_krstd = 0, off_kprep = 0, off_part_o = 0, off_part_ml = 0;
@@ -337,6 +338,9 @@ ltx_attn_status make_plan(const ltx_attn_args *a, Plan *pl,
     pl->n_items = N;
     pl->n_full = n_full;
     pl->grid = n_full + (N - n_full) * pl->splits;
+    // Half the tail splits (a multiple of 8: every XCD the same share) lead the grid when
+    // whole rounds precede them.
+    pl->n_lead = n_full > 0 && n_full < N ? (int32_t)(((N - n_full) * pl->splits / 2) & ~7ll) : 0;
     if (pl->grid > 0x7fffffff)
         return fail(LTX_ATTN_EUNSUPPORTED, "grid too large");
 
@@ -606,6 +610,7 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
     fp.num_splits = pl.splits;
     fp.tiles_per_split = pl.tiles_per_split;
     fp.grid = (int32_t)pl.grid;
+    fp.n_lead = pl.n_lead;
     fp.short_groups = pl.short_groups;
     if (pl.n_full < pl.n_items) {
         fp.part_o = (float *)(ws + pl.off_part_o);
@@ -627,6 +632,7 @@ ltx_attn_status ltx_attn_fwd(const ltx_attn_args *a, void *stream) {
             if (sp.q_rstd) sp.q_rstd += (int64_t)b0 * a->Lq;
             if (sp.k_rstd) sp.k_rstd += (int64_t)b0 * a->Lk;
             sp.n_items = sp.n_full = sp.grid = nb * H * pl.nqblk;
+            sp.n_lead = 0;
             sp.num_splits = 1;
             if (a->ev_attn_start && b0 == 0)
                 if (hipError_t e = hipEventRecord((hipEvent_t)a->ev_attn_start, (hipStream_t)stream))
