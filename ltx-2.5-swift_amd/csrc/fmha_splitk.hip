@@ -14,7 +14,8 @@
 // rounding -- the arithmetic of the K prologue) while every wave with queries computes on
 // the tile before it: S^T = K.Q'^T, the softmax with each row's max taken from its first
 // block and -max as the S accumulators' start (an exact online softmax redoes the range when
-// a row sum overflows), and O^T += V^T.P^T. One barrier per tile separates the phases. The range's partial O, max and row sum go to the
+// a row sum overflows), and O^T += V^T.P^T (P as bf16, or as bf16 hi + lo parts without
+// RoPE). One barrier per tile separates the phases. The range's partial O, max and row sum go to the
 // split-KV workspace the combine kernel merges; a call with a single range writes O directly.
 #include <type_traits>
 
@@ -64,6 +65,12 @@ void fmha_splitk_kernel(const FmhaParams p) {
     constexpr int NC = T::NC, NDB = T::NDB, KU = T::KU, COPIES = T::COPIES;
     constexpr int AHEAD = T::STAGES - 1;
     constexpr bool KWORK = ROPE || NORM;
+    // Without RoPE (the audio queries over the text keys) the reference's own arithmetic
+    // rounds little (the norms), and P rounded to bf16 would be the larger part of the
+    // kernel's error: P then also takes its lo part (P - bf16(P), a second product per P.V
+    // operand; 4-8% on those calls). With RoPE the reference's rounded rotations dominate
+    // and P stays one bf16 part.
+    constexpr bool HILO = !ROPE;
     __shared__ __attribute__((aligned(16))) char smem[T::BYTES];
 
     const int tid = threadIdx.x;
@@ -257,7 +264,7 @@ void fmha_splitk_kernel(const FmhaParams p) {
                 s[1] = mfma32(a, qf[1][c], s[1]);
             }
             const bool ragged = key0 + 32 > n_valid;
-            bf16x8 pn[2][2];
+            bf16x8 pn[2][2], pl[2][2];   // P (fp32 weights) as bf16 hi (+ lo) parts
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
                 if (ragged) {
@@ -290,28 +297,40 @@ void fmha_splitk_kernel(const FmhaParams p) {
                 float ts = 0.f;
 #pragma unroll
                 for (int hf = 0; hf < 2; ++hf) {
-                    u32x4 w;
+                    u32x4 w, wl;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const float x0 = __builtin_amdgcn_exp2f(s[qb][8 * hf + 2 * e]);
                         const float x1 = __builtin_amdgcn_exp2f(s[qb][8 * hf + 2 * e + 1]);
                         ts += x0 + x1;
                         w[e] = pack_bf2(x0, x1);
+                        if constexpr (HILO) wl[e] = pack_bf2(x0 - bf_lo(w[e]), x1 - bf_hi(w[e]));
                     }
                     pn[qb][hf] = __builtin_bit_cast(bf16x8, w);
+                    if constexpr (HILO) pl[qb][hf] = __builtin_bit_cast(bf16x8, wl);
                 }
                 if (!SAFE) overflow |= !(ts <= kRebaseBound);
                 l[qb] += ts;
             }
             first = false;
+            // O += V^T.P, with P's lo part too when HILO
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf)
+            for (int hf = 0; hf < 2; ++hf) {
+                bf16x8 a[NDB];
 #pragma unroll
                 for (int db = 0; db < NDB; ++db) {
-                    const bf16x8 a = v_opnd(Vs, 2 * kb + hf, db);
-                    o[db][0] = mfma32(a, pn[0][hf], o[db][0]);
-                    o[db][1] = mfma32(a, pn[1][hf], o[db][1]);
+                    a[db] = v_opnd(Vs, 2 * kb + hf, db);
+                    o[db][0] = mfma32(a[db], pn[0][hf], o[db][0]);
+                    o[db][1] = mfma32(a[db], pn[1][hf], o[db][1]);
                 }
+                if constexpr (HILO) {
+#pragma unroll
+                    for (int db = 0; db < NDB; ++db) {
+                        o[db][0] = mfma32(a[db], pl[0][hf], o[db][0]);
+                        o[db][1] = mfma32(a[db], pl[1][hf], o[db][1]);
+                    }
+                }
+            }
         }
         if (t_begin >= t_end) wait_copies();
     };
