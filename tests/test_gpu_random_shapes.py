@@ -1,0 +1,119 @@
+"""GPU parity over a seeded sweep of call shapes and options, against the C oracle.
+
+Each case draws (from a fixed seed) the batch, heads, head dim, query and key lengths, per-row
+valid key lengths, the q/k norms, the RoPE tables, the per-head gate, the caller's split count
+and the part size the tail splits are planned for (``resident_groups``), so that the plans the
+library chooses -- LDS-DMA kernel with whole and split items, short-key kernel, split-key
+kernel, register kernel, batches beyond one launch -- meet shapes no hand-written case names.
+Tolerance (the target's): relRMS <= 5e-3 and maxAbs <= 2e-2 against the oracle's fp32
+arithmetic after the bf16 inputs (``DiTAttention.swift:358-381`` with the gate of
+``:395-399``), and at most 1.25x the reference arithmetic's own relRMS (floor 2.5e-3). The
+gate multiplies the attention output, and its rounding, by up to 2: with a gate the maxAbs
+bar is 2e-2 times the case's largest gate factor.
+"""
+
+import numpy as np
+import pytest
+
+import ltx_attn as L
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+REL_RMS, MAX_ABS = 5e-3, 2e-2
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _dev(bits, device):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(device).view(
+        torch.bfloat16)
+
+
+def _tables(positions, heads, D):
+    """1-D RoPE tables [H, L, D/2] (bf16 bits) from integer positions, the reference's recipe
+    (frequency grid, centre over maxPos, theta 1e4)."""
+    pos = np.zeros((1, 1, len(positions), 2), dtype=np.float32)
+    pos[0, 0, :, 0] = positions
+    pos[0, 0, :, 1] = positions
+    return O.rotary_tables(pos, heads * D, [max(int(positions.max()) + 1, 2)], heads)
+
+
+def _case(i):
+    rng = np.random.default_rng(0x5EED + 9000 + i)
+    D = int(rng.choice([64, 128]))
+    H = int(rng.choice([1, 2, 4, 8, 16]))
+    B = int(rng.choice([1, 1, 2, 3]))
+    Lq = int(np.exp(rng.uniform(np.log(16), np.log(2600))))
+    Lk = int(np.exp(rng.uniform(np.log(16), np.log(3200))))
+    while B * H * Lq * Lk > 40_000_000:             # the oracle finishes in seconds
+        Lq = max(16, Lq // 2)
+        Lk = max(16, Lk // 2)
+    valid = [int(rng.integers(1, Lk + 1)) for _ in range(B)] if rng.random() < 0.4 else None
+    return dict(
+        B=B, H=H, D=D, Lq=Lq, Lk=Lk, valid=valid,
+        norm=bool(rng.random() < 0.5), rope=bool(rng.random() < 0.5),
+        gate=bool(rng.random() < 0.3),
+        num_splits=int(rng.choice([0, 0, 0, 2, 5])),
+        resident_groups=int(rng.choice([0, 0, 32, 100, 200])),
+        seed=int(rng.integers(1, 1 << 30)),
+    )
+
+
+CASES = [_case(i) for i in range(24)]
+
+
+@pytest.mark.parametrize("i", range(len(CASES)))
+def test_random_shape(device, i):
+    import torch
+
+    c = CASES[i]
+    B, H, D, Lq, Lk, seed = c["B"], c["H"], c["D"], c["Lq"], c["Lk"], c["seed"]
+    _say(f"random {i}: {c}")
+    q = O.randn_bf16_bits((B, Lq, H * D), seed)
+    k = O.randn_bf16_bits((B, Lk, H * D), seed + 1)
+    v = O.randn_bf16_bits((B, Lk, H * D), seed + 2)
+    kw_host, kw_dev = {}, {}
+    if c["norm"]:
+        wq = O.randn_bf16_bits((H * D,), seed + 3, mean=1.0, std=0.02)
+        wk = O.randn_bf16_bits((H * D,), seed + 4, mean=1.0, std=0.02)
+        kw_host.update(q_norm_w=wq, k_norm_w=wk)
+        kw_dev.update(q_norm_w=_dev(wq, device), k_norm_w=_dev(wk, device))
+    if c["rope"]:
+        qc, qs = _tables(np.arange(Lq) // 3, H, D)
+        kc, ks = _tables(np.arange(Lk) // 5, H, D)
+        kw_host.update(q_cos=qc, q_sin=qs, k_cos=kc, k_sin=ks)
+        kw_dev.update(rotary=L.Rotary(_dev(qc, device), _dev(qs, device)),
+                      key_rotary=L.Rotary(_dev(kc, device), _dev(ks, device)))
+    if c["valid"] is not None:
+        kw_host["valid_len"] = c["valid"]
+        kw_dev["k_valid_len"] = c["valid"]
+    g = None
+    max_abs = MAX_ABS
+    if c["gate"]:
+        g = O.randn_bf16_bits((B, Lq, H), seed + 5, std=2.0)
+        kw_dev["gate_logits"] = _dev(g, device)
+    out = L.attention_fwd(_dev(q, device), _dev(k, device), _dev(v, device), heads=H,
+                          num_splits=c["num_splits"], resident_groups=c["resident_groups"],
+                          **kw_dev)
+    torch.cuda.synchronize()
+    got = O.bf16_bits_to_f32(out.contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+    got = got.reshape(B, Lq, H, D)
+    truth = O.c_attention(q, k, v, H, mode="exact", **kw_host)
+    ref = O.round_bf16(O.c_attention(q, k, v, H, mode="reference", **kw_host))
+    if g is not None:
+        gate = O.head_gate(g, "exact")[..., None]
+        truth = truth * gate
+        max_abs = MAX_ABS * max(1.0, float(gate.max()))
+        ref = O.round_bf16(ref * O.head_gate(g, "reference")[..., None])
+    cg = O.compare(got, truth)
+    cr = O.compare(ref, truth)
+    _say(f"  relRMS {cg['rel_rms']:.3e} maxAbs {cg['max_abs']:.3e} (bar {max_abs:.3e}; "
+         f"reference arithmetic relRMS {cr['rel_rms']:.3e} maxAbs {cr['max_abs']:.3e})")
+    assert cg["rel_rms"] <= REL_RMS, cg
+    assert cg["max_abs"] <= max_abs, (cg, max_abs)
+    assert cg["rel_rms"] <= max(cr["rel_rms"], 2.5e-3) * 1.25, (cg, cr)
