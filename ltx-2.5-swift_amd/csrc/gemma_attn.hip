@@ -422,6 +422,16 @@ void gemma_attn_kernel(const GemmaAttnParams p) {
                     for (int e = 0; e < 4; ++e) s[4 * i4 + e] = a0[e] + a1[e];
                 }
             }
+            // V'^T operands of the first key half, read now: they do not depend on the softmax
+            // below, which hides their LDS round trip (read beside the products, two at a
+            // time, each product waited for one)
+            auto v_opnd = [&](int hf, int db) __attribute__((always_inline)) {
+                return *(const __attribute__((address_space(3))) f16x8 *)(
+                    (lds_void *)(Vs + (hf * (D / 32) + half * NDW + db) * 1024 + lane * 16));
+            };
+            f16x8 va0[NDW];
+#pragma unroll
+            for (int db = 0; db < NDW; ++db) va0[db] = v_opnd(0, db);
             // mask: key k = 32 kb + 8 (i >> 2) + 4 g + (i & 3) for query q
             float mx = -INFINITY;
 #pragma unroll
@@ -464,18 +474,18 @@ void gemma_attn_kernel(const GemmaAttnParams p) {
             }
             l += ts;
             // O^T += V^T.P^T for this wave's channels; consecutive products update different
-            // accumulators (a key half over all channel blocks)
+            // accumulators (a key half over all channel blocks). The second half's operands are
+            // read one before each product of the first half.
+            f16x8 va1[NDW];
 #pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-                f16x8 va[NDW];
-#pragma unroll
-                for (int db = 0; db < NDW; ++db)
-                    va[db] = *(const __attribute__((address_space(3))) f16x8 *)(
-                        (lds_void *)(Vs + (hf * (D / 32) + half * NDW + db) * 1024 + lane * 16));
-#pragma unroll
-                for (int db = 0; db < NDW; ++db)
-                    o[db] = mfma32(va[db], __builtin_bit_cast(f16x8, wh[hf]), o[db]);
+            for (int db = 0; db < NDW; ++db) {
+                va1[db] = v_opnd(1, db);
+                o[db] = mfma32(va0[db], __builtin_bit_cast(f16x8, wh[0]), o[db]);
+                __builtin_amdgcn_sched_barrier(0);
             }
+#pragma unroll
+            for (int db = 0; db < NDW; ++db)
+                o[db] = mfma32(va1[db], __builtin_bit_cast(f16x8, wh[1]), o[db]);
         }
     };
     run(std::false_type{}, true);
