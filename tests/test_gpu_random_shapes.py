@@ -12,6 +12,8 @@ gate multiplies the attention output, and its rounding, by up to 2: with a gate 
 bar is 2e-2 times the case's largest gate factor.
 """
 
+import os
+
 import numpy as np
 import pytest
 
@@ -64,7 +66,8 @@ def _case(i):
     )
 
 
-CASES = [_case(i) for i in range(24)]
+# 24 cases by default; LTX_ATTN_RANDOM_CASES=n runs the first n seeds of the same sequence.
+CASES = [_case(i) for i in range(int(os.environ.get("LTX_ATTN_RANDOM_CASES", "24")))]
 
 
 @pytest.mark.parametrize("i", range(len(CASES)))
