@@ -107,6 +107,26 @@ CASES = {
 }
 
 
+
+
+def _random_case(i):
+    """Seeded draws of batch, prompt length (a multiple of 4, as the call requires), layer
+    kind, window and left padding per row (padding up to the whole prompt), for shapes no
+    hand-written case names."""
+    rng = np.random.default_rng(0x5EED + 7000 + i)
+    B = int(rng.choice([1, 2]))
+    T = 4 * max(1, int(np.exp(rng.uniform(np.log(4), np.log(1400)))) // 4)   # a multiple of 4
+    kind = str(rng.choice(["sliding", "full"]))
+    case = dict(B=B, T=T, kind=kind, seed=int(rng.integers(1, 1 << 30)),
+                fv=[int(rng.integers(0, T + 1)) if rng.random() < 0.5 else 0 for _ in range(B)])
+    if kind == "sliding" and rng.random() < 0.5:
+        case["window"] = int(rng.integers(1, T + 1))
+    return case
+
+
+CASES.update({f"random_{i}": _random_case(i) for i in range(8)})
+
+
 @pytest.mark.parametrize("name", sorted(CASES))
 def test_gemma_attention(device, name):
     _say(f"gemma {name}")
