@@ -276,3 +276,38 @@ def test_tail_split_for_other_part_sizes(device, groups):
     rows = np.r_[0:64, 1024:1088, M - 64:M]
     check_linear(yb[rows], np.ascontiguousarray(x[rows]), w, b, f"groups {groups} rows")
     check_partials(parts.cpu().numpy(), yb, f"groups {groups}")
+
+
+def _random_linear_case(i):
+    """Seeded draws of M (any), N (a multiple of 8), K (a multiple of 64), bias, statistic,
+    the part size the tail split is planned for, and whether a workspace allows the split."""
+    rng = np.random.default_rng(0x5EED + 8000 + i)
+    M = int(np.exp(rng.uniform(np.log(1), np.log(3000))))
+    N = 8 * max(1, int(np.exp(rng.uniform(np.log(8), np.log(3000)))) // 8)
+    K = 64 * int(rng.integers(1, 65))
+    while M * N * K > 2_000_000_000:                 # the float64 oracle finishes in seconds
+        M = max(1, M // 2)
+    return dict(M=M, N=N, K=K, bias=bool(rng.random() < 0.5), sumsq=bool(rng.random() < 0.5),
+                groups=int(rng.choice([0, 0, 32, 100])), split=bool(rng.random() < 0.7),
+                seed=int(rng.integers(1, 1 << 30)))
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_linear_random_shapes(device, i):
+    import torch
+
+    c = _random_linear_case(i)
+    M, N, K, seed = c["M"], c["N"], c["K"], c["seed"]
+    _say(f"linear random {i}: {c}")
+    x = O.randn_bf16_bits((M, K), seed)
+    w = O.randn_bf16_bits((N, K), seed + 1, std=K ** -0.5)
+    b = O.randn_bf16_bits((N,), seed + 2, std=0.5) if c["bias"] else None
+    out = L.linear(dev(x, device), dev(w, device), None if b is None else dev(b, device),
+                   sumsq=c["sumsq"], workspace=None if c["split"] else False,
+                   resident_groups=c["groups"])
+    torch.cuda.synchronize()
+    y, parts = out if c["sumsq"] else (out, None)
+    yb = host_bits(y)
+    check_linear(yb, x, w, b, f"random {i}")
+    if parts is not None:
+        check_partials(parts.cpu().numpy(), yb, f"random {i}")
