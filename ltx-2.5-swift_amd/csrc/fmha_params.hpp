@@ -123,6 +123,9 @@ struct LinearParams {
     // every tile whole (n_full = tiles_m * tiles_n).
     float *part;
     int32_t n_full, splits, steps_per_split;
+    // Workgroups of the launch: workgroup g runs whole tiles g, g + grid, ... below n_full,
+    // then tail range g (grid >= the number of ranges).
+    int32_t grid;
 };
 
 // RMS statistic from partial sums of squares: rstd[row] = 1/sqrt(sum_j parts[row][j] / n + eps)

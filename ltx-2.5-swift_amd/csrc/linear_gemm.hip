@@ -157,177 +157,238 @@ void linear_kernel(const LinearParams p) {
     const int wm = wave >> 1, wn = wave & 1;
     const int r = lane & 31, g = lane >> 5;
 
-    // Tile of this workgroup. Workgroups go to the 8 XCDs round-robin; in each region of the
-    // grid (whole tiles, then tail ranges) each XCD gets a contiguous range of the tile order,
-    // which walks groups of 8 row tiles column tile by column tile, so the ~32 workgroups an
-    // XCD runs at once share 8 row tiles of x and 4 column tiles of w in its L2, and the
-    // ranges of one tail tile share all of it.
+    // Work of this workgroup. The grid is persistent: workgroup g runs the whole tiles
+    // g, g + G, g + 2G, ... of the tile order (G workgroups), then tail range g if there is
+    // one. Workgroups go to the 8 XCDs round-robin and G is a multiple of 8 on a whole part, so
+    // in every round each XCD runs a contiguous range of the tile order, which walks groups of
+    // 8 row tiles column tile by column tile: the ~32 workgroups an XCD runs at once share 8 row
+    // tiles of x and 4 column tiles of w in its L2, and the ranges of one tail tile share all
+    // of it. From one whole tile to the next a workgroup does not stop: the next tile's first
+    // copies are issued during the current tile's last two k steps, as within a tile, so its
+    // epilogue runs while they land instead of after a round's worth of workgroups restarts.
     const int bid = blockIdx.x;
+    const int G = gridDim.x;
     const int nsteps = p.K / BK;
-    int t, k_begin = 0, k_end = nsteps, range = -1;
-    if (bid < p.n_full) {
-        t = xcd_major(bid, p.n_full);
-    } else {
-        const int n_tail = p.tiles_m * p.tiles_n - p.n_full;
-        range = xcd_major(bid - p.n_full, n_tail * p.splits);   // tile-major: (tile, split)
-        t = p.n_full + range / p.splits;
-        k_begin = (range % p.splits) * p.steps_per_split;
-        k_end = min(k_begin + p.steps_per_split, nsteps);
+    const int xrow = (int)(p.x_rs * 2), wrow = (int)(p.w_rs * 2);    // row bytes
+    // Copy j of this wave's share of a tile: LDS unit q = (wave*CPT + j)*64 + lane holds row
+    // q / U, logical unit lswz(row, q % U); its source offset is fixed for every tile, the tile
+    // and the k step move the resource's base.
+    int xl[CPT], wl[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int q = (wave * CPT + j) * 64 + lane;
+        const int row = q / U, u = lswz<U>(row, q % U);
+        xl[j] = row * xrow + 16 * u;
+        wl[j] = row * wrow + 16 * u;
     }
-    int tm, tn;
-    tile_coords(p, t, tm, tn);
-    const int m0 = tm * LT, n0 = tn * LT;
-
-    // Whole tiles and tail ranges run separate copies of what follows, so that neither's
-    // epilogue shares a register assignment with the other's (one shared copy spills).
-    auto body = [&](auto tail) __attribute__((always_inline)) {
-        // ---- copies HBM -> LDS ----------------------------------------------------------
-        const int xrow = (int)(p.x_rs * 2), wrow = (int)(p.w_rs * 2);    // row bytes
-        const char *X0 = (const char *)p.x + (int64_t)m0 * xrow;
-        const char *W0 = (const char *)p.w + (int64_t)n0 * wrow;
-        const int64_t xbytes = (int64_t)min(LT, p.M - m0) * xrow;
-        const int64_t wbytes = (int64_t)min(LT, p.N - n0) * wrow;
-        // Copy j of this wave's share of a tile: LDS unit q = (wave*CPT + j)*64 + lane holds row
-        // q / U, logical unit lswz(row, q % U); its source offset is fixed for the whole tile, the
-        // k step moves the resource's base.
-        int xl[CPT], wl[CPT];
-#pragma unroll
-        for (int j = 0; j < CPT; ++j) {
-            const int q = (wave * CPT + j) * 64 + lane;
-            const int row = q / U, u = lswz<U>(row, q % U);
-            xl[j] = row * xrow + 16 * u;
-            wl[j] = row * wrow + 16 * u;
+    // Copy j (0 .. 2*CPT-1) of this wave's share of a k step into buffer st: even j of w, odd
+    // of x.
+    auto copy_with = [&](const u32x4 &rw, const u32x4 &rx, int st, int j) __attribute__((always_inline)) {
+        if ((j & 1) == 0) {
+            copy_all(rw, (uint32_t)(uintptr_t)((lds_bf16 *)sW + st * ELEMS + (wave * CPT + j / 2) * 512),
+                     wl[j / 2]);
+        } else {
+            copy_all(rx, (uint32_t)(uintptr_t)((lds_bf16 *)sX + st * ELEMS + (wave * CPT + j / 2) * 512),
+                     xl[j / 2]);
         }
-        // Copy j (0 .. 2*CPT-1) of this wave's share of k step s into buffer st: even j of w, odd
-        // of x.
-        auto copy_with = [&](const u32x4 &rw, const u32x4 &rx, int st, int j) __attribute__((always_inline)) {
-            if ((j & 1) == 0) {
-                copy_all(rw, (uint32_t)(uintptr_t)((lds_bf16 *)sW + st * ELEMS + (wave * CPT + j / 2) * 512),
-                         wl[j / 2]);
-            } else {
-                copy_all(rx, (uint32_t)(uintptr_t)((lds_bf16 *)sX + st * ELEMS + (wave * CPT + j / 2) * 512),
-                         xl[j / 2]);
-            }
-        };
-        auto copy_one = [&](int s, int st, int j) __attribute__((always_inline)) {
-            const int kb = s * BK * 2;
-            copy_with(rsrc_words(W0 + kb, wbytes), rsrc_words(X0 + kb, xbytes), st, j);
-        };
-        // Operand of rows row0 + 0..31, reduction chunk c: lane (r, g) reads row row0 + r, unit 2c + g.
-        auto frag = [&](const lds_bf16 *S, int row0, int c) __attribute__((always_inline)) {
-            const int row = row0 + r;
-            return *(const __attribute__((address_space(3))) bf16x8 *)(S + row * BK + 8 * lswz<U>(row, 2 * c + g));
-        };
-
-        f32x16 acc[4][4];              // [n block][m block]
+    };
+    // A tile's operand rows: x rows m0.., w rows n0.. (rows past M, N read as zeros through the
+    // resources' bounds).
+    struct TileSrc {
+        const char *X0, *W0;
+        int64_t xbytes, wbytes;
+        int m0, n0, tn;
+    };
+    auto tile_src = [&](int t) __attribute__((always_inline)) {
+        int tm, tn;
+        tile_coords(p, t, tm, tn);
+        TileSrc ts;
+        ts.m0 = tm * LT;
+        ts.n0 = tn * LT;
+        ts.tn = tn;
+        ts.X0 = (const char *)p.x + (int64_t)ts.m0 * xrow;
+        ts.W0 = (const char *)p.w + (int64_t)ts.n0 * wrow;
+        ts.xbytes = (int64_t)min(LT, p.M - ts.m0) * xrow;
+        ts.wbytes = (int64_t)min(LT, p.N - ts.n0) * wrow;
+        return ts;
+    };
+    // Operand of rows row0 + 0..31, reduction chunk c: lane (r, g) reads row row0 + r, unit 2c + g.
+    auto frag = [&](const lds_bf16 *S, int row0, int c) __attribute__((always_inline)) {
+        const int row = row0 + r;
+        return *(const __attribute__((address_space(3))) bf16x8 *)(S + row * BK + 8 * lswz<U>(row, 2 * c + g));
+    };
+    bf16x8 a[2][4], b[2][4];           // operands of the current and the next chunk
+    auto read_chunk = [&](int st, int c, int buf) __attribute__((always_inline)) {
+        const lds_bf16 *Ws = (const lds_bf16 *)sW + st * ELEMS;
+        const lds_bf16 *Xs = (const lds_bf16 *)sX + st * ELEMS;
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
+        for (int i = 0; i < 4; ++i) {
+            a[buf][i] = frag(Ws, wn * 128 + 32 * i, c);
+            b[buf][i] = frag(Xs, wm * 128 + 32 * i, c);
+        }
+    };
+    // Prologue of a run of k steps: its first step, and the first half of its second (each
+    // step issues the rest for its successor), then the first operands.
+    auto prologue = [&](const TileSrc &ts, int k0, bool two) __attribute__((always_inline)) {
+        const int kb = k0 * BK * 2;
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = splat16(0.f);
-
-        bf16x8 a[2][4], b[2][4];       // operands of the current and the next chunk
-        auto read_chunk = [&](int st, int c, int buf) __attribute__((always_inline)) {
-            const lds_bf16 *Ws = (const lds_bf16 *)sW + st * ELEMS;
-            const lds_bf16 *Xs = (const lds_bf16 *)sX + st * ELEMS;
+        for (int j = 0; j < 2 * CPT; ++j)
+            copy_with(rsrc_words(ts.W0 + kb, ts.wbytes), rsrc_words(ts.X0 + kb, ts.xbytes), 0, j);
+        if (two) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                a[buf][i] = frag(Ws, wn * 128 + 32 * i, c);
-                b[buf][i] = frag(Xs, wm * 128 + 32 * i, c);
-            }
-        };
-        // Prologue: the range's first step, and the first half of its second (the first step
-        // issues the rest, as every step does for its successor), then the first operands.
-#pragma unroll
-        for (int j = 0; j < 2 * CPT; ++j) copy_one(k_begin, 0, j);
-        if (k_end - k_begin > 1) {
-#pragma unroll
-            for (int j = 0; j < CPT; ++j) copy_one(k_begin + 1, 1, j);
+            for (int j = 0; j < CPT; ++j)
+                copy_with(rsrc_words(ts.W0 + kb + BK * 2, ts.wbytes),
+                          rsrc_words(ts.X0 + kb + BK * 2, ts.xbytes), 1, j);
             wait_copies_but<CPT>();
         } else {
             wait_copies();
         }
         __syncthreads();
         read_chunk(0, 0, 0);
+    };
 
-        // One k step; COPY: issue the first half of step s + 2's copies (into the buffer the
-        // step frees), NEXT: read step s + 1's first operands; REST: issue the second half of
-        // step s + 1's copies in the first chunk (half a step's copies per chunk keeps the
-        // address unit's queue from filling).
-        auto step = [&](int s, auto copy, auto next, auto rest) __attribute__((always_inline)) {
-            const int st = (s - k_begin) & 1;
-            // the resources of the copies this step issues: step s + 1's second half, step
-            // s + 2's first half
-            u32x4 rw1, rx1, rw2, rx2;
-            if constexpr (decltype(rest)::value) {
-                rw1 = rsrc_words(W0 + (s + 1) * BK * 2, wbytes);
-                rx1 = rsrc_words(X0 + (s + 1) * BK * 2, xbytes);
-            }
-            if constexpr (decltype(copy)::value) {
-                rw2 = rsrc_words(W0 + (s + 2) * BK * 2, wbytes);
-                rx2 = rsrc_words(X0 + (s + 2) * BK * 2, xbytes);
-            }
+    // One k step on LDS buffer st. has1: there is a next step (in this tile or the next); its
+    // copies' second half (resources rw1, rx1) are issued in the first chunk and its first
+    // operands read in the last. has2: there is a step after it, whose copies' first half
+    // (rw2, rx2) go into the buffer this step frees, in the last chunk (half a step's copies
+    // per chunk keeps the address unit's queue from filling). A1, A2: has1, has2 hold whatever
+    // the run-time flags say (the inner steps of a run, without branches).
+    auto step = [&](auto A1, auto A2, bool h1, bool h2, int st, f32x16(&acc)[4][4],
+                    const u32x4 &rw1, const u32x4 &rx1, const u32x4 &rw2, const u32x4 &rx2)
+        __attribute__((always_inline)) {
+        const bool has1 = decltype(A1)::value || h1, has2 = decltype(A2)::value || h2;
 #pragma unroll
-            for (int c = 0; c < NCH; ++c) {
-                const int cb = c & 1;          // NCH is even: chunk 0 of every step is in buffer 0
-                // The next chunk's operands -- of this step, or after the barrier the next
-                // step's first -- are read one after every other product of this chunk.
-                const bool rd = c < NCH - 1 || decltype(next)::value;
-                const int rst = c < NCH - 1 ? st : st ^ 1, rc = c < NCH - 1 ? c + 1 : 0;
-                if (c == NCH - 1) {
-                    // Step s+1's copies (issued one step ago) have landed for this wave; after the
-                    // barrier they have for every wave, and every wave's reads of buffer st are done.
-                    // The scheduling fences keep the earlier chunks' products ahead of the wait.
-                    __builtin_amdgcn_sched_barrier(0);
-                    wait_copies();
-                    __syncthreads();
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-#pragma unroll
-                for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-                    for (int mb = 0; mb < 4; ++mb) {
-                        const int pr = 4 * nb + mb;                // product of the chunk
-                        if (rd && (pr & 1) == 0) {
-                            // operand pr / 2 of the next chunk: a[0], b[0], a[1], b[1], ...
-                            const int j = pr >> 1;
-                            const lds_bf16 *Ws = (const lds_bf16 *)sW + rst * ELEMS;
-                            const lds_bf16 *Xs = (const lds_bf16 *)sX + rst * ELEMS;
-                            if ((j & 1) == 0) a[cb ^ 1][j >> 1] = frag(Ws, wn * 128 + 32 * (j >> 1), rc);
-                            else b[cb ^ 1][j >> 1] = frag(Xs, wm * 128 + 32 * (j >> 1), rc);
-                            __builtin_amdgcn_sched_barrier(0);
-                        }
-                        acc[nb][mb] = mfma32(a[cb][nb], b[cb][mb], acc[nb][mb]);
-                        if (decltype(copy)::value && c == NCH - 1 && (pr & 1) == 0) {
-                            copy_with(rw2, rx2, st, pr / 2);       // copies 0 .. CPT-1
-                            __builtin_amdgcn_sched_barrier(0);
-                        }
-                        if (decltype(rest)::value && c == 0 && (pr & 1) == 0) {
-                            copy_with(rw1, rx1, st ^ 1, CPT + pr / 2);   // CPT .. 2*CPT-1
-                            __builtin_amdgcn_sched_barrier(0);
-                        }
-                    }
+        for (int c = 0; c < NCH; ++c) {
+            const int cb = c & 1;          // NCH is even: chunk 0 of every step is in buffer 0
+            // The next chunk's operands -- of this step, or after the barrier the next step's
+            // first -- are read one before every other product of this chunk (all eight at the
+            // chunk's start left the LDS reads of the four waves bunched).
+            const bool rd = c < NCH - 1 || has1;
+            const int rst = c < NCH - 1 ? st : st ^ 1, rc = c < NCH - 1 ? c + 1 : 0;
+            if (c == NCH - 1) {
+                // The next step's copies (issued one step ago) have landed for this wave; after
+                // the barrier they have for every wave, and every wave's reads of buffer st are
+                // done. The scheduling fences keep the earlier chunks' products ahead of the wait.
+                __builtin_amdgcn_sched_barrier(0);
+                wait_copies();
+                __syncthreads();
+                __builtin_amdgcn_sched_barrier(0);
             }
-        };
-        using yes = std::true_type;
-        using no = std::false_type;
-        int s = k_begin;
-        for (; s + 2 < k_end; ++s) step(s, yes{}, yes{}, yes{});
-        if (s + 1 < k_end) step(s++, no{}, yes{}, yes{});
-        step(s, no{}, no{}, no{});
-
-        if constexpr (decltype(tail)::value) {
-            // A tail range: its accumulators, in register order, for the fixup.
-            f32x16 *dst = (f32x16 *)(p.part + (int64_t)range * (LT * LT)) + wave * 16 * 64 + lane;
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-                for (int mb = 0; mb < 4; ++mb) dst[(4 * nb + mb) * 64] = acc[nb][mb];
-        } else {
-            store_rows<4>(p, acc, m0 + wm * 128, n0 + wn * 128, tn, wn, wm * 128, LT);
+                for (int mb = 0; mb < 4; ++mb) {
+                    const int pr = 4 * nb + mb;                // product of the chunk
+                    if (rd && (pr & 1) == 0) {
+                        // operand pr / 2 of the next chunk: a[0], b[0], a[1], b[1], ...
+                        const int j = pr >> 1;
+                        const lds_bf16 *Ws = (const lds_bf16 *)sW + rst * ELEMS;
+                        const lds_bf16 *Xs = (const lds_bf16 *)sX + rst * ELEMS;
+                        if ((j & 1) == 0) a[cb ^ 1][j >> 1] = frag(Ws, wn * 128 + 32 * (j >> 1), rc);
+                        else b[cb ^ 1][j >> 1] = frag(Xs, wm * 128 + 32 * (j >> 1), rc);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    acc[nb][mb] = mfma32(a[cb][nb], b[cb][mb], acc[nb][mb]);
+                    if (has2 && c == NCH - 1 && (pr & 1) == 0) {
+                        copy_with(rw2, rx2, st, pr / 2);       // copies 0 .. CPT-1
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    if (has1 && c == 0 && (pr & 1) == 0) {
+                        copy_with(rw1, rx1, st ^ 1, CPT + pr / 2);   // CPT .. 2*CPT-1
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
         }
     };
-    if (range >= 0) body(std::true_type{});
-    else body(std::false_type{});
+    auto zero = [&](f32x16(&acc)[4][4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = splat16(0.f);
+    };
+    // k steps [k0, k1) of tile cur on buffers st, st ^ 1, ... (the prologue or the previous
+    // run issued the first step and half of the second). chain: the stream goes on into steps
+    // 0, 1, ... of tile nxt, whose first copies and operands this run issues and reads.
+    using yes = std::true_type;
+    using rt = std::false_type;
+    auto run = [&](const TileSrc &cur, int k0, int k1, bool chain, const TileSrc &nxt, int &st,
+                   f32x16(&acc)[4][4]) __attribute__((always_inline)) {
+        auto res = [&](int s, u32x4 &rw, u32x4 &rx) __attribute__((always_inline)) {
+            const bool in = s < k1;
+            const TileSrc &t = in ? cur : nxt;
+            const int kb = (in ? s : s - k1) * BK * 2;
+            rw = rsrc_words(t.W0 + kb, t.wbytes);
+            rx = rsrc_words(t.X0 + kb, t.xbytes);
+        };
+        u32x4 rw1, rx1, rw2, rx2;
+        int s = k0;
+        for (; s + 2 < k1; ++s) {
+            res(s + 1, rw1, rx1);
+            res(s + 2, rw2, rx2);
+            step(yes{}, yes{}, true, true, st, acc, rw1, rx1, rw2, rx2);
+            st ^= 1;
+        }
+        if (s + 1 < k1) {              // step k1 - 2: the step after next is nxt's first
+            res(s + 1, rw1, rx1);
+            res(s + 2, rw2, rx2);
+            step(yes{}, rt{}, true, chain, st, acc, rw1, rx1, rw2, rx2);
+            st ^= 1;
+            ++s;
+        }
+        res(s + 1, rw1, rx1);          // step k1 - 1: next nxt's first, then its second
+        res(s + 2, rw2, rx2);
+        step(rt{}, rt{}, chain, chain, st, acc, rw1, rx1, rw2, rx2);
+        st ^= 1;
+    };
+
+    // ---- whole tiles: one stream of k steps over this workgroup's tiles ------------------
+    if (bid < p.n_full) {
+        f32x16 acc[4][4];              // [n block][m block]
+        zero(acc);
+        int i = bid;
+        TileSrc cur = tile_src(xcd_major(i, p.n_full));
+        prologue(cur, 0, nsteps > 1);
+        int st = 0;
+        for (;;) {
+            const bool more = i + G < p.n_full;
+            // With one k step a tile's run cannot issue the tile after next's first copies:
+            // such tiles restart from a prologue.
+            const bool chain = more && nsteps > 1;
+            const TileSrc nxt = more ? tile_src(xcd_major(i + G, p.n_full)) : cur;
+            run(cur, 0, nsteps, chain, nxt, st, acc);
+            store_rows<4>(p, acc, cur.m0 + wm * 128, cur.n0 + wn * 128, cur.tn, wn, wm * 128, LT);
+            if (!more) break;
+            zero(acc);
+            i += G;
+            cur = nxt;
+            if (!chain) {
+                __syncthreads();
+                prologue(cur, 0, false);
+                st = 0;
+            }
+        }
+    }
+
+    // ---- a tail range: k steps [k_begin, k_end) of a tail tile, its accumulators, in
+    // register order, for the fixup --------------------------------------------------------
+    const int n_ranges = (p.tiles_m * p.tiles_n - p.n_full) * p.splits;
+    if (p.splits > 1 && bid < n_ranges) {
+        const int range = xcd_major(bid, n_ranges);                // tile-major: (tile, split)
+        const TileSrc ts = tile_src(p.n_full + range / p.splits);
+        const int k_begin = (range % p.splits) * p.steps_per_split;
+        const int k_end = min(k_begin + p.steps_per_split, nsteps);
+        f32x16 acc[4][4];
+        zero(acc);
+        __syncthreads();               // the whole tiles' last reads of the LDS buffers are done
+        prologue(ts, k_begin, k_end - k_begin > 1);
+        int st = 0;
+        run(ts, k_begin, k_end, false, ts, st, acc);
+        f32x16 *dst = (f32x16 *)(p.part + (int64_t)range * (LT * LT)) + wave * 16 * 64 + lane;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) dst[(4 * nb + mb) * 64] = acc[nb][mb];
+    }
 }
 
 // Tail tiles: the sum of a tile's k ranges, then the epilogue. Eight workgroups per tile, one
@@ -363,8 +424,8 @@ int64_t linear_part_bytes(int64_t tail_tiles, int splits) {
 int launch_linear(const LinearParams &p, void *stream) {
     const int n_tail = p.tiles_m * p.tiles_n - p.n_full;
     const dim3 block(256);
-    hipLaunchKernelGGL((linear_kernel<64>), dim3((unsigned)(p.n_full + n_tail * p.splits)), block,
-                       0, (hipStream_t)stream, p);
+    if (p.grid < 1) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL((linear_kernel<64>), dim3((unsigned)p.grid), block, 0, (hipStream_t)stream, p);
     if (n_tail > 0 && p.splits > 1)
         hipLaunchKernelGGL(linear_fixup_kernel, dim3((unsigned)n_tail * 8), dim3(kFixupThreads),
                            0, (hipStream_t)stream, p);

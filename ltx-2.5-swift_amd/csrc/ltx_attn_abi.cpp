@@ -899,6 +899,11 @@ ltx_attn_status ltx_linear(const ltx_linear_args *a, void *stream) {
         p.splits = ls.splits;
         p.steps_per_split = ls.steps_per_split;
     }
+    // One workgroup per resident slot walks the whole tiles; the tail ranges were planned to
+    // fill the slots the last round leaves.
+    const int64_t n_ranges = (tiles_m * tiles_n - p.n_full) * (p.splits > 1 ? p.splits : 0);
+    p.grid = (int32_t)std::max<int64_t>(std::min<int64_t>(groups, p.n_full), n_ranges);
+    if (p.grid < 1) p.grid = 1;
     if (int e = ltx::launch_linear(p, stream))
         return fail(LTX_ATTN_EHIP, "linear launch: %s", hipGetErrorString((hipError_t)e));
     return LTX_ATTN_OK;

@@ -278,6 +278,33 @@ def test_tail_split_for_other_part_sizes(device, groups):
     check_partials(parts.cpu().numpy(), yb, f"groups {groups}")
 
 
+@pytest.mark.parametrize("K,groups", [(64, 3), (128, 8), (192, 3), (1024, 8)])
+def test_persistent_grid_walks_many_tiles(device, K, groups):
+    """A few resident groups leave each workgroup of the persistent grid many whole tiles
+    (1800 x 1000: 32 tiles on 3 or 8 workgroups). At K = 64 each tile restarts from its own
+    prologue; from K = 128 on, the next tile's first copies and operands are issued during the
+    current tile's last two k steps. A tile's sum order does not depend on the workgroup that
+    runs it, so y and the statistic equal the default grid's (one tile per workgroup) bit for
+    bit; the oracle on rows of the first and last row tiles."""
+    import torch
+
+    M, N = 1800, 1000
+    x = O.randn_bf16_bits((M, K), 1100 + K)
+    w = O.randn_bf16_bits((N, K), 1200 + K, std=K ** -0.5)
+    b = O.randn_bf16_bits((N,), 1300 + K, std=0.5)
+    xt, wt, bt = dev(x, device), dev(w, device), dev(b, device)
+    _say(f"linear {M}x{N}x{K} on {groups} workgroups")
+    y_few, p_few = L.linear(xt, wt, bt, sumsq=True, workspace=False, resident_groups=groups)
+    y_all, p_all = L.linear(xt, wt, bt, sumsq=True, workspace=False)
+    torch.cuda.synchronize()
+    yb = host_bits(y_few)
+    assert np.array_equal(yb, host_bits(y_all))
+    assert np.array_equal(p_few.cpu().numpy(), p_all.cpu().numpy())
+    rows = np.r_[0:64, M - 64:M]
+    check_linear(yb[rows], np.ascontiguousarray(x[rows]), w, b, f"K {K} on {groups} groups")
+    check_partials(p_few.cpu().numpy(), yb, f"K {K} on {groups} groups")
+
+
 def _random_linear_case(i):
     """Seeded draws of M (any), N (a multiple of 8), K (a multiple of 64), bias, statistic,
     the part size the tail split is planned for, and whether a workspace allows the split."""
