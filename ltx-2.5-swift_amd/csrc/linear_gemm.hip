@@ -12,21 +12,23 @@
 // the lane).
 //
 // Staging: every k step's 256 x BK tiles of x and w are copied HBM -> LDS by the
-// buffer-load-to-LDS path into one of two buffers, rows of BK elements with their 16-byte units
-// XOR-swizzled so the operand reads (32 rows, one unit per half-wave) are free of bank
-// conflicts. Rows past M (N) read as zeros through the buffer resource's bound. The step loop is
-// arranged around its one barrier, which sits in the last reduction chunk of each step, after
-// that chunk's operands have been read into registers and before its products:
-//   * the barrier certifies that every wave's copies for the next step have landed (each wave
+// buffer-load-to-LDS path, rows of BK elements with their 16-byte units XOR-swizzled so the
+// operand reads (32 rows, one unit per half-wave) are free of bank conflicts. Rows past M (N)
+// read as zeros through the buffer resource's bound. LDS holds three w tiles and two x tiles
+// (160 KiB): k step g reads w buffer g % 3 and x buffer g % 2. The step loop is arranged
+// around its one barrier, which sits in the last reduction chunk of each step, after that
+// chunk's operands have been read into registers and before its products:
+//   * the barrier certifies that every wave's copies for step g + 1 have landed (each wave
 //     waits for its own first: the copies are untracked assembly, counted by vmcnt) and that
-//     every wave has finished reading the current step's buffer;
-//   * right after it, the wave issues half of the copies for the step after next into the
-//     buffer just freed, one after every other product of the chunk, and reads the next
-//     step's first operands between the same products, so the matrix cores have the chunk's
-//     products to run while the reads return; the other half of the copies follows during the
-//     next step's first chunk. Half a step's copies
-//     per chunk keeps the texture address unit's queues from filling (all sixteen in one chunk
-//     stalled the wave's issue), and the later half still has 2.5 chunks to land.
+//     every wave has finished reading step g's buffers. Step g + 2's w tile, issued during
+//     step g's first chunk into the third w buffer, stays in flight across it: a copy-only
+//     run of this tile stream (30720 x 4096 x 4096) takes 0.53 ms when each step waits for
+//     all its copies and 0.38 ms with half a step's copies always outstanding;
+//   * right after it, the wave issues step g + 2's x tile into the x buffer just freed, one
+//     copy after every other product of the chunk, and reads step g + 1's first operands
+//     between the same products, so the matrix cores have the chunk's products to run while
+//     the reads return. Half a step's copies per chunk keeps the texture address unit's queues
+//     from filling (all sixteen in one chunk stalled the wave's issue).
 // Within a step, the operands of chunk c + 1 are read while the products of chunk c run, one
 // before every other product (all eight at the chunk's start left the LDS reads of the four
 // waves bunched: the fused 12480 x 12288 x 4096 projection 1.075 -> 1.049 ms).
@@ -56,7 +58,7 @@ struct LinTile {
     static constexpr int CPT = LT * U / 64 / 4;   // copies per wave per operand tile
     static constexpr int NCH = BK / 16;           // MFMA reduction chunks per k step
     static_assert(BK == 64, "k step: the copy schedule places CPT = 8 copies in each of two chunks");
-    static_assert(2 * 2 * ELEMS * 2 <= 160 * 1024, "LDS budget");
+    static_assert((3 + 2) * ELEMS * 2 <= 160 * 1024, "LDS budget: three w and two x buffers");
 };
 
 // Unit swizzle: the 16 lanes a 16-byte LDS read serves together read 16 consecutive rows at
@@ -80,15 +82,18 @@ __device__ __forceinline__ void tile_coords(const LinearParams &p, int t, int &t
 }
 
 // Epilogue of NMB 32-row blocks of a wave: round to bf16, add the bias, store, and the rows'
-// sums of squares. Lane (r, g) of product (nb, mb) holds y[m][n + e] for
+// sums of squares (the two column halves' sums meet in red, 2 x 256 floats of LDS). Lane
+// (r, g) of product (nb, mb) holds y[m][n + e] for
 // m = mrow + 32*mb + r, n = ncol + 32*nb + 8*qd + 4*g (qd = 0..3), e = 0..3 in accumulator
 // 4*qd + e; the wave covers columns [ncol, ncol + 128) of column tile tn, the workgroup's two
 // waves of one row range (wn = 0, 1) all 256. The workgroup's rows are the `rows` rows from
 // mrow - red_off, in which the wave's blocks start at red_off. Every thread calls it.
+typedef __attribute__((address_space(3))) float lds_float;
+
 template <int NMB>
 __device__ __forceinline__ void store_rows(const LinearParams &p, const f32x16 (&acc)[4][NMB],
                                            int mrow, int ncol, int tn, int wn, int red_off,
-                                           int rows) {
+                                           int rows, lds_float *red) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int r = lane & 31, g = lane >> 5;
@@ -101,7 +106,6 @@ __device__ __forceinline__ void store_rows(const LinearParams &p, const f32x16 (
             bias[nb][qd] = (p.bias && n < p.N) ? *(const u32x2 *)((const bf16 *)p.bias + n)
                                                : u32x2{0u, 0u};
         }
-    __shared__ float red[2][LT];
     float ss[NMB];
 #pragma unroll
     for (int mb = 0; mb < NMB; ++mb) {
@@ -136,11 +140,11 @@ __device__ __forceinline__ void store_rows(const LinearParams &p, const f32x16 (
     if (!p.sumsq) return;
     if (g == 0) {
 #pragma unroll
-        for (int mb = 0; mb < NMB; ++mb) red[wn][red_off + 32 * mb + r] = ss[mb];
+        for (int mb = 0; mb < NMB; ++mb) red[wn * LT + red_off + 32 * mb + r] = ss[mb];
     }
     __syncthreads();
     const int m = mrow - red_off + tid;
-    if (tid < rows && m < p.M) p.sumsq[(int64_t)m * p.ss_rs + tn] = red[0][tid] + red[1][tid];
+    if (tid < rows && m < p.M) p.sumsq[(int64_t)m * p.ss_rs + tn] = red[tid] + red[LT + tid];
 }
 
 template <int BK>
@@ -148,7 +152,10 @@ __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_pe
 void linear_kernel(const LinearParams p) {
     using T = LinTile<BK>;
     constexpr int U = T::U, CPT = T::CPT, NCH = T::NCH, ELEMS = T::ELEMS;
-    __shared__ __attribute__((aligned(16))) bf16 sW[2 * ELEMS];
+    // Three buffers of w tiles and two of x tiles (160 KiB): k step g of a run reads w buffer
+    // g % 3 and x buffer g % 2, so half of step g + 2's copies (its w tile) can be in flight
+    // before step g's barrier frees anything.
+    __shared__ __attribute__((aligned(16))) bf16 sW[3 * ELEMS];
     __shared__ __attribute__((aligned(16))) bf16 sX[2 * ELEMS];
 
     const int tid = threadIdx.x;
@@ -181,16 +188,12 @@ void linear_kernel(const LinearParams p) {
         xl[j] = row * xrow + 16 * u;
         wl[j] = row * wrow + 16 * u;
     }
-    // Copy j (0 .. 2*CPT-1) of this wave's share of a k step into buffer st: even j of w, odd
-    // of x.
-    auto copy_with = [&](const u32x4 &rw, const u32x4 &rx, int st, int j) __attribute__((always_inline)) {
-        if ((j & 1) == 0) {
-            copy_all(rw, (uint32_t)(uintptr_t)((lds_bf16 *)sW + st * ELEMS + (wave * CPT + j / 2) * 512),
-                     wl[j / 2]);
-        } else {
-            copy_all(rx, (uint32_t)(uintptr_t)((lds_bf16 *)sX + st * ELEMS + (wave * CPT + j / 2) * 512),
-                     xl[j / 2]);
-        }
+    // Copy j (0 .. CPT-1) of this wave's share of a w (x) tile into w (x) buffer bf.
+    auto copy_w = [&](const u32x4 &rw, int bf, int j) __attribute__((always_inline)) {
+        copy_all(rw, (uint32_t)(uintptr_t)((lds_bf16 *)sW + bf * ELEMS + (wave * CPT + j) * 512), wl[j]);
+    };
+    auto copy_x = [&](const u32x4 &rx, int bf, int j) __attribute__((always_inline)) {
+        copy_all(rx, (uint32_t)(uintptr_t)((lds_bf16 *)sX + bf * ELEMS + (wave * CPT + j) * 512), xl[j]);
     };
     // A tile's operand rows: x rows m0.., w rows n0.. (rows past M, N read as zeros through the
     // resources' bounds).
@@ -218,45 +221,50 @@ void linear_kernel(const LinearParams p) {
         return *(const __attribute__((address_space(3))) bf16x8 *)(S + row * BK + 8 * lswz<U>(row, 2 * c + g));
     };
     bf16x8 a[2][4], b[2][4];           // operands of the current and the next chunk
-    auto read_chunk = [&](int st, int c, int buf) __attribute__((always_inline)) {
-        const lds_bf16 *Ws = (const lds_bf16 *)sW + st * ELEMS;
-        const lds_bf16 *Xs = (const lds_bf16 *)sX + st * ELEMS;
+    auto read_chunk = [&](int ws, int xs, int c, int buf) __attribute__((always_inline)) {
+        const lds_bf16 *Ws = (const lds_bf16 *)sW + ws * ELEMS;
+        const lds_bf16 *Xs = (const lds_bf16 *)sX + xs * ELEMS;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             a[buf][i] = frag(Ws, wn * 128 + 32 * i, c);
             b[buf][i] = frag(Xs, wm * 128 + 32 * i, c);
         }
     };
-    // Prologue of a run of k steps: its first step, and the first half of its second (each
-    // step issues the rest for its successor), then the first operands.
+    // Prologue of a run of k steps: its first two steps' tiles into buffers 0 and 1, then the
+    // first operands.
     auto prologue = [&](const TileSrc &ts, int k0, bool two) __attribute__((always_inline)) {
         const int kb = k0 * BK * 2;
 #pragma unroll
-        for (int j = 0; j < 2 * CPT; ++j)
-            copy_with(rsrc_words(ts.W0 + kb, ts.wbytes), rsrc_words(ts.X0 + kb, ts.xbytes), 0, j);
+        for (int j = 0; j < CPT; ++j) {
+            copy_w(rsrc_words(ts.W0 + kb, ts.wbytes), 0, j);
+            copy_x(rsrc_words(ts.X0 + kb, ts.xbytes), 0, j);
+        }
         if (two) {
 #pragma unroll
-            for (int j = 0; j < CPT; ++j)
-                copy_with(rsrc_words(ts.W0 + kb + BK * 2, ts.wbytes),
-                          rsrc_words(ts.X0 + kb + BK * 2, ts.xbytes), 1, j);
-            wait_copies_but<CPT>();
+            for (int j = 0; j < CPT; ++j) {
+                copy_w(rsrc_words(ts.W0 + kb + BK * 2, ts.wbytes), 1, j);
+                copy_x(rsrc_words(ts.X0 + kb + BK * 2, ts.xbytes), 1, j);
+            }
+            wait_copies_but<2 * CPT>();
         } else {
             wait_copies();
         }
         __syncthreads();
-        read_chunk(0, 0, 0);
+        read_chunk(0, 0, 0, 0);
     };
 
-    // One k step on LDS buffer st. has1: there is a next step (in this tile or the next); its
-    // copies' second half (resources rw1, rx1) are issued in the first chunk and its first
-    // operands read in the last. has2: there is a step after it, whose copies' first half
-    // (rw2, rx2) go into the buffer this step frees, in the last chunk (half a step's copies
-    // per chunk keeps the address unit's queue from filling). A1, A2: has1, has2 hold whatever
-    // the run-time flags say (the inner steps of a run, without branches).
-    auto step = [&](auto A1, auto A2, bool h1, bool h2, int st, f32x16(&acc)[4][4],
-                    const u32x4 &rw1, const u32x4 &rx1, const u32x4 &rw2, const u32x4 &rx2)
-        __attribute__((always_inline)) {
+    // One k step g on w buffer ws, x buffer xs. has1: there is a step g + 1 (in this tile or
+    // the next), whose first operands are read in the last chunk. has2: there is a step g + 2:
+    // its w tile (resource rw2) is copied during the first chunk into w buffer (g + 2) % 3,
+    // free since step g - 1's barrier, and its x tile (rx2) during the last chunk into x buffer
+    // xs, which this step's barrier frees (a step's copies over two chunks keeps the address
+    // unit's queue from filling). The barrier waits for step g + 1's tiles only: step g + 2's
+    // w tile, the wave's CPT most recent copies, stays in flight. A1, A2: has1, has2 hold
+    // whatever the run-time flags say (the inner steps of a run, without branches).
+    auto step = [&](auto A1, auto A2, bool h1, bool h2, int ws, int xs, f32x16(&acc)[4][4],
+                    const u32x4 &rw2, const u32x4 &rx2) __attribute__((always_inline)) {
         const bool has1 = decltype(A1)::value || h1, has2 = decltype(A2)::value || h2;
+        const int ws1 = ws == 2 ? 0 : ws + 1, ws2 = ws == 0 ? 2 : ws - 1;
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
             const int cb = c & 1;          // NCH is even: chunk 0 of every step is in buffer 0
@@ -264,13 +272,15 @@ void linear_kernel(const LinearParams p) {
             // first -- are read one before every other product of this chunk (all eight at the
             // chunk's start left the LDS reads of the four waves bunched).
             const bool rd = c < NCH - 1 || has1;
-            const int rst = c < NCH - 1 ? st : st ^ 1, rc = c < NCH - 1 ? c + 1 : 0;
+            const int rws = c < NCH - 1 ? ws : ws1, rxs = c < NCH - 1 ? xs : xs ^ 1;
+            const int rc = c < NCH - 1 ? c + 1 : 0;
             if (c == NCH - 1) {
-                // The next step's copies (issued one step ago) have landed for this wave; after
-                // the barrier they have for every wave, and every wave's reads of buffer st are
-                // done. The scheduling fences keep the earlier chunks' products ahead of the wait.
+                // Step g + 1's tiles have landed for this wave; after the barrier they have for
+                // every wave, and every wave's reads of this step's buffers are done. The
+                // scheduling fences keep the earlier chunks' products ahead of the wait.
                 __builtin_amdgcn_sched_barrier(0);
-                wait_copies();
+                if (has2) wait_copies_but<CPT>();
+                else wait_copies();
                 __syncthreads();
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -282,19 +292,19 @@ void linear_kernel(const LinearParams p) {
                     if (rd && (pr & 1) == 0) {
                         // operand pr / 2 of the next chunk: a[0], b[0], a[1], b[1], ...
                         const int j = pr >> 1;
-                        const lds_bf16 *Ws = (const lds_bf16 *)sW + rst * ELEMS;
-                        const lds_bf16 *Xs = (const lds_bf16 *)sX + rst * ELEMS;
+                        const lds_bf16 *Ws = (const lds_bf16 *)sW + rws * ELEMS;
+                        const lds_bf16 *Xs = (const lds_bf16 *)sX + rxs * ELEMS;
                         if ((j & 1) == 0) a[cb ^ 1][j >> 1] = frag(Ws, wn * 128 + 32 * (j >> 1), rc);
                         else b[cb ^ 1][j >> 1] = frag(Xs, wm * 128 + 32 * (j >> 1), rc);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                     acc[nb][mb] = mfma32(a[cb][nb], b[cb][mb], acc[nb][mb]);
-                    if (has2 && c == NCH - 1 && (pr & 1) == 0) {
-                        copy_with(rw2, rx2, st, pr / 2);       // copies 0 .. CPT-1
+                    if (has2 && c == 0 && (pr & 1) == 0) {
+                        copy_w(rw2, ws2, pr / 2);
                         __builtin_amdgcn_sched_barrier(0);
                     }
-                    if (has1 && c == 0 && (pr & 1) == 0) {
-                        copy_with(rw1, rx1, st ^ 1, CPT + pr / 2);   // CPT .. 2*CPT-1
+                    if (has2 && c == NCH - 1 && (pr & 1) == 0) {
+                        copy_x(rx2, xs, pr / 2);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
@@ -306,13 +316,14 @@ void linear_kernel(const LinearParams p) {
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb) acc[nb][mb] = splat16(0.f);
     };
-    // k steps [k0, k1) of tile cur on buffers st, st ^ 1, ... (the prologue or the previous
-    // run issued the first step and half of the second). chain: the stream goes on into steps
-    // 0, 1, ... of tile nxt, whose first copies and operands this run issues and reads.
+    // k steps [k0, k1) of tile cur (the prologue or the previous run issued the first two
+    // steps' tiles). chain: the stream goes on into steps 0, 1, ... of tile nxt, whose first
+    // tiles and operands this run issues and reads. ws, xs: the buffers of the run's first
+    // step, on return those of the step after its last.
     using yes = std::true_type;
     using rt = std::false_type;
-    auto run = [&](const TileSrc &cur, int k0, int k1, bool chain, const TileSrc &nxt, int &st,
-                   f32x16(&acc)[4][4]) __attribute__((always_inline)) {
+    auto run = [&](const TileSrc &cur, int k0, int k1, bool chain, const TileSrc &nxt, int &ws,
+                   int &xs, f32x16(&acc)[4][4]) __attribute__((always_inline)) {
         auto res = [&](int s, u32x4 &rw, u32x4 &rx) __attribute__((always_inline)) {
             const bool in = s < k1;
             const TileSrc &t = in ? cur : nxt;
@@ -320,25 +331,26 @@ void linear_kernel(const LinearParams p) {
             rw = rsrc_words(t.W0 + kb, t.wbytes);
             rx = rsrc_words(t.X0 + kb, t.xbytes);
         };
-        u32x4 rw1, rx1, rw2, rx2;
+        auto advance = [&]() __attribute__((always_inline)) {
+            ws = ws == 2 ? 0 : ws + 1;
+            xs ^= 1;
+        };
+        u32x4 rw2, rx2;
         int s = k0;
         for (; s + 2 < k1; ++s) {
-            res(s + 1, rw1, rx1);
             res(s + 2, rw2, rx2);
-            step(yes{}, yes{}, true, true, st, acc, rw1, rx1, rw2, rx2);
-            st ^= 1;
+            step(yes{}, yes{}, true, true, ws, xs, acc, rw2, rx2);
+            advance();
         }
         if (s + 1 < k1) {              // step k1 - 2: the step after next is nxt's first
-            res(s + 1, rw1, rx1);
             res(s + 2, rw2, rx2);
-            step(yes{}, rt{}, true, chain, st, acc, rw1, rx1, rw2, rx2);
-            st ^= 1;
+            step(yes{}, rt{}, true, chain, ws, xs, acc, rw2, rx2);
+            advance();
             ++s;
         }
-        res(s + 1, rw1, rx1);          // step k1 - 1: next nxt's first, then its second
-        res(s + 2, rw2, rx2);
-        step(rt{}, rt{}, chain, chain, st, acc, rw1, rx1, rw2, rx2);
-        st ^= 1;
+        res(s + 2, rw2, rx2);          // step k1 - 1: next nxt's first, then its second
+        step(rt{}, rt{}, chain, chain, ws, xs, acc, rw2, rx2);
+        advance();
     };
 
     // ---- whole tiles: one stream of k steps over this workgroup's tiles ------------------
@@ -348,15 +360,19 @@ void linear_kernel(const LinearParams p) {
         int i = bid;
         TileSrc cur = tile_src(xcd_major(i, p.n_full));
         prologue(cur, 0, nsteps > 1);
-        int st = 0;
+        int ws = 0, xs = 0;
         for (;;) {
             const bool more = i + G < p.n_full;
             // With one k step a tile's run cannot issue the tile after next's first copies:
             // such tiles restart from a prologue.
             const bool chain = more && nsteps > 1;
             const TileSrc nxt = more ? tile_src(xcd_major(i + G, p.n_full)) : cur;
-            run(cur, 0, nsteps, chain, nxt, st, acc);
-            store_rows<4>(p, acc, cur.m0 + wm * 128, cur.n0 + wn * 128, cur.tn, wn, wm * 128, LT);
+            run(cur, 0, nsteps, chain, nxt, ws, xs, acc);
+            // The tile's last w buffer is free until the next tile's second step copies into
+            // it: the epilogue's row sums meet there.
+            const int red_ws = ws == 0 ? 2 : ws - 1;
+            store_rows<4>(p, acc, cur.m0 + wm * 128, cur.n0 + wn * 128, cur.tn, wn, wm * 128, LT,
+                          (lds_float *)((lds_bf16 *)sW + red_ws * ELEMS));
             if (!more) break;
             zero(acc);
             i += G;
@@ -364,7 +380,9 @@ void linear_kernel(const LinearParams p) {
             if (!chain) {
                 __syncthreads();
                 prologue(cur, 0, false);
-                st = 0;
+                ws = xs = 0;
+            } else if (p.sumsq) {
+                __syncthreads();       // every wave's reads of the row sums are done
             }
         }
     }
@@ -381,8 +399,8 @@ void linear_kernel(const LinearParams p) {
         zero(acc);
         __syncthreads();               // the whole tiles' last reads of the LDS buffers are done
         prologue(ts, k_begin, k_end - k_begin > 1);
-        int st = 0;
-        run(ts, k_begin, k_end, false, ts, st, acc);
+        int ws = 0, xs = 0;
+        run(ts, k_begin, k_end, false, ts, ws, xs, acc);
         f32x16 *dst = (f32x16 *)(p.part + (int64_t)range * (LT * LT)) + wave * 16 * 64 + lane;
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb)
@@ -412,7 +430,9 @@ void linear_fixup_kernel(const LinearParams p) {
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) acc[nb][0] += src[nb * 4 * 64];
     }
-    store_rows<1>(p, acc, tm * LT + wm * 128 + 32 * mb, tn * LT + wn * 128, tn, wn, 0, 32);
+    __shared__ float red[2 * LT];
+    store_rows<1>(p, acc, tm * LT + wm * 128 + 32 * mb, tn * LT + wn * 128, tn, wn, 0, 32,
+                  (lds_float *)red);
 }
 
 }  // namespace
