@@ -14,6 +14,8 @@ Bar for the statistic: each fp32 partial equals the float64 sum of squares of th
 bf16 outputs over its 256 columns to fp32 summation accuracy (relative 2e-5 >= 258 u).
 """
 
+import os
+
 import numpy as np
 import pytest
 
@@ -319,7 +321,8 @@ def _random_linear_case(i):
                 seed=int(rng.integers(1, 1 << 30)))
 
 
-@pytest.mark.parametrize("i", range(12))
+# 12 cases by default; LTX_LINEAR_RANDOM_CASES=n runs the first n seeds of the same sequence.
+@pytest.mark.parametrize("i", range(int(os.environ.get("LTX_LINEAR_RANDOM_CASES", "12"))))
 def test_linear_random_shapes(device, i):
     import torch
 
