@@ -432,13 +432,21 @@ void gemma_attn_kernel(const GemmaAttnParams p) {
             f16x8 va0[NDW];
 #pragma unroll
             for (int db = 0; db < NDW; ++db) va0[db] = v_opnd(0, db);
-            // mask: key k = 32 kb + 8 (i >> 2) + 4 g + (i & 3) for query q
+            // mask: key k = 32 kb + 8 (i >> 2) + 4 g + (i & 3) for query q. A block inside
+            // every row's allowed range of the wave (most blocks of a causal or windowed range)
+            // needs none: its five instructions per weight were a tenth of the block's
+            // (1024 tokens, D 256: 33.1 -> 30.8 us)
             float mx = -INFINITY;
+            if (__builtin_amdgcn_ballot_w64(k_lo > 32 * kb || 32 * kb + 31 > k_hi) == 0) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int k = 32 * kb + 8 * (e >> 2) + 4 * g + (e & 3);
-                s[e] = ((k >= k_lo) & (k <= k_hi)) ? s[e] : -INFINITY;
-                mx = fmaxf(mx, s[e]);
+                for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[e]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int k = 32 * kb + 8 * (e >> 2) + 4 * g + (e & 3);
+                    s[e] = ((k >= k_lo) & (k <= k_hi)) ? s[e] : -INFINITY;
+                    mx = fmaxf(mx, s[e]);
+                }
             }
             mx = fmaxf(mx, xlane32(mx));
             if constexpr (SAFE) {
