@@ -732,8 +732,8 @@ def main():
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
-        print("bench.py measures one MI355X: the attention path runs on a single GPU in this "
-              "build (multi-GPU head/query sharding is described in DESIGN.md, not built); "
+        print("bench.py measures one MI355X: the attention path runs on a single GPU "
+              "(head/query sharding over several GPUs is designed, not built); "
               f"--gpus {args.gpus} is not supported.", file=sys.stderr)
         sys.exit(2)
 

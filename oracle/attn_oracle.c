@@ -1,7 +1,7 @@
 /*
  * attn_oracle.c -- CPU restatement of the LTX 2.5 DiT attention path, in C.
  *
- * TEST INFRASTRUCTURE ONLY: loaded by tests/ (as the checker) and by bench.py's cpu_baseline
+ * TEST INFRASTRUCTURE ONLY: loaded by tests/ (the parity reference) and by bench.py's cpu_baseline
  * leg (as the timed CPU baseline). The shipped library never links or calls it.
  *
  * It restates the reference's `.explicit` attention arithmetic with its rounding points:

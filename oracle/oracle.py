@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY. Nothing in the shipped library imports, links or calls this
 module; only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
-use it, and only as the checker. The product path is the HIP library in
+use it, and only as the parity reference. The product path is the HIP library in
 ``ltx-2.5-swift_amd/``.
 
 This is a numpy restatement of the reference's arithmetic:
