@@ -232,7 +232,8 @@ typedef struct ltx_linear_args {
 int32_t ltx_linear_sumsq_blocks(int32_t N);
 
 /* Bytes of workspace that let ltx_linear split its tail: the 256 x 256 tiles past the last
- * whole round of 256 (one per CU) are cut along K into as many ranges as fill the CUs, and a
+ * whole round of 256 (one per CU) are cut along K into ranges (at most as many as fill the
+ * CUs; the count weighs a range's k steps against its partials' round trip), and a
  * fixup launch sums each tile's ranges (256 KiB of fp32 per range; 0 when the tiles fill
  * whole rounds or the tail is more than half a round). Pure host function; 0 for invalid
  * arguments. Sized for a whole gfx950 part (256 CUs): on a device with another CU count

@@ -38,8 +38,9 @@
 //
 // Tail split: one workgroup runs per CU, so a tile count just past a multiple of 256 costs a
 // whole extra round (12480 x 4096: 784 tiles = 3 rounds + 16 tiles). The host cuts the tiles
-// past the last whole round into k ranges, as many per tile as fill the CUs (16 tiles -> 16
-// ranges of 4 k steps each); a range stores its fp32 accumulators, in register order, to the
+// past the last whole round into k ranges, at most as many as fill the CUs, the count weighing
+// a range's k steps against its partials' round trip (16 tiles -> 8 ranges of 8 k steps
+// each); a range stores its fp32 accumulators, in register order, to the
 // workspace, and linear_fixup_kernel sums a tile's ranges in order and runs the same epilogue
 // (eight workgroups per tile).
 #include <type_traits>

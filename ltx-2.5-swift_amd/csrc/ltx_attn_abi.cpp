@@ -781,7 +781,11 @@ namespace {
 
 // Tail split of a projection: the tiles past the last whole round of `groups` resident
 // workgroups, when they fill at most half a round, are cut into k ranges of at least two
-// 64-wide steps, as many per tile as keep every CU busy. Pure host arithmetic.
+// 64-wide steps, at most as many as fill one round. The count minimises the tail's time: a
+// range's k steps (about 1.3 us each) against its fp32 partials (256 KiB per range and tile,
+// written and read back by the fixup, about 0.116 us at 4.5 TB/s). Measured at 12480 x 4096 x
+// 4096 (16 tail tiles): 8 ranges 0.373 ms, 16 ranges (every CU busy) 0.382 ms. Pure host
+// arithmetic.
 struct LinearSplit {
     int64_t tiles = 0, n_full = 0;
     int32_t splits = 1, steps_per_split = 0;
@@ -798,9 +802,20 @@ LinearSplit linear_split(int64_t M, int64_t N, int64_t K,
     ls.steps_per_split = (int32_t)nsteps;
     const int64_t rem = T % groups;
     if (T == 0 || rem == 0 || 2 * rem > groups || nsteps < 4) return ls;
-    int64_t s = std::min<int64_t>(groups / rem, nsteps / 2);
-    const int64_t per = (nsteps + s - 1) / s;
-    s = (nsteps + per - 1) / per;          // no empty range
+    const int64_t s_max = std::min<int64_t>(groups / rem, nsteps / 2);
+    constexpr double kStepUs = 1.3, kPartUs = 0.116;
+    int64_t s = 1, per = nsteps;
+    double best = 0.0;
+    for (int64_t c = 2; c <= s_max; ++c) {
+        const int64_t cp = (nsteps + c - 1) / c;
+        const int64_t cs = (nsteps + cp - 1) / cp;   // no empty range
+        const double t = (double)cp * kStepUs + (double)(rem * cs) * kPartUs;
+        if (s == 1 || t < best - 1e-9) {
+            best = t;
+            s = cs;
+            per = cp;
+        }
+    }
     if (s < 2) return ls;
     ls.n_full = T - rem;
     ls.splits = (int32_t)s;

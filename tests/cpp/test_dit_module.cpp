@@ -1,6 +1,7 @@
 // Host-side behaviour of the C++ module driver (no GPU needed): weight-shape checks, the
 // workspace layout (projections, statistic partials, gate logits, merged output and the
 // attention call's own workspace) and failures thrown before anything is launched.
+#include <algorithm>
 #include <cstdio>
 #include <cstdint>
 #include <string>
@@ -55,11 +56,16 @@ int main() {
                         up(2ull * T * 4096);
     EXPECT(need > proj, "workspace holds the projections and the attention's own");
     const size_t need_p = m.workspaceBytes(B, x, nullptr, V::videoSelf, &pe, nullptr, nullptr, true);
-    // the projections' split-tail scratch: to_v / to_out at 12480 x 4096 x 4096 is the largest
+    // the projections' split-tail scratch, the larger of to_v / to_out (12480 x 4096 x 4096:
+    // 16 tail tiles in 8 k ranges) and to_gate_logits (12480 x 32 x 4096: 49 tiles in 4)
     ltx_linear_args la{};
     la.M = T; la.N = 4096; la.K = 4096;
-    const size_t scratch = ltx_linear_workspace_bytes(&la);
-    EXPECT(scratch == 16ull * 16 * 256 * 256 * 4, "linear scratch: 16 tail tiles x 16 k ranges");
+    const size_t scratch_v = ltx_linear_workspace_bytes(&la);
+    EXPECT(scratch_v == 16ull * 8 * 256 * 256 * 4, "linear scratch: 16 tail tiles x 8 k ranges");
+    la.N = 32;
+    const size_t scratch_g = ltx_linear_workspace_bytes(&la);
+    EXPECT(scratch_g == 49ull * 4 * 256 * 256 * 4, "gate logits scratch: 49 tiles x 4 k ranges");
+    const size_t scratch = std::max(scratch_v, scratch_g);
     EXPECT(need_p == up(2ull * T * 4096) + up(2ull * T * 32) + up(2ull * T * 4096) + up(scratch),
            "perturbed: v, gate logits, the merged output and the projections' scratch only");
 

@@ -318,10 +318,10 @@ def test_linear_statistic_layout():
 
 
 @pytest.mark.parametrize("M,N,K,tail_tiles,ranges", [
-    (12480, 4096, 4096, 16, 16),   # 784 tiles: 3 rounds + 16 tiles, 16 ranges of 4 steps
-    (12480, 12288, 4096, 48, 5),   # fused q/k/v: 2352 = 9 rounds + 48 tiles, 5 ranges of 13
-    (12480, 32, 4096, 49, 5),      # gate logits: 49 tiles in one round
-    (1000, 4096, 2048, 64, 4),     # 64 tiles, 4 ranges of 8 steps
+    (12480, 4096, 4096, 16, 8),    # 784 tiles: 3 rounds + 16 tiles, 8 ranges of 8 steps
+    (12480, 12288, 4096, 48, 4),   # fused q/k/v: 2352 = 9 rounds + 48 tiles, 4 ranges of 16
+    (12480, 32, 4096, 49, 4),      # gate logits: 49 tiles in one round
+    (1000, 4096, 2048, 64, 2),     # 64 tiles, 2 ranges of 16 steps
     (77, 32, 4096, 1, 32),         # one tile: 32 ranges of 2 steps
     (3120, 4096, 4096, 0, 0),      # 208 tiles: a tail of more than half a round runs whole
     (4096, 4096, 4096, 0, 0),      # 256 tiles: one whole round
@@ -329,7 +329,9 @@ def test_linear_statistic_layout():
 ])
 def test_linear_tail_split_workspace(M, N, K, tail_tiles, ranges):
     """ltx_linear_workspace_bytes: 256 KiB of fp32 partials per k range of each tile past the
-    last whole round of 256; a host-only query."""
+    last whole round of 256, the range count minimising ceil(steps / ranges) x 1.3 us plus
+    tiles x ranges x 0.116 us (a range's k steps against its partials' round trip); a
+    host-only query."""
     assert L.linear_workspace_bytes(M, N, K) == tail_tiles * ranges * 256 * 256 * 4
     lib = L.load_library()
     bad = _linear_args(K=96)

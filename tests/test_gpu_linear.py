@@ -119,7 +119,7 @@ def test_fused_projection_equals_separate_ones(device):
     """With every tile whole (no tail split), one GEMM over [to_q; to_k; to_v] weights writes
     the same bits, and the same statistic partials for the q and k column ranges (which start
     at multiples of 256), as three separate projections: each 256 x 256 tile depends only on
-    its own rows of x and w. With the tail split (36 and 12 tiles: 7 and 16 k ranges) the
+    its own rows of x and w. With the tail split (36 and 12 tiles: 3 and 4 k ranges) the
     summation order differs, so the two agree within the fp32 bound of check_linear."""
     import torch
 
@@ -216,8 +216,8 @@ def test_attention_takes_the_projection_statistic(device, Lq, Lk):
 
 
 @pytest.mark.parametrize("M,N,K", [
-    (12480, 4096, 4096),    # to_q at 12480 tokens: 784 tiles = 3 rounds + 16 tiles in 16 ranges
-    (12480, 32, 4096),      # to_gate_logits: 49 tiles in 5 ranges each
+    (12480, 4096, 4096),    # to_q at 12480 tokens: 784 tiles = 3 rounds + 16 tiles in 8 ranges
+    (12480, 32, 4096),      # to_gate_logits: 49 tiles in 4 ranges each
 ])
 def test_tail_split_matches_whole_tiles(device, M, N, K):
     """The tiles past the last whole round of 256, cut along K into ranges whose fp32 partials
@@ -258,8 +258,8 @@ def test_tail_split_matches_whole_tiles(device, M, N, K):
 def test_tail_split_for_other_part_sizes(device, groups):
     """ltx_linear splits its tail for the device's CU count (the resident_groups argument
     stands in for it) when the workspace sized for 256 CUs covers that split: 3000 x 1024 x 512 is 48
-    tiles; 32 groups split the 16 past one round two ways, 100 split all 48 two ways (the sized
-    split: four ways). The oracle on the rows of a whole tile and of a split one, and the
+    tiles; 32 groups split the 16 past one round two ways, 100 split all 48 two ways (as the
+    split sized for 256 does). The oracle on the rows of a whole tile and of a split one, and the
     statistic partials of every row."""
     import torch
 
